@@ -1,0 +1,335 @@
+"""Benchmark of the gfx950 quantized-linear hot path; prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps 512] [--warmup 64] [--only NAME] [--no-extra] [--no-cpu]
+
+Headline: INT4 g128 decode GEMV, M = 1, K = N = 4096,
+bf16 activations, fp16 group scales, bf16 output. A step is one launch over one
+batch; consecutive steps read distinct copies of the packed weights (>= 1 GiB of
+copies in total), so the 256 MB Infinity Cache cannot serve them and the data
+really streams from HBM. The W warmup steps and the K timed steps are each one
+HIP graph of back-to-back launches, replayed on the launching stream between
+HIP events; value = algorithmic bytes x K / elapsed.
+
+The other BASELINE configs (INT4 M = 4 / 16, the INT8 GEMV target, INT8 prefill,
+FP8 e4m3 GEMM, INT4 MoE grouped GEMM) are reported under "extra" with the same
+protocol. cpu_baseline times the reference's CPU algorithm (the numpy
+restatement in oracle/: dequantize, then fp32 matmul) on the host for a bounded
+sample of the headline workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT / "mini-llm-stack_amd"), str(ROOT)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "INT4/INT8/FP8 GEMM: HBM TB/s at M=1, TFLOP/s at M=2048 (% of roofline)"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP8_PEAK_TFLOPS = 5000.0
+ROTATE_BYTES = 1 << 30
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ----------------------------------------------------------------------------- timing
+
+
+def time_steps(fns, warmup: int, steps: int) -> float:
+    """ms per step: `warmup` then `steps` launches, fns[i % len(fns)] for step i,
+    each batch captured as one HIP graph and replayed between events."""
+    import torch
+    for f in fns:  # first calls: library load, LDS attributes, output pools
+        f()
+    torch.cuda.synchronize()
+
+    def capture(n):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                fns[i % len(fns)]()
+        return g
+
+    gw = capture(warmup) if warmup > 0 else None
+    gt = capture(steps)
+    torch.cuda.synchronize()
+    if gw is not None:
+        gw.replay()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    gt.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+# ----------------------------------------------------------------------------- workloads
+
+
+def int4_gemv(dev, M: int, steps: int, warmup: int, N: int = 4096, K: int = 4096, gs: int = 128):
+    import torch
+    from kernels.dequant_matmul import int4_matmul
+    from serve.quantize import quantize_int4
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    p, s = quantize_int4(torch.randn(N, K, generator=g, device=dev) * 0.02, gs)
+    s = s.to(torch.float16)
+    wbytes = p.numel() + s.numel() * 2
+    copies = max(2, -(-ROTATE_BYTES // wbytes))
+    ps = [p] + [p.clone() for _ in range(copies - 1)]
+    ss = [s] + [s.clone() for _ in range(copies - 1)]
+    fns = [lambda i=i: int4_matmul(x, ps[i], ss[i], gs) for i in range(copies)]
+    ms = time_steps(fns, warmup, steps)
+    nbytes = wbytes + M * K * 2 + M * N * 2
+    return dict(ms=ms, bytes=nbytes, flops=2 * M * N * K, copies=copies)
+
+
+def int8_gemv(dev, M: int, steps: int, warmup: int, N: int = 4096, K: int = 4096):
+    import torch
+    from kernels.dequant_matmul import int8_matmul
+    from serve.quantize import quantize_int8
+    g = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    q, s = quantize_int8(torch.randn(N, K, generator=g, device=dev) * 0.02)
+    s = s.to(torch.float16)
+    wbytes = q.numel() + s.numel() * 2
+    copies = max(2, -(-ROTATE_BYTES // wbytes))
+    qs = [q] + [q.clone() for _ in range(copies - 1)]
+    fns = [lambda i=i: int8_matmul(x, qs[i], s) for i in range(copies)]
+    ms = time_steps(fns, warmup, steps)
+    return dict(ms=ms, bytes=wbytes + M * K * 2 + M * N * 2, flops=2 * M * N * K, copies=copies)
+
+
+def int8_prefill(dev, steps: int, warmup: int, M=2048, N=11008, K=4096):
+    import torch
+    from kernels.dequant_matmul import int8_matmul
+    from serve.quantize import quantize_int8
+    g = torch.Generator(device=dev).manual_seed(2)
+    q, s = quantize_int8(torch.randn(N, K, generator=g, device=dev) * 0.02)
+    s = s.to(torch.float16)
+    copies = 6
+    xs = [torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+    qs = [q] + [q.clone() for _ in range(copies - 1)]
+    fns = [lambda i=i: int8_matmul(xs[i], qs[i], s) for i in range(copies)]
+    ms = time_steps(fns, warmup, steps)
+    nbytes = N * K + N * 2 + M * K * 2 + M * N * 2
+    return dict(ms=ms, bytes=nbytes, flops=2 * M * N * K, copies=copies)
+
+
+def fp8_gemm(dev, steps: int, warmup: int, M=4096, N=8192, K=8192):
+    import torch
+    from kernels.fp8_matmul import E4M3_MAX, fp8_matmul, quantize_e4m3
+    g = torch.Generator(device=dev).manual_seed(3)
+    copies = 4
+    ops = []
+    for _ in range(copies):
+        a = torch.randn(M, K, generator=g, device=dev)
+        a = torch.where(torch.rand(M, K, generator=g, device=dev) < 0.01, a * 20, a)
+        b = torch.randn(N, K, generator=g, device=dev)
+        b = torch.where(torch.rand(N, K, generator=g, device=dev) < 0.01, b * 20, b)
+        sa, sb = a.abs().amax(1) / E4M3_MAX, b.abs().amax(1) / E4M3_MAX
+        ops.append((quantize_e4m3(a, sa[:, None]), quantize_e4m3(b, sb[:, None]), sa, sb))
+        del a, b
+    fns = [lambda o=o: fp8_matmul(o[0], o[1], o[2], o[3], out_dtype=torch.bfloat16) for o in ops]
+    ms = time_steps(fns, warmup, steps)
+    nbytes = M * K + N * K + 4 * (M + N) + M * N * 2
+    return dict(ms=ms, bytes=nbytes, flops=2 * M * N * K, copies=copies)
+
+
+def moe_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=128):
+    import torch
+    from kernels.moe_grouped import int4_grouped_matmul
+    from kernels.moe_routing import gather_rows, route_topk, sort_by_expert
+    from serve.quantize import quantize_int4
+    g = torch.Generator(device=dev).manual_seed(4)
+    x = torch.randn(T, D, generator=g, device=dev).to(torch.bfloat16)
+    _, ex = route_topk(torch.randn(T, E, generator=g, device=dev), 2)
+    tok, counts, _ = sort_by_expert(ex, E)
+    a = gather_rows(x, tok)
+    copies = 2
+    sets = []
+    for _ in range(copies):
+        P, S = [], []
+        for _ in range(E):
+            p, s = quantize_int4(torch.randn(H, D, generator=g, device=dev) * 0.02, gs)
+            P.append(p)
+            S.append(s.to(torch.float16))
+        sets.append((torch.stack(P), torch.stack(S)))
+    fns = [lambda st=st: int4_grouped_matmul(a, st[0], st[1], counts, gs) for st in sets]
+    ms = time_steps(fns, warmup, steps)
+    rows = T * 2
+    nbytes = E * H * D // 2 + E * H * (D // gs) * 2 + rows * D * 2 + rows * H * 2
+    return dict(ms=ms, bytes=nbytes, flops=2 * rows * H * D, copies=copies,
+                counts=counts.tolist())
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+
+
+def cpu_baseline(budget_s: float = 10.0):
+    """The reference's CPU path (QuantLinear(use_kernel=False): dequantize W, then an
+    fp32 matmul; serve/quantize.py:39-47, 94) restated in numpy (oracle/ref.py),
+    timed on this host for the headline workload until `budget_s` seconds pass."""
+    import numpy as np
+    from oracle import ref
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # noqa: BLE001
+        threads = 1
+    rng = np.random.default_rng(0)
+    N = K = 4096
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    packed, scale = ref.quantize_int4((rng.standard_normal((N, K)) * 0.02).astype(np.float32), 128)
+    scale = scale.astype(np.float16).astype(np.float32)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        ref.int4_matmul(x, packed, scale, 128)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
+    nbytes = N * K // 2 + N * (K // 128) * 2 + K * 2 + N * 2
+    return {"value": round(nbytes / t / 1e12, 6), "unit": "TB/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} iterations of the M=1, K=N=4096 INT4 g128 layer (dequantize "
+                      f"+ fp32 matmul, numpy; elementwise dequant on 1 thread, BLAS on {threads}); "
+                      f"median {t * 1e3:.2f} ms per iteration"}
+
+
+# ----------------------------------------------------------------------------- main
+
+
+def _hbm_row(name, r, extra=None):
+    gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+    row = {"name": name, "ms_per_step": round(r["ms"], 6), "TB/s": round(gbs / 1e3, 4),
+           "TFLOP/s": round(r["flops"] / (r["ms"] * 1e-3) / 1e12, 3),
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)},
+           "bytes_per_step": r["bytes"], "weight_copies": r["copies"]}
+    row.update(extra or {})
+    return row
+
+
+def _mfma_row(name, r, peak, extra=None):
+    tf = r["flops"] / (r["ms"] * 1e-3) / 1e12
+    gbs = r["bytes"] / (r["ms"] * 1e-3) / 1e9
+    row = {"name": name, "ms_per_step": round(r["ms"], 6), "TFLOP/s": round(tf, 2),
+           "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": peak, "unit": "TFLOP/s",
+                        "frac": round(tf / peak, 4)},
+           "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "flops_per_step": r["flops"],
+           "copies": r["copies"]}
+    row.update(extra or {})
+    return row
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic.json), if any."""
+    f = ROOT / "profiles" / "traffic.json"
+    if f.exists():
+        try:
+            return json.loads(f.read_text()).get(name, {}).get("bytes_per_launch")
+        except (OSError, ValueError):
+            return None
+    return None
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=512)
+    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--only", default=None,
+                    help="run one workload: int4_gemv, int4_m4, int4_m16, int8_gemv, int8_prefill, "
+                         "fp8_gemm, moe_int4")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build runs on a single MI355X and has no "
+              "multi-GPU path (see DESIGN.md for how the path would shard); use --gpus 1",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    dev = torch.device("cuda:0")
+    small = max(8, args.steps // 8)
+    runners = {
+        "int4_gemv": lambda: _hbm_row("int4_gemv_m1", int4_gemv(dev, 1, args.steps, args.warmup)),
+        "int4_m4": lambda: _hbm_row("int4_gemv_m4", int4_gemv(dev, 4, args.steps, args.warmup)),
+        "int4_m16": lambda: _hbm_row("int4_gemv_m16", int4_gemv(dev, 16, args.steps, args.warmup)),
+        "int8_gemv": lambda: _hbm_row("int8_gemv_m1", int8_gemv(dev, 1, args.steps, args.warmup)),
+        "int8_prefill": lambda: _mfma_row("int8_prefill_2048x11008x4096",
+                                          int8_prefill(dev, small, 4), BF16_PEAK_TFLOPS),
+        "fp8_gemm": lambda: _mfma_row("fp8_e4m3_4096x8192x8192", fp8_gemm(dev, small, 4),
+                                      FP8_PEAK_TFLOPS),
+        "moe_int4": lambda: (lambda r: _mfma_row("moe_int4_grouped_1024x14336x4096", r,
+                                                 BF16_PEAK_TFLOPS,
+                                                 {"hbm_roofline_frac": round(
+                                                     r["bytes"] / (r["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                                  "segments": r["counts"]}))(
+            moe_int4(dev, small, 4)),
+    }
+    if args.only:
+        log(f"running {args.only}")
+        row = runners[args.only]()
+        log(json.dumps(row))
+        print(json.dumps({"only": args.only, **row}))
+        return 0
+
+    log("int4 GEMV M=1 (headline)")
+    head = runners["int4_gemv"]()
+    log(json.dumps(head))
+    extra = []
+    if not args.no_extra:
+        for k in ("int4_m4", "int4_m16", "int8_gemv", "int8_prefill", "fp8_gemm", "moe_int4"):
+            log(f"{k} ...")
+            row = runners[k]()
+            log(json.dumps(row))
+            extra.append(row)
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle on host cores, ~10 s)")
+        cpu = cpu_baseline()
+        log(json.dumps(cpu))
+
+    ms = head["ms_per_step"]
+    roof = dict(head["roofline"])
+    roof["traffic"] = load_traffic("int4_gemv_m1")
+    line = {
+        "metric": METRIC,
+        "value": head["TB/s"],
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "INT4 g128 weight-only decode GEMV (BASELINE.json configs[1])",
+                   "M": 1, "N": 4096, "K": 4096, "group": 128, "activations": "bf16",
+                   "scales": "fp16", "output": "bf16", "bytes_per_step": head["bytes_per_step"],
+                   "weight_copies_rotated": head["weight_copies"], "launch": "HIP graph replay"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,148 @@
+/*
+ * mls.h — C ABI of libmls_hip.so, the gfx950 (MI355X) quantized-linear library.
+ *
+ * Plain C: raw device pointers, element strides, sizes and a HIP stream. No
+ * torch types cross this boundary. Every entry point validates its arguments on
+ * the host before any HIP call and returns MLS_OK (0) or a negative MLS_ERR_*
+ * code; mls_last_error() then holds a message (thread-local).
+ *
+ * Ownership: the caller allocates every buffer (inputs, outputs and any
+ * workspace). The library never allocates, frees or synchronises on these
+ * paths; all work is enqueued on `stream` (a hipStream_t; NULL = the default
+ * stream of the current device).
+ *
+ * Layouts (all row-major, unit inner stride, leading dimensions in ELEMENTS):
+ *   activations  a[M][K]           lda >= K
+ *   INT8 weights w[N][K] int8      ldw >= K        scale s[N]
+ *   INT4 weights w[N][K/2] uint8   ldw >= K/2      scale s[N][K/group] with
+ *                (even k -> low nibble, value = nibble - 8)     strides ld_sn, ld_sg
+ *   e4m3 bytes   OCP FP8 E4M3 ("fn": bias 7, no inf, max 448, NaN = S.1111.111)
+ *
+ * dtype codes: MLS_F32, MLS_F16, MLS_BF16.
+ */
+#ifndef MLS_H
+#define MLS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* mls_stream_t; /* identical to hipStream_t */
+
+enum { MLS_F32 = 0, MLS_F16 = 1, MLS_BF16 = 2 };
+enum {
+  MLS_OK = 0,
+  MLS_ERR_ARG = -1,         /* invalid argument (shape, stride, dtype, null, alignment) */
+  MLS_ERR_UNSUPPORTED = -2, /* valid but outside what the library implements */
+  MLS_ERR_HIP = -3          /* a HIP runtime call failed */
+};
+
+#define MLS_ABI_VERSION 1
+
+/* No reference counterpart: version of this ABI (MLS_ABI_VERSION). */
+int mls_abi_version(void);
+
+/* No reference counterpart: message for the last failing call on this thread. */
+const char* mls_last_error(void);
+
+/* ---------------------------------------------------------------- e4m3 codec */
+
+/* Replaces _decode_e4m3_kernel + decode_e4m3 (kernels/fp8_matmul.py:37-47, 84-100):
+ * out[i] = value of e4m3 byte bits[i] as fp32; the NaN patterns 0x7F/0xFF decode
+ * to 0 (fp8_matmul.py:46). Bit-exact. */
+int mls_e4m3_decode(const uint8_t* bits, float* out, int64_t n, mls_stream_t stream);
+
+/* Replaces dequantize_e4m3 (kernels/fp8_matmul.py:109-110): out[r][c] =
+ * value(bits[r][c]) * scale_r, where NaN patterns stay NaN (torch's float8 view
+ * semantics) and scale_r = scale_ptr ? scale_ptr[r * scale_stride] : scale.
+ * The multiply is one fp32 rounding, as in the reference. */
+int mls_e4m3_dequantize(const uint8_t* bits, int64_t rows, int64_t cols, int64_t ldb,
+                        float scale, const float* scale_ptr, int64_t scale_stride,
+                        float* out, int64_t ldo, mls_stream_t stream);
+
+/* Replaces quantize_e4m3 (kernels/fp8_matmul.py:103-106): q = x / scale_r
+ * (IEEE fp32 division), clamped to [-448, 448], then rounded to the nearest e4m3
+ * value, ties to even. x is f32/f16/bf16 (x_dt). NaN inputs give 0x7F|sign.
+ * scale_r as for mls_e4m3_dequantize. Bit-exact against the reference's CPU path. */
+int mls_e4m3_encode(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
+                    float scale, const float* scale_ptr, int64_t scale_stride,
+                    uint8_t* out, int64_t ldo, mls_stream_t stream);
+
+/* ---------------------------------------------------------------- quantizers */
+
+/* Replaces quantize_int8 (serve/quantize.py:18-21) for device tensors:
+ * scale[n] = max(max_k |w[n][k]| / 127, 1e-8); wq = clamp(rint(w / scale), -127, 127).
+ * fp32 in, IEEE division, round half to even. Bit-exact. */
+int mls_quantize_int8(const float* w, int64_t N, int64_t K, int64_t ldw,
+                      int8_t* wq, int64_t ldq, float* scale, mls_stream_t stream);
+
+/* Replaces quantize_int4 (serve/quantize.py:28-36) for device tensors: per group of
+ * `group` along K, scale = max(amax / 7, 1e-8); q = clamp(rint(w / scale), -8, 7) + 8;
+ * packed[n][j] = q[n][2j] | q[n][2j+1] << 4. scale is [N][K/group] contiguous.
+ * Requires K % group == 0 and K even. Bit-exact. */
+int mls_quantize_int4(const float* w, int64_t N, int64_t K, int64_t ldw, int group,
+                      uint8_t* packed, int64_t ldp, float* scale, mls_stream_t stream);
+
+/* ---------------------------------------------------------------- GEMMs */
+
+/* Replaces _int8_matmul_kernel + int8_matmul (kernels/dequant_matmul.py:39-66, 140-152):
+ * c[m][n] = s[n] * sum_k a[m][k] * w[n][k], fp32 accumulation, one rounding to c_dt.
+ * a_dt = c_dt in {F32, F16, BF16}; s_dt in {F32, F16}. Any M, N, K >= 1. */
+int mls_int8_gemm(const void* a, int a_dt, int64_t lda,
+                  const int8_t* w, int64_t ldw,
+                  const void* s, int s_dt,
+                  void* c, int c_dt, int64_t ldc,
+                  int64_t M, int64_t N, int64_t K, mls_stream_t stream);
+
+/* Replaces _int4_matmul_kernel + int4_matmul (kernels/dequant_matmul.py:69-100, 170-185):
+ * c[m][n] = sum_k a[m][k] * (nib(w, n, k) - 8) * s[n * ld_sn + (k / group) * ld_sg].
+ * Requires K % group == 0 (the reference's assert, :175). fp32 accumulation. */
+int mls_int4_gemm(const void* a, int a_dt, int64_t lda,
+                  const uint8_t* w, int64_t ldw,
+                  const void* s, int s_dt, int64_t ld_sn, int64_t ld_sg, int group,
+                  void* c, int c_dt, int64_t ldc,
+                  int64_t M, int64_t N, int64_t K, mls_stream_t stream);
+
+/* Replaces _int8_dgrad_kernel + int8_dgrad (kernels/dequant_matmul.py:103-132, 155-167):
+ * dx[m][k] = sum_n dy[m][n] * s[n] * w[n][k] (the input gradient of y = x W^T). */
+int mls_int8_dgrad(const void* dy, int dy_dt, int64_t lddy,
+                   const int8_t* w, int64_t ldw,
+                   const void* s, int s_dt,
+                   void* dx, int dx_dt, int64_t lddx,
+                   int64_t M, int64_t N, int64_t K, mls_stream_t stream);
+
+/* Replaces _fp8_matmul_kernel + fp8_matmul (kernels/fp8_matmul.py:50-81, 113-128):
+ * c[m][n] = (sum_k e4m3(a[m][k]) * e4m3(b[n][k])) * sa_m * sb_n with fp32
+ * accumulation (native gfx950 fp8 MFMA). sa_m = sa_ptr ? sa_ptr[m * sa_stride] : sa,
+ * likewise sb_n: per-tensor (the reference) or per-row scales. c_dt any of F32/F16/BF16.
+ * NaN operand bytes propagate NaN (the reference decodes them to 0; quantize_e4m3
+ * never produces them). */
+int mls_fp8_gemm(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb,
+                 float sa, const float* sa_ptr, int64_t sa_stride,
+                 float sb, const float* sb_ptr, int64_t sb_stride,
+                 void* c, int c_dt, int64_t ldc,
+                 int64_t M, int64_t N, int64_t K, mls_stream_t stream);
+
+/* Replaces the per-expert segment loop of moe_dispatch_combine
+ * (kernels/moe_routing.py:145-151) that calls int4_matmul once per expert through
+ * QuantLinear (serve/quantize.py:110-114): one launch over all experts.
+ * Rows seg_off[e] .. seg_off[e+1]-1 of a (expert-sorted, M_total rows) multiply
+ * expert e's packed weights w + e*w_estride (bytes) with scales s + e*s_estride
+ * (elements). seg_off is a DEVICE int32 array of E+1 non-decreasing offsets with
+ * seg_off[0] = 0 and seg_off[E] = M_total; it is read on the device (no host sync).
+ * a_dt = c_dt in {F16, BF16}. */
+int mls_int4_grouped_gemm(const void* a, int a_dt, int64_t lda,
+                          const int32_t* seg_off, int E, int64_t M_total,
+                          const uint8_t* w, int64_t w_estride, int64_t ldw,
+                          const void* s, int s_dt, int64_t s_estride,
+                          int64_t ld_sn, int64_t ld_sg, int group,
+                          void* c, int c_dt, int64_t ldc,
+                          int64_t N, int64_t K, mls_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MLS_H */

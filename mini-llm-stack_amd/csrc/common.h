@@ -1,0 +1,87 @@
+// Internal helpers shared by the gfx950 kernels and the C-ABI entry points.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mls.h"
+
+namespace mls {
+
+// ----------------------------------------------------------------- host side
+
+// Records `msg` as this thread's last error and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Checks the launch that was just enqueued.
+int check_launch(const char* what);
+
+inline bool is_float_dt(int dt) { return dt == MLS_F32 || dt == MLS_F16 || dt == MLS_BF16; }
+inline int dt_size(int dt) { return dt == MLS_F32 ? 4 : 2; }
+inline bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ----------------------------------------------------------------- device side
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(_Float16 v) { return (float)v; }
+__device__ __forceinline__ float to_f32(__bf16 v) { return (float)v; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { return (_Float16)v; }
+template <> __device__ __forceinline__ __bf16 from_f32<__bf16>(float v) { return (__bf16)v; }
+
+__device__ __forceinline__ uint32_t pack2_bits(__bf16 lo, __bf16 hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+__device__ __forceinline__ uint32_t pack2_bits(_Float16 lo, _Float16 hi) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+
+// Stores 4 consecutive outputs (converted from fp32) with one 8- or 16-byte store.
+// dst must be aligned to 4 elements.
+template <typename T>
+__device__ __forceinline__ void store4(T* dst, float v0, float v1, float v2, float v3) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<float4*>(dst) = make_float4(v0, v1, v2, v3);
+  } else {
+    const uint2 u = make_uint2(pack2_bits(from_f32<T>(v0), from_f32<T>(v1)),
+                               pack2_bits(from_f32<T>(v2), from_f32<T>(v3)));
+    *reinterpret_cast<uint2*>(dst) = u;
+  }
+}
+
+// Sum over the 64 lanes of a wavefront; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Remaps a linear workgroup id so that consecutive logical tiles land on the same
+// XCD. The dispatcher hands workgroup i to XCD i % 8; logical tile t is executed by
+// the workgroup whose id places it on XCD t / ceil(n/8). Valid for any n.
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+  const int per = (n + 7) / 8;      // logical tiles per XCD (last XCDs may get fewer)
+  const int full = n % 8 == 0 ? 8 : n % 8;  // XCDs that receive `per` workgroups
+  const int xcd = bid % 8, slot = bid / 8;
+  // XCDs [0, full) hold `per` workgroups, the rest hold per-1.
+  return xcd < full ? xcd * per + slot : full * per + (xcd - full) * (per - 1) + slot;
+}
+
+}  // namespace mls

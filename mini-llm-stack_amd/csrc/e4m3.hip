@@ -1,0 +1,148 @@
+// OCP FP8 E4M3 ("fn") codec kernels: decode (reference semantics: NaN -> 0),
+// dequantize (NaN stays NaN, times a scale) and the saturating encoder used by
+// quantize_e4m3. Written from the OCP OFP8 definition: 1 sign, 4 exponent bits
+// (bias 7), 3 mantissa bits, no infinities, S.1111.111 = NaN, max finite 448.
+#include "common.h"
+
+namespace mls {
+
+// Exact value of an e4m3 byte. nan_to_zero selects the reference kernel's
+// decode (kernels/fp8_matmul.py:37-47), which maps the NaN patterns to (signed) 0.
+__device__ __forceinline__ float e4m3_value(uint32_t b, bool nan_to_zero) {
+  const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  float mag;
+  if (e == 0) mag = (float)m * 0x1p-9f;                        // subnormal: m/8 * 2^-6
+  else mag = __uint_as_float(((e + 120u) << 23) | (m << 20));  // (1 + m/8) * 2^(e-7)
+  if (e == 15u && m == 7u) mag = nan_to_zero ? 0.0f : __uint_as_float(0x7FC00000u);
+  return (b & 0x80u) ? -mag : mag;
+}
+
+// e4m3 code of a finite magnitude 0 <= a <= 448, round to nearest, ties to even.
+__device__ __forceinline__ uint32_t e4m3_code_of_mag(float a) {
+  const uint32_t u = __float_as_uint(a);
+  if (u < 0x3C800000u)  // a < 2^-6: the subnormal grid has step 2^-9; code 8 is 2^-6
+    return (uint32_t)__builtin_rintf(a * 512.0f);
+  // a >= 2^-6: fp32 exponent field E >= 121. Keep the 3 top mantissa bits and
+  // rebias the exponent (127 -> 7); a carry out of the mantissa bumps the exponent.
+  uint32_t code = (u >> 20) - (120u << 3);
+  const uint32_t rem = u & 0xFFFFFu;
+  if (rem > 0x80000u || (rem == 0x80000u && (code & 1u))) code += 1u;
+  return code;
+}
+
+// Saturating encode of q (already divided by the scale): NaN -> 0x7F | sign,
+// otherwise clamp |q| to 448 and round.
+__device__ __forceinline__ uint32_t e4m3_encode(float q) {
+  const uint32_t sign = (__float_as_uint(q) >> 24) & 0x80u;
+  if (__builtin_isnan(q)) return 0x7Fu | sign;
+  return e4m3_code_of_mag(fminf(fabsf(q), 448.0f)) | sign;
+}
+
+// vec: bits/out are 16-byte aligned, so the bulk is read 16 bytes per thread.
+__global__ void e4m3_decode_kernel(const uint8_t* __restrict__ bits, float* __restrict__ out,
+                                   int64_t n, bool vec) {
+  const int64_t nvec = vec ? n / 16 : 0;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int64_t v = tid; v < nvec; v += stride) {
+    const uint4 w = reinterpret_cast<const uint4*>(bits)[v];
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    float4* o = reinterpret_cast<float4*>(out + v * 16);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float4 f;
+      f.x = e4m3_value(words[q] & 0xFFu, true);
+      f.y = e4m3_value((words[q] >> 8) & 0xFFu, true);
+      f.z = e4m3_value((words[q] >> 16) & 0xFFu, true);
+      f.w = e4m3_value(words[q] >> 24, true);
+      o[q] = f;
+    }
+  }
+  for (int64_t i = nvec * 16 + tid; i < n; i += stride) out[i] = e4m3_value(bits[i], true);
+}
+
+__global__ void e4m3_dequant_kernel(const uint8_t* __restrict__ bits, int64_t rows, int64_t cols,
+                                    int64_t ldb, float scale, const float* __restrict__ sp,
+                                    int64_t sstride, float* __restrict__ out, int64_t ldo) {
+  const int64_t total = rows * cols;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t r = i / cols, c = i - r * cols;
+    const float s = sp ? sp[r * sstride] : scale;
+    out[r * ldo + c] = e4m3_value(bits[r * ldb + c], false) * s;
+  }
+}
+
+template <typename T>
+__global__ void e4m3_encode_kernel(const T* __restrict__ x, int64_t rows, int64_t cols, int64_t ldx,
+                                   float scale, const float* __restrict__ sp, int64_t sstride,
+                                   uint8_t* __restrict__ out, int64_t ldo) {
+  const int64_t total = rows * cols;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t r = i / cols, c = i - r * cols;
+    const float s = sp ? sp[r * sstride] : scale;
+    out[r * ldo + c] = (uint8_t)e4m3_encode(to_f32(x[r * ldx + c]) / s);
+  }
+}
+
+static int grid_for(int64_t work, int block) {
+  int64_t g = cdiv(work, block);
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+}  // namespace mls
+
+using namespace mls;
+
+extern "C" int mls_e4m3_decode(const uint8_t* bits, float* out, int64_t n, mls_stream_t stream) {
+  if (n < 0) return fail(MLS_ERR_ARG, "mls_e4m3_decode: n=%lld < 0", (long long)n);
+  if (n == 0) return MLS_OK;
+  if (!bits || !out) return fail(MLS_ERR_ARG, "mls_e4m3_decode: null pointer");
+  const bool vec = aligned(bits, 16) && aligned(out, 16);
+  const int block = 256;
+  hipLaunchKernelGGL(e4m3_decode_kernel, dim3(grid_for(vec ? n / 16 + 1 : n, block)), dim3(block),
+                     0, (hipStream_t)stream, bits, out, n, vec);
+  return check_launch("mls_e4m3_decode");
+}
+
+extern "C" int mls_e4m3_dequantize(const uint8_t* bits, int64_t rows, int64_t cols, int64_t ldb,
+                                   float scale, const float* scale_ptr, int64_t scale_stride,
+                                   float* out, int64_t ldo, mls_stream_t stream) {
+  if (rows < 0 || cols < 0) return fail(MLS_ERR_ARG, "mls_e4m3_dequantize: negative size");
+  if (rows == 0 || cols == 0) return MLS_OK;
+  if (!bits || !out) return fail(MLS_ERR_ARG, "mls_e4m3_dequantize: null pointer");
+  if (ldb < cols || ldo < cols || scale_stride < 0)
+    return fail(MLS_ERR_ARG, "mls_e4m3_dequantize: bad leading dimension or scale stride");
+  const int block = 256;
+  hipLaunchKernelGGL(e4m3_dequant_kernel, dim3(grid_for(rows * cols, block)), dim3(block), 0,
+                     (hipStream_t)stream, bits, rows, cols, ldb, scale, scale_ptr, scale_stride,
+                     out, ldo);
+  return check_launch("mls_e4m3_dequantize");
+}
+
+extern "C" int mls_e4m3_encode(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
+                               float scale, const float* scale_ptr, int64_t scale_stride,
+                               uint8_t* out, int64_t ldo, mls_stream_t stream) {
+  if (rows < 0 || cols < 0) return fail(MLS_ERR_ARG, "mls_e4m3_encode: negative size");
+  if (rows == 0 || cols == 0) return MLS_OK;
+  if (!x || !out) return fail(MLS_ERR_ARG, "mls_e4m3_encode: null pointer");
+  if (!is_float_dt(x_dt)) return fail(MLS_ERR_ARG, "mls_e4m3_encode: bad x dtype %d", x_dt);
+  if (ldx < cols || ldo < cols || scale_stride < 0)
+    return fail(MLS_ERR_ARG, "mls_e4m3_encode: bad leading dimension or scale stride");
+  const int block = 256;
+  const dim3 grid(grid_for(rows * cols, block));
+  hipStream_t st = (hipStream_t)stream;
+  if (x_dt == MLS_F32)
+    hipLaunchKernelGGL(e4m3_encode_kernel<float>, grid, dim3(block), 0, st, (const float*)x, rows,
+                       cols, ldx, scale, scale_ptr, scale_stride, out, ldo);
+  else if (x_dt == MLS_F16)
+    hipLaunchKernelGGL(e4m3_encode_kernel<_Float16>, grid, dim3(block), 0, st, (const _Float16*)x,
+                       rows, cols, ldx, scale, scale_ptr, scale_stride, out, ldo);
+  else
+    hipLaunchKernelGGL(e4m3_encode_kernel<__bf16>, grid, dim3(block), 0, st, (const __bf16*)x, rows,
+                       cols, ldx, scale, scale_ptr, scale_stride, out, ldo);
+  return check_launch("mls_e4m3_encode");
+}

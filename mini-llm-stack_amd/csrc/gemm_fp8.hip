@@ -1,0 +1,220 @@
+// e4m3 x e4m3 -> fp32-accumulated GEMM with inline scales (kernels/fp8_matmul.py:50-81),
+// on the gfx950 fp8 MFMA (v_mfma_f32_16x16x128_f8f6f4 with both operands OCP e4m3).
+//
+// Block tile 256 (m) x 256 (n) x 128 (k); 4 wavefronts in 2 x 2, each owning a
+// 128 x 128 sub-tile = 8 x 8 MFMA tiles (256 fp32 accumulators per lane). Both
+// operands are K-contiguous ("NT"): a stage is 256 rows x 128 bytes per operand,
+// staged global -> registers -> LDS with the 16-byte chunk index XOR-swizzled by
+// (row & 7), double-buffered with one barrier per stage. The B tile is the MFMA
+// "A" operand so each lane ends with 4 consecutive n of one m: the epilogue
+// applies sa[m] * sb[n] and stores 4 outputs at once.
+//
+// Shapes outside the fast path (K % 128 != 0, small or unaligned operands) run
+// a one-thread-per-output kernel that decodes with the reference's NaN -> 0 rule.
+#include "common.h"
+
+namespace mls {
+
+__device__ __forceinline__ float e4m3_ref_value(uint32_t b) {
+  const uint32_t e = (b >> 3) & 15u, m = b & 7u;
+  float mag = e == 0 ? (float)m * 0x1p-9f : __uint_as_float(((e + 120u) << 23) | (m << 20));
+  if (e == 15u && m == 7u) mag = 0.0f;
+  return (b & 0x80u) ? -mag : mag;
+}
+
+template <typename CT>
+__global__ void fp8_gemm_generic_kernel(const uint8_t* __restrict__ a, int64_t lda,
+                                        const uint8_t* __restrict__ b, int64_t ldb, float sa,
+                                        const float* __restrict__ sap, int64_t sas, float sb,
+                                        const float* __restrict__ sbp, int64_t sbs,
+                                        CT* __restrict__ c, int64_t ldc, int64_t M, int64_t N,
+                                        int64_t K) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= M * N) return;
+  const int64_t m = t / N, n = t - m * N;
+  const uint8_t* ar = a + m * lda;
+  const uint8_t* br = b + n * ldb;
+  float acc = 0.0f;
+  for (int64_t k = 0; k < K; ++k) acc = fmaf(e4m3_ref_value(ar[k]), e4m3_ref_value(br[k]), acc);
+  const float s = (sap ? sap[m * sas] : sa) * (sbp ? sbp[n * sbs] : sb);
+  c[m * ldc + n] = from_f32<CT>(acc * s);
+}
+
+__device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, const f32x4& c) {
+  // format 0 / 0 = e4m3 for both operands; zero scales select the unscaled instruction
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void fp8_gemm_mfma_kernel(
+    const uint8_t* __restrict__ a, int64_t lda, const uint8_t* __restrict__ b, int64_t ldb,
+    float sa, const float* __restrict__ sap, int64_t sas, float sb,
+    const float* __restrict__ sbp, int64_t sbs, CT* __restrict__ c, int64_t ldc, int M, int N,
+    int K, int m_tiles, int n_tiles) {
+  constexpr int BM = 256, BN = 256, BK = 128;
+  constexpr int GM = 4;  // m-tiles per group in the tile order
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint4* As = reinterpret_cast<uint4*>(smem);  // [2][BM][8] 16-byte chunks
+  uint4* Bs = As + 2 * BM * 8;                  // [2][BN][8]
+
+  // grouped tile order after the XCD remap: runs of GM m-tiles sweep all n-tiles
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_group = GM * n_tiles;
+  const int g = L / per_group, first_m = g * GM;
+  const int gsz = min(m_tiles - first_m, GM);
+  const int r = L % per_group;
+  const int mt = first_m + r % gsz, nt = r / gsz;
+  const int m0 = mt * BM, n0 = nt * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave >> 1) * 128, wn0 = (wave & 1) * 128;
+
+  // each thread stages chunks q = tid + 256 i (i < 8) of both operands: row q / 8 =
+  // srow + 32 i, chunk q % 8 = skc; the swizzled LDS slot is lds0 + 256 i. Loads go
+  // through buffer descriptors covering only this tile's valid rows, so rows past
+  // M or N read as zeros; the stage offset k0 travels in the scalar offset.
+  const int srow = tid >> 3, skc = tid & 7;
+  const int lds0 = srow * 8 + (skc ^ (srow & 7));
+  const int rows_a = min(BM, M - m0), rows_b = min(BN, N - n0);
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a + (int64_t)m0 * lda), (short)0, (int)(rows_a * lda), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(b + (int64_t)n0 * ldb), (short)0, (int)(rows_b * ldb), 0x00020000);
+  int a_off[8], b_off[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a_off[i] = (srow + 32 * i) * (int)lda + skc * 16;
+    b_off[i] = (srow + 32 * i) * (int)ldb + skc * 16;
+  }
+  uint4 ra[8], rb[8];
+#define MLS_FP8_LOAD(k0)                                                                  \
+  _Pragma("unroll") for (int i = 0; i < 8; ++i) {                                         \
+    ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsa, a_off[i], (k0), 0)); \
+    rb[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsb, b_off[i], (k0), 0)); \
+  }
+#define MLS_FP8_STORE(buf)                                              \
+  _Pragma("unroll") for (int i = 0; i < 8; ++i) {                       \
+    As[(buf) * BM * 8 + lds0 + 256 * i] = ra[i];                        \
+    Bs[(buf) * BN * 8 + lds0 + 256 * i] = rb[i];                        \
+  }
+
+  f32x4 acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = K / BK;
+  MLS_FP8_LOAD(0)
+  MLS_FP8_STORE(0)
+  __syncthreads();
+
+  const int lr = lane & 15, lk = lane >> 4;  // operand row, 32-byte k block
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) { MLS_FP8_LOAD((kt + 1) * BK) }
+    const uint4* as = As + buf * BM * 8;
+    const uint4* bs = Bs + buf * BN * 8;
+    i32x8 bop[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int row = wn0 + i * 16 + lr, sw = row & 7;
+      const uint4 lo = bs[row * 8 + ((2 * lk) ^ sw)];
+      const uint4 hi = bs[row * 8 + ((2 * lk + 1) ^ sw)];
+      bop[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                     (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = wm0 + j * 16 + lr, sw = row & 7;
+      const uint4 lo = as[row * 8 + ((2 * lk) ^ sw)];
+      const uint4 hi = as[row * 8 + ((2 * lk + 1) ^ sw)];
+      const i32x8 aop = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
+                         (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i][j] = mfma_fp8(bop[i], aop, acc[i][j]);
+    }
+    if (kt + 1 < nk) { MLS_FP8_STORE(buf ^ 1) }
+    __syncthreads();
+  }
+
+#undef MLS_FP8_LOAD
+#undef MLS_FP8_STORE
+
+  // epilogue: acc[i][j][r] = C[m = m0+wm0+16j+lr][n = n0+wn0+16i+4lk+r]
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int nb = n0 + wn0 + i * 16 + 4 * lk;
+    float sbn[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) sbn[rr] = sbp ? (nb + rr < N ? sbp[(int64_t)(nb + rr) * sbs] : 0.f) : sb;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int m = m0 + wm0 + j * 16 + lr;
+      if (m >= M) continue;
+      const float sam = sap ? sap[(int64_t)m * sas] : sa;
+      CT* dst = c + (int64_t)m * ldc + nb;
+      const float v0 = acc[i][j][0] * (sam * sbn[0]), v1 = acc[i][j][1] * (sam * sbn[1]);
+      const float v2 = acc[i][j][2] * (sam * sbn[2]), v3 = acc[i][j][3] * (sam * sbn[3]);
+      if (nb + 3 < N && (ldc % 4) == 0) {
+        store4<CT>(dst, v0, v1, v2, v3);
+      } else {
+        if (nb + 0 < N) dst[0] = from_f32<CT>(v0);
+        if (nb + 1 < N) dst[1] = from_f32<CT>(v1);
+        if (nb + 2 < N) dst[2] = from_f32<CT>(v2);
+        if (nb + 3 < N) dst[3] = from_f32<CT>(v3);
+      }
+    }
+  }
+}
+
+template <typename CT>
+static int launch_fp8(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, float sa,
+                      const float* sap, int64_t sas, float sb, const float* sbp, int64_t sbs,
+                      void* c, int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+  // buffer descriptors address at most 2^31 bytes per 256-row tile
+  const bool fast = K >= 128 && K % 128 == 0 && M >= 64 && N >= 64 && aligned(a, 16) &&
+                    aligned(b, 16) && lda % 16 == 0 && ldb % 16 == 0 && aligned(c, 16) &&
+                    M < (1 << 30) && N < (1 << 30) && lda * 256 < (1ll << 31) &&
+                    ldb * 256 < (1ll << 31);
+  if (!fast) {
+    hipLaunchKernelGGL(fp8_gemm_generic_kernel<CT>, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0,
+                       st, a, lda, b, ldb, sa, sap, sas, sb, sbp, sbs, (CT*)c, ldc, M, N, K);
+    return check_launch("mls_fp8_gemm(generic)");
+  }
+  const int mt = (int)cdiv(M, 256), nt = (int)cdiv(N, 256);
+  const size_t lds = 2 * 2 * 256 * 128;
+  auto kern = fp8_gemm_mfma_kernel<CT>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return fail(MLS_ERR_HIP, "mls_fp8_gemm: cannot reserve %zu bytes of LDS", lds);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)(mt * nt)), dim3(256), lds, st, a, lda, b, ldb, sa, sap,
+                     sas, sb, sbp, sbs, (CT*)c, ldc, (int)M, (int)N, (int)K, mt, nt);
+  return check_launch("mls_fp8_gemm");
+}
+
+}  // namespace mls
+
+using namespace mls;
+
+extern "C" int mls_fp8_gemm(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, float sa,
+                            const float* sa_ptr, int64_t sa_stride, float sb, const float* sb_ptr,
+                            int64_t sb_stride, void* c, int c_dt, int64_t ldc, int64_t M, int64_t N,
+                            int64_t K, mls_stream_t stream) {
+  if (M < 0 || N < 0 || K < 0)
+    return fail(MLS_ERR_ARG, "mls_fp8_gemm: negative size M=%lld N=%lld K=%lld", (long long)M,
+                (long long)N, (long long)K);
+  if (!is_float_dt(c_dt)) return fail(MLS_ERR_ARG, "mls_fp8_gemm: bad output dtype %d", c_dt);
+  if (M == 0 || N == 0) return MLS_OK;
+  if (!a || !b || !c) return fail(MLS_ERR_ARG, "mls_fp8_gemm: null pointer");
+  if (lda < K || ldb < K || ldc < N || sa_stride < 0 || sb_stride < 0)
+    return fail(MLS_ERR_ARG, "mls_fp8_gemm: bad leading dimension or scale stride");
+  hipStream_t st = (hipStream_t)stream;
+  if (c_dt == MLS_F32) return launch_fp8<float>(a, lda, b, ldb, sa, sa_ptr, sa_stride, sb, sb_ptr, sb_stride, c, ldc, M, N, K, st);
+  if (c_dt == MLS_F16) return launch_fp8<_Float16>(a, lda, b, ldb, sa, sa_ptr, sa_stride, sb, sb_ptr, sb_stride, c, ldc, M, N, K, st);
+  return launch_fp8<__bf16>(a, lda, b, ldb, sa, sa_ptr, sa_stride, sb, sb_ptr, sb_stride, c, ldc, M, N, K, st);
+}

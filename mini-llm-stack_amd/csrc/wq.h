@@ -1,0 +1,45 @@
+// Internal launchers of the weight-only (INT8 / INT4) GEMM family.
+#pragma once
+
+#include "common.h"
+
+namespace mls {
+
+// Arguments of one weight-only GEMM c[M][N] = a[M][K] . dequant(w)[N][K]^T.
+struct WqArgs {
+  const void* a;
+  int a_dt;
+  int64_t lda;
+  const uint8_t* w;  // int8 [N][ldw] or packed int4 [N][ldw]
+  int64_t ldw;
+  const void* s;
+  int s_dt;
+  int64_t ld_sn, ld_sg;  // scale strides (INT8: ld_sn = 1, ld_sg = 0)
+  int group;             // INT4 group (INT8: 0)
+  void* c;
+  int64_t ldc;
+  int64_t M, N, K;
+  hipStream_t stream;
+};
+
+// VALU decode GEMV for small M (x kept in registers). Returns MLS_ERR_UNSUPPORTED
+// when the shape or alignment is outside its fast path.
+int launch_gemv_wq(int wbits, const WqArgs& p);
+
+// MFMA tiled GEMM for 16-bit activations. MLS_ERR_UNSUPPORTED outside its fast path.
+int launch_gemm_wq_mfma(int wbits, const WqArgs& p);
+
+// Any shape, any dtype: one thread per output element.
+int launch_gemm_wq_generic(int wbits, const WqArgs& p);
+
+// Per-expert INT4 GEMM over expert-sorted row segments (MFMA).
+struct GroupedArgs {
+  WqArgs base;            // base.M = total rows; base.w/base.s point at expert 0
+  const int32_t* seg_off; // device [E+1]
+  int E;
+  int64_t w_estride;      // bytes between experts' packed weights
+  int64_t s_estride;      // elements between experts' scales
+};
+int launch_grouped_int4(const GroupedArgs& p);
+
+}  // namespace mls

@@ -1,0 +1,99 @@
+// C-ABI entry points of the weight-only GEMMs: argument validation on the host,
+// then dispatch by shape: the VALU decode GEMV for small M (and fp32
+// activations), the MFMA tiled GEMM for larger M with 16-bit activations, and a
+// one-thread-per-output kernel for shapes neither fast path covers.
+#include "wq.h"
+
+using namespace mls;
+
+namespace {
+
+int validate(const char* fn, int wbits, const WqArgs& p, int c_dt) {
+  if (p.M < 0 || p.N < 0 || p.K < 0)
+    return fail(MLS_ERR_ARG, "%s: negative size M=%lld N=%lld K=%lld", fn, (long long)p.M,
+                (long long)p.N, (long long)p.K);
+  if (!is_float_dt(p.a_dt)) return fail(MLS_ERR_ARG, "%s: bad activation dtype %d", fn, p.a_dt);
+  if (c_dt != p.a_dt)
+    return fail(MLS_ERR_ARG, "%s: output dtype %d must equal activation dtype %d", fn, c_dt, p.a_dt);
+  if (p.s_dt != MLS_F32 && p.s_dt != MLS_F16)
+    return fail(MLS_ERR_ARG, "%s: scale dtype %d (f32 or f16)", fn, p.s_dt);
+  if (wbits == 4) {
+    if (p.group < 1) return fail(MLS_ERR_ARG, "%s: group %d < 1", fn, p.group);
+    if (p.K % p.group != 0 || p.K % 2 != 0)
+      return fail(MLS_ERR_ARG, "%s: K=%lld must be even and a multiple of group %d", fn,
+                  (long long)p.K, p.group);
+    if (p.ld_sn < 0 || p.ld_sg < 0) return fail(MLS_ERR_ARG, "%s: negative scale stride", fn);
+  }
+  if (p.M == 0 || p.N == 0) return MLS_OK;
+  if (!p.a || !p.w || !p.s || !p.c) return fail(MLS_ERR_ARG, "%s: null pointer", fn);
+  const int64_t wcols = wbits == 4 ? p.K / 2 : p.K;
+  if (p.lda < p.K || p.ldw < wcols || p.ldc < p.N)
+    return fail(MLS_ERR_ARG, "%s: bad leading dimension (lda=%lld ldw=%lld ldc=%lld)", fn,
+                (long long)p.lda, (long long)p.ldw, (long long)p.ldc);
+  if (p.M * p.N / 256 > 0x7FFFFFFF) return fail(MLS_ERR_UNSUPPORTED, "%s: M*N too large", fn);
+  return MLS_OK;
+}
+
+int run(const char* fn, int wbits, const WqArgs& p) {
+  if (p.M == 0 || p.N == 0) return MLS_OK;
+  int rc = MLS_ERR_UNSUPPORTED;
+  if (p.K > 0) {
+    const bool small_m = p.a_dt == MLS_F32 || p.M <= 16;
+    if (small_m) {
+      rc = launch_gemv_wq(wbits, p);
+    } else {
+      rc = launch_gemm_wq_mfma(wbits, p);
+      if (rc == MLS_ERR_UNSUPPORTED) rc = launch_gemv_wq(wbits, p);
+    }
+  }
+  if (rc == MLS_ERR_UNSUPPORTED) rc = launch_gemm_wq_generic(wbits, p);
+  if (rc != MLS_OK) return rc;
+  return check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" int mls_int8_gemm(const void* a, int a_dt, int64_t lda, const int8_t* w, int64_t ldw,
+                             const void* s, int s_dt, void* c, int c_dt, int64_t ldc, int64_t M,
+                             int64_t N, int64_t K, mls_stream_t stream) {
+  WqArgs p{a, a_dt, lda, reinterpret_cast<const uint8_t*>(w), ldw, s, s_dt, 1, 0, 0,
+           c, ldc, M, N, K, (hipStream_t)stream};
+  int rc = validate("mls_int8_gemm", 8, p, c_dt);
+  if (rc != MLS_OK) return rc;
+  return run("mls_int8_gemm", 8, p);
+}
+
+extern "C" int mls_int4_gemm(const void* a, int a_dt, int64_t lda, const uint8_t* w, int64_t ldw,
+                             const void* s, int s_dt, int64_t ld_sn, int64_t ld_sg, int group,
+                             void* c, int c_dt, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                             mls_stream_t stream) {
+  WqArgs p{a, a_dt, lda, w, ldw, s, s_dt, ld_sn, ld_sg, group, c, ldc, M, N, K,
+           (hipStream_t)stream};
+  int rc = validate("mls_int4_gemm", 4, p, c_dt);
+  if (rc != MLS_OK) return rc;
+  return run("mls_int4_gemm", 4, p);
+}
+
+extern "C" int mls_int4_grouped_gemm(const void* a, int a_dt, int64_t lda, const int32_t* seg_off,
+                                     int E, int64_t M_total, const uint8_t* w, int64_t w_estride,
+                                     int64_t ldw, const void* s, int s_dt, int64_t s_estride,
+                                     int64_t ld_sn, int64_t ld_sg, int group, void* c, int c_dt,
+                                     int64_t ldc, int64_t N, int64_t K, mls_stream_t stream) {
+  const char* fn = "mls_int4_grouped_gemm";
+  GroupedArgs g{{a, a_dt, lda, w, ldw, s, s_dt, ld_sn, ld_sg, group, c, ldc, M_total, N, K,
+                 (hipStream_t)stream},
+                seg_off, E, w_estride, s_estride};
+  int rc = validate(fn, 4, g.base, c_dt);
+  if (rc != MLS_OK) return rc;
+  if (E < 1) return fail(MLS_ERR_ARG, "%s: E=%d < 1", fn, E);
+  if (w_estride < 0 || s_estride < 0) return fail(MLS_ERR_ARG, "%s: negative expert stride", fn);
+  if (M_total == 0 || N == 0) return MLS_OK;
+  if (!seg_off) return fail(MLS_ERR_ARG, "%s: null seg_off", fn);
+  if (a_dt != MLS_F16 && a_dt != MLS_BF16)
+    return fail(MLS_ERR_UNSUPPORTED, "%s: activations must be f16 or bf16", fn);
+  rc = launch_grouped_int4(g);
+  if (rc == MLS_ERR_UNSUPPORTED)
+    return fail(MLS_ERR_UNSUPPORTED,
+                "%s: needs K %% 64 == 0, group %% 32 == 0 and 16-byte aligned rows", fn);
+  return rc;
+}

@@ -1,0 +1,129 @@
+"""OCP e4m3 ("fn") codec and the e4m3 GEMM with inline scales.
+
+Same names and call signatures as the reference (kernels/fp8_matmul.py:34-128).
+e4m3fn: 1 sign, 4 exponent bits (bias 7), 3 mantissa bits, no infinities,
+NaN = S.1111.111, max finite 448.
+
+Unlike the reference, whose kernel decodes e4m3 to fp32 and runs an fp32 dot,
+fp8_matmul here feeds the raw e4m3 bytes to gfx950's fp8 matrix cores
+(v_mfma_f32_16x16x128_f8f6f4, fp32 accumulation) and applies the scales in the
+epilogue. Scales may be Python floats (per tensor, the reference's form) or fp32
+tensors of shape [M] / [N] (per row), or 0-d tensors.
+
+quantize_e4m3 / dequantize_e4m3 run the gfx950 codec kernels on HIP tensors. On
+host tensors (the load-time and CPU-training callers) they run the reference's
+own host op sequence, which is the definition the HIP codec is bit-exact to.
+"""
+
+from __future__ import annotations
+
+import torch
+
+import kernels
+from kernels._hip import dt_code, ld, require_hip, rows, stream
+
+E4M3_MAX = 448.0
+
+
+def decode_e4m3(bits: torch.Tensor) -> torch.Tensor:
+    """Kernel-decode a uint8 tensor of e4m3fn bit patterns to fp32; the NaN
+    patterns 0x7F / 0xFF decode to 0 (kernels/fp8_matmul.py:37-47, 93-100)."""
+    dev = require_hip("decode_e4m3", bits)
+    if bits.dtype not in (torch.uint8, torch.float8_e4m3fn):
+        raise TypeError(f"decode_e4m3: expected uint8 bits, got {bits.dtype}")
+    flat = bits.reshape(-1).contiguous().view(torch.uint8)
+    out = torch.empty(flat.shape, dtype=torch.float32, device=dev)
+    kernels.check(kernels.lib().mls_e4m3_decode(flat.data_ptr(), out.data_ptr(), flat.numel(),
+                                                stream(dev)), "decode_e4m3")
+    return out.reshape(bits.shape)
+
+
+def _row_scale(scale, rows_: int, dev, what: str, per_row_1d: bool):
+    """(scalar, pointer, stride, keepalive) for a scale that is per tensor (a float
+    or a 1-element tensor) or per row of a [rows_, cols] operand (shape [rows_, 1],
+    or [rows_] when per_row_1d). None when the scale needs general broadcasting."""
+    if not isinstance(scale, torch.Tensor):
+        return float(scale), None, 0, None
+    if scale.device != dev:
+        raise ValueError(f"{what}: scale on {scale.device}, operand on {dev}")
+    s = scale.to(torch.float32)
+    if s.numel() == 1:
+        s = s.reshape(1)
+        return 0.0, s.data_ptr(), 0, s
+    per_row = (s.dim() == 2 and tuple(s.shape) == (rows_, 1)) or \
+        (per_row_1d and s.dim() == 1 and s.shape[0] == rows_)
+    if per_row:
+        s = s.reshape(-1).contiguous()
+        return 0.0, s.data_ptr(), 1, s
+    return None
+
+
+def quantize_e4m3(x: torch.Tensor, scale) -> torch.Tensor:
+    """e4m3 bits of x / scale, saturated to ±448, round to nearest even
+    (kernels/fp8_matmul.py:103-106). Returns uint8. `scale` broadcasts as in
+    torch: a float, a 1-element tensor, [M, 1] per row of a 2-D x, or any other
+    broadcastable tensor."""
+    if x.device.type != "cuda":
+        q = (x.float() / scale).clamp(-E4M3_MAX, E4M3_MAX)
+        return q.to(torch.float8_e4m3fn).view(torch.uint8)
+    dev = x.device
+    shape = x.shape
+    xdt = dt_code(x.dtype, "quantize_e4m3")
+    x2 = rows(x.reshape(1, 1) if x.dim() == 0 else x.reshape(-1, shape[-1]))
+    sa = _row_scale(scale, x2.shape[0], dev, "quantize_e4m3", False) \
+        if x.dim() <= 2 or not isinstance(scale, torch.Tensor) or scale.numel() == 1 else None
+    if sa is None:
+        # general broadcast: IEEE division on the device (tensor / tensor is a true
+        # division in torch), then encode with scale 1 (division by 1 is exact)
+        q = x.float() / scale
+        shape = q.shape
+        x2 = rows(q.reshape(1, 1) if q.dim() == 0 else q.reshape(-1, shape[-1]))
+        xdt, sa = dt_code(torch.float32, "quantize_e4m3"), (1.0, None, 0, None)
+    out = torch.empty(x2.shape, dtype=torch.uint8, device=dev)
+    kernels.check(kernels.lib().mls_e4m3_encode(
+        x2.data_ptr(), xdt, x2.shape[0], x2.shape[1], ld(x2), sa[0], sa[1], sa[2],
+        out.data_ptr(), ld(out), stream(dev)), "quantize_e4m3")
+    return out.reshape(shape)
+
+
+def dequantize_e4m3(bits: torch.Tensor, scale) -> torch.Tensor:
+    """value(bits) * scale in fp32; the NaN patterns stay NaN, as in torch's float8
+    view (kernels/fp8_matmul.py:109-110)."""
+    if bits.device.type != "cuda":
+        return bits.view(torch.float8_e4m3fn).float() * scale
+    dev = bits.device
+    shape = bits.shape
+    u8 = bits.view(torch.uint8)
+    b2 = rows(u8.reshape(1, 1) if u8.dim() == 0 else u8.reshape(-1, shape[-1]))
+    sa = _row_scale(scale, b2.shape[0], dev, "dequantize_e4m3", False) \
+        if bits.dim() <= 2 or not isinstance(scale, torch.Tensor) or scale.numel() == 1 else None
+    if sa is None:  # general broadcast: exact decode, then one fp32 multiply on the device
+        return dequantize_e4m3(bits, 1.0) * scale
+    out = torch.empty(b2.shape, dtype=torch.float32, device=dev)
+    kernels.check(kernels.lib().mls_e4m3_dequantize(
+        b2.data_ptr(), b2.shape[0], b2.shape[1], ld(b2), sa[0], sa[1], sa[2],
+        out.data_ptr(), ld(out), stream(dev)), "dequantize_e4m3")
+    return out.reshape(shape)
+
+
+def fp8_matmul(a_bits: torch.Tensor, b_bits: torch.Tensor,
+               sa, sb, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """a_bits [M,K], b_bits [N,K] uint8 e4m3 -> sa*sb*(Â @ B̂ᵀ) [M,N]
+    (kernels/fp8_matmul.py:113-128). sa / sb: float, 0-d tensor, or fp32 [M] / [N]."""
+    dev = require_hip("fp8_matmul", a_bits, b_bits)
+    M, K = a_bits.shape
+    N = b_bits.shape[0]
+    if b_bits.shape[1] != K:
+        raise ValueError(f"fp8_matmul: K mismatch {tuple(a_bits.shape)} vs {tuple(b_bits.shape)}")
+    cdt = dt_code(out_dtype, "fp8_matmul out_dtype")
+    a2, b2 = rows(a_bits.view(torch.uint8)), rows(b_bits.view(torch.uint8))
+    sa_args = _row_scale(sa, M, dev, "fp8_matmul sa", True)
+    sb_args = _row_scale(sb, N, dev, "fp8_matmul sb", True)
+    if sa_args is None or sb_args is None:
+        raise ValueError("fp8_matmul: scales must be floats, 0-d tensors or per-row [M] / [N]")
+    c = torch.empty(M, N, dtype=out_dtype, device=dev)
+    kernels.check(kernels.lib().mls_fp8_gemm(
+        a2.data_ptr(), ld(a2), b2.data_ptr(), ld(b2),
+        sa_args[0], sa_args[1], sa_args[2], sb_args[0], sb_args[1], sb_args[2],
+        c.data_ptr(), cdt, ld(c), M, N, K, stream(dev)), "fp8_matmul")
+    return c

@@ -1,0 +1,61 @@
+"""INT4 weight-only GEMM over expert-sorted token segments, one launch for all experts.
+
+The reference runs a quantized MoE layer as a Python loop over experts, one
+int4_matmul per non-empty expert segment after a host sync on the counts
+(kernels/moe_routing.py:145-151 through QuantLinear, serve/quantize.py:110-114).
+Here the segment offsets stay on the device and a single gfx950 MFMA launch
+covers every (expert, row tile, column tile); each workgroup finds its expert
+from the offsets. Weights of all experts are stacked: packed [E, N, K/2] and
+scales [E, N, K/group] in the INT4 layout of kernels.dequant_matmul.
+"""
+
+from __future__ import annotations
+
+import torch
+
+import kernels
+from kernels._hip import dt_code, ld, require_hip, rows, stream
+
+
+def segment_offsets(counts: torch.Tensor) -> torch.Tensor:
+    """int32 [E+1] exclusive prefix sum of per-expert row counts (on the device)."""
+    off = torch.zeros(counts.numel() + 1, dtype=torch.int32, device=counts.device)
+    off[1:] = torch.cumsum(counts.reshape(-1).to(torch.int64), 0).to(torch.int32)
+    return off
+
+
+def int4_grouped_matmul(a_sorted: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor,
+                        counts_or_offsets: torch.Tensor, group_size: int) -> torch.Tensor:
+    """out[r] = a_sorted[r] @ dequant(w_packed[e], scale[e], group_size).T for every row r
+    of expert e's segment. counts_or_offsets: per-expert counts [E] or offsets [E+1]
+    (int, on the device). a_sorted [M_total, K] bf16/fp16 -> out [M_total, N] same dtype."""
+    dev = require_hip("int4_grouped_matmul", a_sorted, w_packed, scale, counts_or_offsets)
+    if w_packed.dim() != 3 or w_packed.dtype != torch.uint8:
+        raise ValueError(f"int4_grouped_matmul: w_packed must be uint8 [E, N, K/2], got "
+                         f"{w_packed.dtype} {tuple(w_packed.shape)}")
+    E, N, Kh = w_packed.shape
+    M, K = a_sorted.shape
+    assert K % group_size == 0 and K == Kh * 2
+    G = K // group_size
+    if tuple(scale.shape) != (E, N, G):
+        raise ValueError(f"int4_grouped_matmul: scale shape {tuple(scale.shape)}, expected {(E, N, G)}")
+    if counts_or_offsets.numel() == E:
+        off = segment_offsets(counts_or_offsets)
+    elif counts_or_offsets.numel() == E + 1:
+        off = counts_or_offsets.reshape(-1).to(torch.int32).contiguous()
+    else:
+        raise ValueError(f"int4_grouped_matmul: expected {E} counts or {E + 1} offsets, "
+                         f"got {counts_or_offsets.numel()}")
+    adt = dt_code(a_sorted.dtype, "int4_grouped_matmul")
+    a = rows(a_sorted)
+    w = w_packed if w_packed.is_contiguous() else w_packed.contiguous()
+    if scale.dtype not in (torch.float32, torch.float16):
+        scale = scale.to(torch.float32)
+    s = scale if scale.is_contiguous() else scale.contiguous()
+    sdt = dt_code(s.dtype, "int4_grouped_matmul scale")
+    c = torch.empty(M, N, dtype=a.dtype, device=dev)
+    kernels.check(kernels.lib().mls_int4_grouped_gemm(
+        a.data_ptr(), adt, ld(a), off.data_ptr(), E, M,
+        w.data_ptr(), N * Kh, Kh, s.data_ptr(), sdt, N * G, G, 1, group_size,
+        c.data_ptr(), adt, ld(c), N, K, stream(dev)), "int4_grouped_matmul")
+    return c

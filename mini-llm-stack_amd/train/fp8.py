@@ -1,0 +1,106 @@
+"""FP8 (e4m3) linear with per-tensor delayed scaling, on the gfx950 fp8 GEMM.
+
+Same classes and behaviour as the reference's train/fp8.py (:33-131): the
+forward quantizes x and W to e4m3 with delayed per-tensor scales and, when
+use_kernel is set, multiplies them with kernels.fp8_matmul (native fp8 MFMA);
+otherwise it multiplies the decoded operands in fp32. The backward re-quantizes
+dy to e5m2 (just-in-time scale) and computes both gradients against the same
+fp8 operands the forward used, in fp32.
+"""
+
+from __future__ import annotations
+
+from collections import deque
+
+import torch
+import torch.nn as nn
+
+from kernels.fp8_matmul import E4M3_MAX, dequantize_e4m3, fp8_matmul, quantize_e4m3
+
+E5M2_MAX = 57344.0
+
+
+class DynamicScaler:
+    """Per-tensor delayed scaling: scale_t = max(amax history) / fp8_max."""
+
+    def __init__(self, fp8_max: float = E4M3_MAX, history: int = 16, enabled: bool = True):
+        self.fp8_max = fp8_max
+        self.hist: deque = deque(maxlen=history)
+        self.enabled = enabled
+
+    def scale_for(self, t: torch.Tensor) -> float:
+        if not self.enabled:
+            return 1.0
+        amax = float(t.detach().abs().amax())
+        if not self.hist:  # first call: just-in-time amax
+            self.hist.append(max(amax, 1e-12))
+        s = max(self.hist) / self.fp8_max
+        self.hist.append(max(amax, 1e-12))
+        return max(s, 1e-12)
+
+
+def _quant_e5m2(x: torch.Tensor, scale: float) -> torch.Tensor:
+    q = (x.float() / scale).clamp(-E5M2_MAX, E5M2_MAX)
+    return q.to(torch.float8_e5m2).view(torch.uint8)
+
+
+def _dequant_e5m2(bits: torch.Tensor, scale: float) -> torch.Tensor:
+    return bits.view(torch.float8_e5m2).float() * scale
+
+
+class _FP8LinearFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, sx, sw, use_kernel, scale_grads):
+        xb = quantize_e4m3(x, sx)
+        wb = quantize_e4m3(w, sw)
+        ctx.save_for_backward(xb, wb)
+        ctx.scales = (sx, sw)
+        ctx.scale_grads = scale_grads
+        if use_kernel:
+            return fp8_matmul(xb, wb, sx, sw)
+        return dequantize_e4m3(xb, sx) @ dequantize_e4m3(wb, sw).t()
+
+    @staticmethod
+    def backward(ctx, dy):
+        xb, wb = ctx.saved_tensors
+        sx, sw = ctx.scales
+        if ctx.scale_grads:
+            sdy = max(float(dy.detach().abs().amax()) / E5M2_MAX, 1e-12)
+        else:
+            sdy = 1.0
+        dyh = _dequant_e5m2(_quant_e5m2(dy, sdy), sdy)
+        xh = dequantize_e4m3(xb, sx)
+        wh = dequantize_e4m3(wb, sw)
+        return dyh @ wh, dyh.t() @ xh, None, None, None, None
+
+
+class FP8Linear(nn.Module):
+    def __init__(self, linear: nn.Linear, enabled: bool = True, use_kernel: bool = False):
+        super().__init__()
+        self.weight = nn.Parameter(linear.weight.detach().clone())
+        self.sx = DynamicScaler(enabled=enabled)
+        self.sw = DynamicScaler(enabled=enabled)
+        self.use_kernel = use_kernel
+
+    def forward(self, x):
+        shape = x.shape
+        flat = x.reshape(-1, shape[-1])
+        y = _FP8LinearFn.apply(flat, self.weight, self.sx.scale_for(flat),
+                               self.sw.scale_for(self.weight), self.use_kernel,
+                               self.sx.enabled)
+        return y.reshape(*shape[:-1], -1)
+
+
+def convert_linears_to_fp8(model: nn.Module, enabled: bool = True,
+                           use_kernel: bool = False) -> nn.Module:
+    """Swap every attention (wq/wk/wv/wo) and MLP (w_gate/w_up/w_down) linear for
+    FP8Linear; embeddings, head and norms stay fp32 (train/fp8.py:117-131). Modules
+    are recognised by their slot names rather than by class."""
+    import copy
+    model = copy.deepcopy(model)
+    for m in model.modules():
+        for names in (("wq", "wk", "wv", "wo"), ("w_gate", "w_up", "w_down")):
+            if all(isinstance(getattr(m, n, None), nn.Linear) for n in names):
+                for n in names:
+                    setattr(m, n, FP8Linear(getattr(m, n), enabled, use_kernel))
+    return model

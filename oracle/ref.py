@@ -1,0 +1,232 @@
+"""CPU oracle for the quantized-linear path — TEST INFRASTRUCTURE, NOT PRODUCT CODE.
+
+A numpy restatement of the reference's arithmetic for this path, used only by
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg as the checker
+(and, for the baseline, as the reference's CPU algorithm being timed). The
+product (mini-llm-stack_amd/) never imports it.
+
+Each function cites the reference code it restates. Pins (see tests/test_oracle.py):
+  e4m3_decode      256-byte known-answer table of torch's float8_e4m3fn view
+                   (test_fp8.py:16-26 of the reference) + golden fixture.
+  e4m3_encode      torch's float8_e4m3fn cast on every rounding boundary, the
+                   special values and random samples (golden fixture and live).
+                   Implemented by nearest-value search over the 126 finite
+                   magnitudes, not by bit manipulation, so that it is an
+                   independent derivation from the HIP encoder.
+  quantize_int8/4  torch op sequences of serve/quantize.py (golden fixtures),
+                   round-trip bound |w - dq| <= s/2 (test_quantize.py:16-28),
+                   all-zero rows/groups, exact ties.
+  dequantize_*     closed form; brute-force per-element loop on tiny inputs.
+  *_matmul         fp64 brute-force triple loop on tiny inputs; golden fixture
+                   of config A produced by torch's fp32 matmul.
+  route / sort     torch softmax/topk/argsort golden fixture.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+E4M3_MAX = 448.0
+
+# ------------------------------------------------------------------ e4m3 (OCP "fn")
+
+
+def _e4m3_table() -> np.ndarray:
+    """Value of every byte: 1 sign, 4 exponent bits (bias 7), 3 mantissa bits;
+    exponent 0 is subnormal (m/8 * 2^-6); S.1111.111 is NaN; no infinities
+    (kernels/fp8_matmul.py:20-21, 37-47)."""
+    vals = np.empty(256, dtype=np.float64)
+    for b in range(256):
+        s = -1.0 if b & 0x80 else 1.0
+        e = (b >> 3) & 0xF
+        m = b & 0x7
+        if e == 15 and m == 7:
+            vals[b] = np.nan
+        elif e == 0:
+            vals[b] = s * (m / 8.0) * 2.0 ** -6
+        else:
+            vals[b] = s * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return vals
+
+
+E4M3_TABLE = _e4m3_table()
+_POS_CODES = np.arange(0, 127)                 # 0x00 .. 0x7E: finite non-negative values
+_POS_VALUES = E4M3_TABLE[_POS_CODES]           # strictly increasing
+
+
+def e4m3_decode(bits: np.ndarray, nan_to_zero: bool = True) -> np.ndarray:
+    """fp32 values of e4m3 bytes. nan_to_zero follows the reference kernel's decode
+    (kernels/fp8_matmul.py:46: the NaN patterns decode to a signed 0); False follows
+    torch's float8 view (NaN stays NaN, kernels/fp8_matmul.py:110)."""
+    bits = np.asarray(bits, dtype=np.uint8)
+    v = E4M3_TABLE[bits]
+    if nan_to_zero:
+        nan = np.isnan(v)
+        v = np.where(nan, np.where(bits & 0x80, -0.0, 0.0), v)
+    return v.astype(np.float32)
+
+
+def e4m3_encode(q: np.ndarray) -> np.ndarray:
+    """e4m3 code of q (already divided by the scale): clamp to [-448, 448]
+    (kernels/fp8_matmul.py:105), then the nearest representable value, ties to the
+    even code (torch's float8_e4m3fn cast, :106). NaN -> 0x7F with q's sign bit."""
+    q = np.asarray(q, dtype=np.float32)
+    sign = (q.view(np.uint32) >> 31).astype(np.uint8) << 7
+    a = np.minimum(np.abs(q.astype(np.float64)), E4M3_MAX)
+    hi = np.searchsorted(_POS_VALUES, a, side="left")          # first value >= a
+    hi = np.minimum(hi, len(_POS_VALUES) - 1)
+    lo = np.maximum(hi - 1, 0)
+    d_lo = a - _POS_VALUES[lo]
+    d_hi = _POS_VALUES[hi] - a
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & (_POS_CODES[hi] % 2 == 0))
+    code = np.where(pick_hi, _POS_CODES[hi], _POS_CODES[lo]).astype(np.uint8)
+    code = np.where(np.isnan(q), np.uint8(0x7F), code)
+    return (code | sign).astype(np.uint8)
+
+
+def quantize_e4m3(x: np.ndarray, scale) -> np.ndarray:
+    """kernels/fp8_matmul.py:103-106 with IEEE fp32 division by float32(scale)
+    (scale: a float or an array broadcastable against x)."""
+    q = np.asarray(x, dtype=np.float32) / np.asarray(scale, dtype=np.float32)
+    return e4m3_encode(q.astype(np.float32))
+
+
+def dequantize_e4m3(bits: np.ndarray, scale) -> np.ndarray:
+    """kernels/fp8_matmul.py:109-110: exact value times the scale, one fp32 rounding."""
+    return (e4m3_decode(bits, nan_to_zero=False) * np.asarray(scale, dtype=np.float32)).astype(
+        np.float32)
+
+
+# ------------------------------------------------------------------ INT8 / INT4 weights
+
+
+def quantize_int8(w: np.ndarray):
+    """serve/quantize.py:18-21."""
+    w = np.asarray(w, dtype=np.float32)
+    scale = np.maximum(np.abs(w).max(axis=1) / np.float32(127.0), np.float32(1e-8))
+    q = np.clip(np.rint(w / scale[:, None]), -127, 127).astype(np.int8)
+    return q, scale.astype(np.float32)
+
+
+def dequantize_int8(w_q: np.ndarray, scale: np.ndarray) -> np.ndarray:
+    """serve/quantize.py:24-25."""
+    return (w_q.astype(np.float32) * np.asarray(scale, dtype=np.float32)[:, None]).astype(np.float32)
+
+
+def quantize_int4(w: np.ndarray, group_size: int = 32):
+    """serve/quantize.py:28-36: unsigned nibbles with offset 8, even k in the low nibble."""
+    w = np.asarray(w, dtype=np.float32)
+    N, K = w.shape
+    assert K % group_size == 0
+    g = w.reshape(N, K // group_size, group_size)
+    scale = np.maximum(np.abs(g).max(axis=2) / np.float32(7.0), np.float32(1e-8)).astype(np.float32)
+    q = np.clip(np.rint(g / scale[:, :, None]), -8, 7) + 8
+    q = q.reshape(N, K).astype(np.uint8)
+    packed = (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+    return packed, scale
+
+
+def unpack_int4(packed: np.ndarray) -> np.ndarray:
+    """Stored nibbles (0..15) [N, K] of packed [N, K/2]."""
+    packed = np.asarray(packed, dtype=np.uint8)
+    N, H = packed.shape
+    q = np.empty((N, 2 * H), dtype=np.uint8)
+    q[:, 0::2] = packed & 0x0F
+    q[:, 1::2] = packed >> 4
+    return q
+
+
+def dequantize_int4(packed: np.ndarray, scale: np.ndarray, group_size: int) -> np.ndarray:
+    """serve/quantize.py:39-47."""
+    q = unpack_int4(packed).astype(np.float32) - np.float32(8.0)
+    N, K = q.shape
+    s = np.asarray(scale, dtype=np.float32)
+    return (q.reshape(N, K // group_size, group_size) * s[:, :, None]).reshape(N, K).astype(np.float32)
+
+
+# ------------------------------------------------------------------ GEMMs (dequantize, fp32 matmul)
+
+
+def _f32(x) -> np.ndarray:
+    return np.asarray(x, dtype=np.float32)
+
+
+def int8_matmul(a, w_q, scale) -> np.ndarray:
+    """a @ dequantize_int8(w_q, s).T in fp32 (test_quantize.py:37; dequant_matmul.py:140-152)."""
+    return (_f32(a) @ dequantize_int8(w_q, scale).T).astype(np.float32)
+
+
+def int4_matmul(a, packed, scale, group_size) -> np.ndarray:
+    """a @ dequantize_int4(...).T in fp32 (test_quantize.py:48; dequant_matmul.py:170-185)."""
+    return (_f32(a) @ dequantize_int4(packed, scale, group_size).T).astype(np.float32)
+
+
+def int8_dgrad(dy, w_q, scale) -> np.ndarray:
+    """(dy * s) @ w_q in fp32 (kaggle/gpu_smoke.py:133-135; dequant_matmul.py:103-132)."""
+    return ((_f32(dy) * _f32(scale)[None, :]) @ np.asarray(w_q).astype(np.float32)).astype(np.float32)
+
+
+def fp8_matmul(a_bits, b_bits, sa, sb) -> np.ndarray:
+    """(decode(A) @ decode(B).T) * (sa * sb), decode with NaN -> 0
+    (kernels/fp8_matmul.py:50-81). sa / sb: floats or per-row arrays [M] / [N]."""
+    acc = e4m3_decode(a_bits) @ e4m3_decode(b_bits).T
+    sa = np.asarray(sa, dtype=np.float32).reshape(-1, 1) if np.ndim(sa) else np.float32(sa)
+    sb = np.asarray(sb, dtype=np.float32).reshape(1, -1) if np.ndim(sb) else np.float32(sb)
+    return (acc * (sa * sb)).astype(np.float32)
+
+
+def grouped_int4_matmul(a_sorted, packed, scale, offsets, group_size) -> np.ndarray:
+    """Per-expert segment loop of kernels/moe_routing.py:145-151 with int4 experts:
+    rows offsets[e]:offsets[e+1] times expert e's dequantized weights."""
+    a = _f32(a_sorted)
+    E, N, _ = packed.shape
+    out = np.zeros((a.shape[0], N), dtype=np.float32)
+    for e in range(E):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi > lo:
+            out[lo:hi] = a[lo:hi] @ dequantize_int4(packed[e], scale[e], group_size).T
+    return out
+
+
+# ------------------------------------------------------------------ routing harness
+
+
+def route_topk(logits: np.ndarray, k: int):
+    """train/model.py:158-162: softmax in fp32, top-k (largest first, lower index on
+    ties), renormalised weights."""
+    x = np.asarray(logits, dtype=np.float32)
+    x = x - x.max(axis=-1, keepdims=True)
+    p = np.exp(x)
+    p = p / p.sum(axis=-1, keepdims=True)
+    order = np.argsort(-p, axis=-1, kind="stable")[:, :k]
+    w = np.take_along_axis(p, order, axis=-1)
+    return (w / w.sum(axis=-1, keepdims=True)).astype(np.float32), order.astype(np.int64)
+
+
+def sort_by_expert(experts_idx: np.ndarray, n_experts: int):
+    """kernels/moe_routing.py:116-130: (token_of_slot, counts, pos)."""
+    T, k = experts_idx.shape
+    flat = experts_idx.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    counts = np.bincount(flat, minlength=n_experts)
+    pos = np.empty_like(order)
+    pos[order] = np.arange(T * k)
+    return order // k, counts, pos.reshape(T, k)
+
+
+# ------------------------------------------------------------------ tolerances (BASELINE)
+
+
+def close_bf16(out: np.ndarray, ref: np.ndarray) -> tuple[bool, float]:
+    """|out - ref| <= 1e-2 + 1e-2 |ref| (rtol = atol = 1e-2 for bf16 outputs)."""
+    err = np.abs(_f32(out) - _f32(ref)) - (1e-2 + 1e-2 * np.abs(_f32(ref)))
+    return bool((err <= 0).all()), float(err.max()) if err.size else 0.0
+
+
+def close_fp32(out: np.ndarray, ref: np.ndarray) -> tuple[bool, float]:
+    """2 fp16 ULP-equivalent relative error: |out - ref| <= 2^-9 max(|ref|, rms(ref))."""
+    out, ref = _f32(out), _f32(ref)
+    rms = float(np.sqrt(np.mean(ref.astype(np.float64) ** 2))) if ref.size else 0.0
+    bound = 2.0 ** -9 * np.maximum(np.abs(ref), rms)
+    ratio = np.abs(out - ref) / np.maximum(bound, 1e-30)
+    return bool((np.abs(out - ref) <= bound).all()), float(ratio.max()) if ratio.size else 0.0

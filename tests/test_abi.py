@@ -1,0 +1,105 @@
+"""The C-ABI library: it loads, exports every symbol include/mls.h declares, and
+rejects invalid arguments on the host before any HIP call (these calls pass null
+device pointers, so they never reach the GPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+import pytest
+
+from conftest import ROOT
+
+import kernels
+
+HEADER = ROOT / "include" / "mls.h"
+NULL = None
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    return re.findall(r"^\s*(?:int|const char\*)\s+(mls_\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_the_boundary():
+    syms = declared_symbols()
+    assert len(syms) == len(set(syms)) == 12
+    assert set(syms) == set(kernels.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(kernels.LIB_PATH))
+    for s in declared_symbols():
+        assert hasattr(lib, s), s
+
+
+def test_abi_version_and_error_string():
+    lib = kernels.load_library()
+    assert lib.mls_abi_version() == kernels.ABI_VERSION == 1
+    assert isinstance(lib.mls_last_error(), bytes)
+
+
+def _err(rc):
+    return rc, kernels.lib().mls_last_error().decode()
+
+
+@pytest.mark.parametrize("bad", ["neg_m", "null", "dtype", "out_dtype", "scale_dtype", "lda"])
+def test_int8_gemm_rejects(bad):
+    L = kernels.load_library()
+    a = dict(a=1, adt=kernels.MLS_BF16, lda=64, w=1, ldw=64, s=1, sdt=kernels.MLS_F32, c=1,
+             cdt=kernels.MLS_BF16, ldc=32, M=4, N=32, K=64)
+    if bad == "neg_m":
+        a["M"] = -1
+    elif bad == "null":
+        a["a"] = NULL
+    elif bad == "dtype":
+        a["adt"] = a["cdt"] = 7
+    elif bad == "out_dtype":
+        a["cdt"] = kernels.MLS_F32
+    elif bad == "scale_dtype":
+        a["sdt"] = kernels.MLS_BF16
+    elif bad == "lda":
+        a["lda"] = 10
+    rc, msg = _err(L.mls_int8_gemm(a["a"], a["adt"], a["lda"], a["w"], a["ldw"], a["s"], a["sdt"],
+                                   a["c"], a["cdt"], a["ldc"], a["M"], a["N"], a["K"], NULL))
+    assert rc == kernels.MLS_ERR_ARG and "mls_int8_gemm" in msg
+
+
+def test_int4_gemm_rejects_group_mismatch():
+    L = kernels.load_library()
+    rc, msg = _err(L.mls_int4_gemm(1, kernels.MLS_F32, 96, 1, 48, 1, kernels.MLS_F32, 3, 1, 64,
+                                   1, kernels.MLS_F32, 8, 2, 8, 96, NULL))
+    assert rc == kernels.MLS_ERR_ARG and "group" in msg
+    rc, _ = _err(L.mls_int4_gemm(1, kernels.MLS_F32, 96, 1, 48, 1, kernels.MLS_F32, 3, 1, 0,
+                                 1, kernels.MLS_F32, 8, 2, 8, 96, NULL))
+    assert rc == kernels.MLS_ERR_ARG
+
+
+def test_zero_sized_calls_are_noops():
+    L = kernels.load_library()
+    assert L.mls_int8_gemm(NULL, 0, 0, NULL, 0, NULL, 0, NULL, 0, 0, 0, 5, 5, NULL) == 0
+    assert L.mls_e4m3_decode(NULL, NULL, 0, NULL) == 0
+    assert L.mls_fp8_gemm(NULL, 0, NULL, 0, 1.0, NULL, 0, 1.0, NULL, 0, NULL, 0, 0, 0, 0, 8, NULL) == 0
+
+
+def test_fp8_and_codec_reject():
+    L = kernels.load_library()
+    assert L.mls_fp8_gemm(1, 64, 1, 64, 1.0, NULL, 0, 1.0, NULL, 0, 1, 9, 8, 4, 8, 64, NULL) == \
+        kernels.MLS_ERR_ARG
+    assert L.mls_fp8_gemm(1, 32, 1, 64, 1.0, NULL, 0, 1.0, NULL, 0, 1, 0, 8, 4, 8, 64, NULL) == \
+        kernels.MLS_ERR_ARG
+    assert L.mls_e4m3_decode(1, 1, -3, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_e4m3_encode(1, 5, 2, 2, 2, 1.0, NULL, 0, 1, 2, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_quantize_int4(1, 4, 30, 30, 4, 1, 15, 1, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_int8_dgrad(1, 0, 8, 1, 8, 1, 0, 1, 1, 8, 2, 8, 8, NULL) == kernels.MLS_ERR_ARG
+
+
+def test_grouped_rejects():
+    L = kernels.load_library()
+    # E = 0
+    assert L.mls_int4_grouped_gemm(1, kernels.MLS_BF16, 64, 1, 0, 8, 1, 0, 32, 1, 0, 0, 2, 1, 32,
+                                   1, kernels.MLS_BF16, 16, 16, 64, NULL) == kernels.MLS_ERR_ARG
+    # fp32 activations are outside the grouped kernel
+    assert L.mls_int4_grouped_gemm(1, kernels.MLS_F32, 64, 1, 2, 8, 1, 0, 32, 1, 0, 0, 2, 1, 32,
+                                   1, kernels.MLS_F32, 16, 16, 64, NULL) == kernels.MLS_ERR_UNSUPPORTED

@@ -1,0 +1,199 @@
+"""gfx950 INT8 / INT4 weight-only GEMMs vs the dequantize-then-fp32-matmul oracle.
+
+Tolerances (BASELINE): fp32 outputs |Δ| <= 2^-9 max(|ref|, rms(ref)); bf16 and fp16
+outputs rtol = atol = 1e-2. Full-size configs compare every output against torch's
+fp32 matmul of the dequantized weights on the GPU (a floating-point reference of
+the same op, TF32 off) and sampled rows against the CPU oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from oracle import ref
+
+from kernels.dequant_matmul import int4_matmul, int8_dgrad, int8_matmul
+from serve.quantize import quantize_int4, quantize_int8
+
+pytestmark = pytest.mark.gpu
+
+torch.backends.cuda.matmul.allow_tf32 = False
+
+
+def _check(out: torch.Tensor, want: np.ndarray, what: str):
+    o = out.float().cpu().numpy()
+    if out.dtype == torch.float32:
+        ok, worst = ref.close_fp32(o, want)
+    else:
+        ok, worst = ref.close_bf16(o, want)
+    assert ok, f"{what}: worst {worst:.3g} (max |Δ| {np.abs(o - want).max():.3g})"
+
+
+def _data(M, N, K, seed, wscale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(M, K, generator=g), torch.randn(N, K, generator=g) * wscale
+
+
+# --------------------------------------------------------------- reference test shapes (fp32)
+
+@pytest.mark.parametrize("M,N,K", [(4, 32, 48), (17, 33, 64), (1, 64, 32), (33, 256, 512)])
+def test_int8_reference_shapes(dev, M, N, K):
+    a, w = _data(M, N, K, M * 1000 + N)
+    q, s = quantize_int8(w)
+    out = int8_matmul(a.to(dev), q.to(dev), s.to(dev))
+    assert out.dtype == torch.float32 and out.shape == (M, N)
+    _check(out, ref.int8_matmul(a.numpy(), q.numpy(), s.numpy()), "int8")
+
+
+@pytest.mark.parametrize("M,N,K,gs", [(4, 32, 64, 16), (9, 33, 32, 16), (1, 16, 64, 32),
+                                      (33, 256, 512, 64), (3, 40, 512, 128)])
+def test_int4_reference_shapes(dev, M, N, K, gs):
+    a, w = _data(M, N, K, M * 1000 + N + gs)
+    p, s = quantize_int4(w, gs)
+    out = int4_matmul(a.to(dev), p.to(dev), s.to(dev), gs)
+    _check(out, ref.int4_matmul(a.numpy(), p.numpy(), s.numpy(), gs), "int4")
+
+
+def test_int4_golden_fixture(dev):
+    d = golden("gemm_int4_small")
+    for t in ("t1", "t2", "t3", "g128"):
+        gs = int(d[f"{t}_gs"])
+        out = int4_matmul(torch.from_numpy(d[f"{t}_a"]).to(dev), torch.from_numpy(d[f"{t}_packed"]).to(dev),
+                          torch.from_numpy(d[f"{t}_scale"]).to(dev), gs)
+        _check(out, d[f"{t}_y"], t)
+
+
+def test_config_a_golden(dev):
+    """INT8, x fp32 [8, 512], W [2048, 512], seed 0."""
+    d = golden("gemm_int8_config_a")
+    out = int8_matmul(torch.from_numpy(d["x"]).to(dev), torch.from_numpy(d["w_q"]).to(dev),
+                      torch.from_numpy(d["scale"]).to(dev))
+    _check(out, d["y"], "config A")
+
+
+# --------------------------------------------------------------- decode configs (bf16)
+
+def _int4_setup(dev, M, N, K, gs, seed, dtype=torch.bfloat16):
+    a, w = _data(M, N, K, seed, 0.02)
+    p, s = quantize_int4(w.to(dev), gs)
+    s16 = s.to(torch.float16)
+    ab = a.to(dtype)
+    want = ref.int4_matmul(ab.float().numpy(), p.cpu().numpy(), s16.float().cpu().numpy(), gs)
+    return ab.to(dev), p, s16, want
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 16])
+def test_config_b_int4_gemv(dev, M):
+    """INT4 g128, K = N = 4096, bf16 x, fp16 scales, M in {1, 4, 16}."""
+    a, p, s, want = _int4_setup(dev, M, 4096, 4096, 128, 100 + M)
+    out = int4_matmul(a, p, s, 128)
+    assert out.dtype == torch.bfloat16
+    _check(out, want, f"config B M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_int8_gemv_target(dev, M):
+    """North-star INT8 GEMV: M=1, K = N = 4096, bf16 x, fp16 per-row scales."""
+    a, w = _data(M, 4096, 4096, 200 + M, 0.02)
+    q, s = quantize_int8(w.to(dev))
+    s16 = s.to(torch.float16)
+    ab = a.to(torch.bfloat16)
+    out = int8_matmul(ab.to(dev), q, s16)
+    _check(out, ref.int8_matmul(ab.float().numpy(), q.cpu().numpy(), s16.float().cpu().numpy()),
+           f"int8 gemv M={M}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_gemv_other_dtypes(dev, dtype, M):
+    a, p, s, want = _int4_setup(dev, M, 1024, 2048, 64, 300 + M, dtype)
+    _check(int4_matmul(a, p, s, 64), want, f"int4 {dtype} M={M}")
+    a2, w = _data(M, 768, 1536, 400 + M, 0.02)
+    q, s8 = quantize_int8(w.to(dev))
+    a2 = a2.to(dtype)
+    _check(int8_matmul(a2.to(dev), q, s8),
+           ref.int8_matmul(a2.float().numpy(), q.cpu().numpy(), s8.cpu().numpy()), f"int8 {dtype} M={M}")
+
+
+def test_gemv_long_k(dev):
+    """K = 11008 (the down-projection's input): chunks do not divide evenly across lanes."""
+    a, p, s, want = _int4_setup(dev, 1, 4096, 11008, 128, 7)
+    _check(int4_matmul(a, p, s, 128), want, "int4 K=11008")
+    a2, w = _data(2, 512, 11008, 8, 0.02)
+    q, s8 = quantize_int8(w.to(dev))
+    a2 = a2.to(torch.bfloat16)
+    _check(int8_matmul(a2.to(dev), q, s8),
+           ref.int8_matmul(a2.float().numpy(), q.cpu().numpy(), s8.cpu().numpy()), "int8 K=11008")
+
+
+# --------------------------------------------------------------- prefill (MFMA) path
+
+@pytest.mark.parametrize("M,N,K", [(17, 256, 256), (64, 512, 512), (100, 300, 320),
+                                   (256, 1024, 1024), (513, 768, 640)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mfma_int8(dev, M, N, K, dtype):
+    a, w = _data(M, N, K, M + N + K, 0.02)
+    q, s = quantize_int8(w.to(dev))
+    a = a.to(dtype)
+    out = int8_matmul(a.to(dev), q, s)
+    _check(out, ref.int8_matmul(a.float().numpy(), q.cpu().numpy(), s.cpu().numpy()), f"int8 {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K,gs", [(17, 256, 256, 128), (64, 512, 512, 32), (100, 300, 320, 64),
+                                      (256, 1024, 1024, 128), (513, 768, 640, 128)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mfma_int4(dev, M, N, K, gs, dtype):
+    a, p, s, want = _int4_setup(dev, M, N, K, gs, M + N + K + gs, dtype)
+    _check(int4_matmul(a, p, s, gs), want, f"int4 {M}x{N}x{K} g{gs}")
+
+
+def test_config_c_int8_prefill(dev):
+    """INT8, x bf16 [2048, 4096], W [11008, 4096], fp16 scales, bf16 out."""
+    M, N, K = 2048, 11008, 4096
+    g = torch.Generator(device=dev).manual_seed(0)
+    a = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    w = torch.randn(N, K, generator=g, device=dev) * 0.02
+    q, s = quantize_int8(w)
+    s16 = s.to(torch.float16)
+    del w
+    out = int8_matmul(a, q, s16)
+    wd = q.float() * s16.float()[:, None]
+    want = a.float() @ wd.t().contiguous()
+    o = out.float()
+    err = (o - want).abs() - (1e-2 + 1e-2 * want.abs())
+    assert float(err.max()) <= 0, f"config C worst excess {float(err.max()):.3g}"
+    rows = [0, 1, 777, 2047]
+    _check(out[rows], ref.int8_matmul(a[rows].float().cpu().numpy(), q.cpu().numpy(),
+                                      s16.float().cpu().numpy()), "config C rows")
+
+
+def test_strided_activation(dev):
+    a, w = _data(40, 256, 512, 5, 0.02)
+    q, s = quantize_int8(w.to(dev))
+    big = torch.zeros(40, 1024, dtype=torch.bfloat16, device=dev)
+    big[:, 256:768] = a.to(torch.bfloat16).to(dev)
+    view = big[:, 256:768]                         # row stride 1024
+    out = int8_matmul(view, q, s)
+    _check(out, ref.int8_matmul(a.bfloat16().float().numpy(), q.cpu().numpy(), s.cpu().numpy()), "strided")
+
+
+def test_empty_m(dev):
+    q, s = quantize_int8(torch.randn(16, 64, device=dev))
+    out = int8_matmul(torch.zeros(0, 64, device=dev), q, s)
+    assert out.shape == (0, 16)
+
+
+# --------------------------------------------------------------- INT8 dgrad
+
+@pytest.mark.parametrize("M,N,K", [(9, 24, 32), (33, 256, 512), (130, 300, 70)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_int8_dgrad(dev, M, N, K, dtype):
+    g = torch.Generator().manual_seed(M + N)
+    dy = torch.randn(M, N, generator=g).to(dtype)
+    q, s = quantize_int8(torch.randn(N, K, generator=g))
+    out = int8_dgrad(dy.to(dev), q.to(dev), s.to(dev))
+    assert out.dtype == dtype and out.shape == (M, K)
+    _check(out, ref.int8_dgrad(dy.float().numpy(), q.numpy(), s.numpy()), f"dgrad {M}x{N}x{K}")

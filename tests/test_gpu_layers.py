@@ -1,0 +1,105 @@
+"""The drop-in layers on the GPU: QuantLinear, quantize_model, the INT8 STE and
+FP8Linear use the gfx950 kernels and agree with their reference paths."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn as nn
+
+from oracle import ref
+
+from kernels.autograd_ops import Int8MatmulSTE
+from serve.quantize import QuantLinear, dequantize_int8, quantize_int8, quantize_model
+
+pytestmark = pytest.mark.gpu
+
+torch.backends.cuda.matmul.allow_tf32 = False
+
+
+def _close(out, want, what):
+    o, w = out.float().cpu().numpy(), want.float().cpu().numpy()
+    ok, worst = ref.close_fp32(o, w) if out.dtype == torch.float32 else ref.close_bf16(o, w)
+    assert ok, f"{what}: worst {worst:.3g}"
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M", [1, 5, 8, 64, 300])   # draft, verify (gamma+1), batch, prompt
+def test_quantlinear_kernel_vs_reference_path(dev, bits, dtype, M):
+    torch.manual_seed(M + bits)
+    lin = nn.Linear(512, 384, bias=False)
+    qk = QuantLinear(lin, bits=bits, group_size=128, use_kernel=True).to(dev)
+    qr = QuantLinear(lin, bits=bits, group_size=128, use_kernel=False).to(dev)
+    x = torch.randn(M, 512, device=dev)
+    # the reference path rounds dequantized weights to x.dtype; compare against fp32 math
+    want = x.to(dtype).float() @ qr.dequant().t()
+    _close(qk(x.to(dtype)), want, f"QuantLinear bits={bits} {dtype} M={M}")
+
+
+def test_quantize_model_on_device_matches_host_quantization(dev):
+    from test_host import _Model  # toy model with the reference's slot names
+    m = _Model()
+    host = quantize_model(m, bits=4, group_size=32, use_kernel=False)
+    dq = quantize_model(m.to(dev), bits=4, group_size=32, use_kernel=True)
+    for a, b in zip(host.modules(), dq.modules()):
+        if isinstance(a, QuantLinear):
+            assert torch.equal(a.w_q, b.w_q.cpu()) and torch.equal(a.scale, b.scale.cpu())
+    x = torch.randn(3, 64, device=dev)
+    blk = dq.blocks[0]
+    _close(blk.attn.wq(x), x @ host.blocks[0].attn.wq.dequant().to(dev).t(), "quantized model slot")
+
+
+def test_int8_ste_matches_reference(dev):
+    """test_backward.py:151-170 on the device."""
+    torch.manual_seed(1)
+    x = torch.randn(9, 32, device=dev, requires_grad=True)
+    w = torch.randn(24, 32, device=dev)
+    w_q, s = quantize_int8(w)
+    master = w.clone().requires_grad_(True)
+    y = Int8MatmulSTE.apply(x, w_q, s, master)
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    x2 = x.detach().clone().requires_grad_(True)
+    ref_y = x2 @ dequantize_int8(w_q, s).t()
+    ref_y.backward(dy)
+    _close(y.detach(), ref_y.detach(), "STE forward")
+    _close(x.grad, x2.grad, "STE input grad")
+    _close(master.grad, dy.t() @ x.detach(), "STE master grad")
+
+
+def test_fp8_linear_kernel_vs_emulation(dev):
+    from train.fp8 import FP8Linear
+    torch.manual_seed(2)
+    lin = nn.Linear(256, 192, bias=False)
+    fk = FP8Linear(lin, use_kernel=True).to(dev)
+    fe = FP8Linear(lin, use_kernel=False).to(dev)
+    x = torch.randn(70, 256, device=dev)
+    _close(fk(x), fe(x), "FP8Linear forward")
+
+
+def test_greedy_decode_tokens_identical(dev):
+    """The engine / speculative call pattern (M = 1 draft steps, M = gamma + 1 verify,
+    M = batch, M = prompt length) through a stack of QuantLinear layers: greedy tokens
+    from the kernel path equal those of the use_kernel=False path."""
+    torch.manual_seed(3)
+    d, vocab = 256, 96
+    emb = torch.randn(vocab, d, device=dev) * 0.5
+    layers = [nn.Linear(d, d, bias=False) for _ in range(3)]
+    head = torch.randn(vocab, d, device=dev) * 0.1
+    for bits in (8, 4):
+        stacks = {uk: [QuantLinear(l, bits=bits, group_size=64, use_kernel=uk).to(dev) for l in layers]
+                  for uk in (True, False)}
+
+        def run(uk, toks):
+            h = emb[toks]
+            for q in stacks[uk]:
+                h = torch.tanh(q(h))
+            return (h @ head.t()).argmax(-1)
+
+        for M in (1, 5, 4, 40):
+            toks = torch.randint(0, vocab, (M,), device=dev)
+            for _ in range(6):
+                a, b = run(True, toks), run(False, toks)
+                assert torch.equal(a, b), f"bits={bits} M={M}"
+                toks = a

@@ -1,0 +1,157 @@
+"""Host-side behaviour of the drop-in modules (no GPU): kernel entry points refuse
+host tensors instead of computing elsewhere, the load-time quantizers and the
+use_kernel=False paths match the oracle, and the module surface matches the
+reference's."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from conftest import golden
+from oracle import ref
+
+from kernels.dequant_matmul import int4_matmul, int8_dgrad, int8_matmul
+from kernels.fp8_matmul import E4M3_MAX, decode_e4m3, dequantize_e4m3, fp8_matmul, quantize_e4m3
+from kernels.moe_grouped import int4_grouped_matmul
+from serve.quantize import (QuantLinear, dequantize_int4, dequantize_int8, model_weight_bytes,
+                            quantize_int4, quantize_int8, quantize_model)
+
+
+def test_kernel_entry_points_refuse_host_tensors():
+    a = torch.randn(2, 64)
+    w8, s8 = quantize_int8(torch.randn(16, 64))
+    w4, s4 = quantize_int4(torch.randn(16, 64), 32)
+    with pytest.raises(TypeError, match="HIP device"):
+        int8_matmul(a, w8, s8)
+    with pytest.raises(TypeError, match="HIP device"):
+        int4_matmul(a, w4, s4, 32)
+    with pytest.raises(TypeError, match="HIP device"):
+        int8_dgrad(torch.randn(2, 16), w8, s8)
+    with pytest.raises(TypeError, match="HIP device"):
+        decode_e4m3(torch.arange(256, dtype=torch.uint8))
+    bits = quantize_e4m3(a, 0.01)
+    with pytest.raises(TypeError, match="HIP device"):
+        fp8_matmul(bits, bits, 0.01, 0.01)
+    with pytest.raises(TypeError, match="HIP device"):
+        int4_grouped_matmul(a.bfloat16(), w4[None], s4[None], torch.tensor([2]), 32)
+
+
+def test_int4_matmul_keeps_reference_assert():
+    with pytest.raises(AssertionError):
+        int4_matmul(torch.randn(2, 64), torch.zeros(4, 16, dtype=torch.uint8),
+                    torch.ones(4, 2), 32)
+
+
+def test_host_quantizers_match_oracle():
+    d = golden("quant_int8")
+    q, s = quantize_int8(torch.from_numpy(d["w"]))
+    assert np.array_equal(q.numpy(), d["w_q"]) and np.array_equal(s.numpy(), d["scale"])
+    d = golden("quant_int4")
+    for gs in (16, 32, 64, 128):
+        p, s = quantize_int4(torch.from_numpy(d[f"w_g{gs}"]), gs)
+        assert np.array_equal(p.numpy(), d[f"packed_g{gs}"])
+        assert np.array_equal(s.numpy(), d[f"scale_g{gs}"])
+    e = golden("e4m3_encode")
+    assert np.array_equal(quantize_e4m3(torch.from_numpy(e["x_rows"]),
+                                        torch.from_numpy(e["s_rows"])).numpy(), e["q_rows"])
+
+
+def test_host_dequantizers_match_oracle():
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(24, 96, generator=g)
+    q, s = quantize_int8(w)
+    assert np.array_equal(dequantize_int8(q, s).numpy(), ref.dequantize_int8(q.numpy(), s.numpy()))
+    p, s = quantize_int4(w, 32)
+    assert np.array_equal(dequantize_int4(p, s, 32).numpy(),
+                          ref.dequantize_int4(p.numpy(), s.numpy(), 32))
+    bits = torch.arange(256, dtype=torch.uint8)
+    assert np.array_equal(dequantize_e4m3(bits, 0.5).numpy(),
+                          ref.dequantize_e4m3(bits.numpy(), 0.5), equal_nan=True)
+
+
+def test_quantlinear_reference_path_on_host():
+    """test_quantize.py:52-58 shape: QuantLinear(use_kernel=False) equals x @ dequant(W)^T."""
+    lin = nn.Linear(48, 32, bias=False)
+    x = torch.randn(2, 7, 48)
+    for bits in (8, 4):
+        ql = QuantLinear(lin, bits=bits, group_size=16, use_kernel=False)
+        y = ql(x)
+        assert y.shape == (2, 7, 32)
+        wq, sc = ql.w_q.numpy(), ql.scale.numpy()
+        want = ref.int8_matmul(x.reshape(-1, 48).numpy(), wq, sc) if bits == 8 else \
+            ref.int4_matmul(x.reshape(-1, 48).numpy(), wq, sc, 16)
+        assert np.allclose(y.reshape(-1, 32).detach().numpy(), want, rtol=1e-5, atol=1e-5)
+        assert ql.weight_bytes() == wq.nbytes + sc.nbytes
+    with pytest.raises(AssertionError):
+        QuantLinear(nn.Linear(4, 4, bias=True))
+    with pytest.raises(AssertionError):
+        QuantLinear(nn.Linear(4, 4, bias=False), bits=3)
+
+
+class _Attn(nn.Module):
+    def __init__(self, d):
+        super().__init__()
+        self.wq, self.wk, self.wv, self.wo = (nn.Linear(d, d, bias=False) for _ in range(4))
+
+
+class _MLP(nn.Module):
+    def __init__(self, d, h):
+        super().__init__()
+        self.w_gate, self.w_up = nn.Linear(d, h, bias=False), nn.Linear(d, h, bias=False)
+        self.w_down = nn.Linear(h, d, bias=False)
+
+
+class _MoE(nn.Module):
+    def __init__(self, d, h, e):
+        super().__init__()
+        self.router = nn.Linear(d, e, bias=False)
+        self.experts = nn.ModuleList(_MLP(d, h) for _ in range(e))
+
+
+class _Block(nn.Module):
+    def __init__(self, d, h, moe):
+        super().__init__()
+        self.attn = _Attn(d)
+        self.is_moe = moe
+        self.mlp = _MoE(d, h, 2) if moe else _MLP(d, h)
+
+
+class _Model(nn.Module):
+    def __init__(self, d=64, h=128):
+        super().__init__()
+        self.embed = nn.Embedding(32, d)
+        self.blocks = nn.ModuleList([_Block(d, h, False), _Block(d, h, True)])
+
+
+def test_quantize_model_swaps_every_block_linear():
+    """serve/quantize.py:98-115: attention and (expert) MLP linears become QuantLinear,
+    the router and embeddings stay fp; memory shrinks (test_quantize.py:88-97)."""
+    m = _Model()
+    q8 = quantize_model(m, bits=8, use_kernel=False)
+    q4 = quantize_model(m, bits=4, use_kernel=False)
+    n_q = sum(isinstance(x, QuantLinear) for x in q8.modules())
+    assert n_q == 4 + 3 + 4 + 3 * 2
+    assert isinstance(q8.blocks[1].mlp.router, nn.Linear)
+    assert isinstance(m.blocks[0].attn.wq, nn.Linear)          # original untouched
+    fp = model_weight_bytes(m)
+    assert model_weight_bytes(q8) < fp * 0.5 and model_weight_bytes(q4) < model_weight_bytes(q8)
+
+
+def test_fp8_linear_emulation_on_host():
+    """train/fp8.py: FP8Linear(use_kernel=False) forward equals the decoded-operand matmul."""
+    from train.fp8 import DynamicScaler, FP8Linear
+    torch.manual_seed(1)
+    lin = nn.Linear(16, 12, bias=False)
+    f = FP8Linear(lin)
+    x = torch.randn(5, 16)
+    y = f(x)
+    sx = DynamicScaler().scale_for(x)
+    sw = DynamicScaler().scale_for(lin.weight)
+    xb = ref.quantize_e4m3(x.numpy(), sx)
+    wb = ref.quantize_e4m3(lin.weight.detach().numpy(), sw)
+    want = ref.dequantize_e4m3(xb, sx) @ ref.dequantize_e4m3(wb, sw).T
+    assert np.allclose(y.detach().numpy(), want, rtol=1e-5, atol=1e-6)
+    assert E4M3_MAX == 448.0

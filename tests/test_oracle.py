@@ -1,0 +1,294 @@
+"""Pins the CPU oracle (oracle/ref.py) before it is trusted as the checker.
+
+Each oracle function is checked against (a) the golden fixtures written by
+tests/golden/make_golden.py from torch's CPU ops in the reference's order,
+(b) torch live, where torch is the library the reference computes with, and
+(c) what the mathematics fixes: brute-force loops on tiny inputs, round-trip
+bounds and closed-form special cases. Planted mistakes in a copy of the oracle
+must fail these checks.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden
+from oracle import ref
+
+
+# ------------------------------------------------------------------ e4m3 decode
+
+
+def test_decode_kat_all_256_patterns():
+    """test_fp8.py:16-26: every byte equals torch's float8_e4m3fn view; the two NaN
+    patterns 0x7F / 0xFF decode to 0 in the kernel semantics."""
+    d = golden("e4m3_decode_kat")
+    nan = np.isnan(d["value"])
+    assert nan.sum() == 2 and set(np.nonzero(nan)[0]) == {0x7F, 0xFF}
+    dec = ref.e4m3_decode(d["bits"])
+    assert np.array_equal(dec[~nan].view(np.uint32), d["value"][~nan].view(np.uint32))
+    assert (dec[nan] == 0).all()
+    assert np.array_equal(ref.e4m3_decode(d["bits"], nan_to_zero=False), d["value"], equal_nan=True)
+    live = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(live, d["value"], equal_nan=True)
+
+
+def test_decode_closed_form_points():
+    assert ref.E4M3_TABLE[0x7E] == 448.0          # max finite
+    assert ref.E4M3_TABLE[0x01] == 2.0 ** -9      # smallest subnormal
+    assert ref.E4M3_TABLE[0x08] == 2.0 ** -6      # smallest normal
+    assert ref.E4M3_TABLE[0x38] == 1.0
+    assert ref.E4M3_TABLE[0xB8] == -1.0
+    finite = ref.E4M3_TABLE[:127]
+    assert (np.diff(finite) > 0).all()            # codes 0x00..0x7E are ordered
+
+
+# ------------------------------------------------------------------ e4m3 encode
+
+
+@pytest.mark.parametrize("part", ["boundary", "random"])
+def test_encode_matches_golden(part):
+    e = golden("e4m3_encode")
+    q = ref.quantize_e4m3(e[f"x_{part}"], 1.0)
+    assert np.array_equal(q, e[f"q_{part}"])
+
+
+def test_encode_scaled_and_per_row_match_golden():
+    e = golden("e4m3_encode")
+    assert np.array_equal(ref.quantize_e4m3(e["x_scaled"], float(e["scale"])), e["q_scaled"])
+    assert np.array_equal(ref.quantize_e4m3(e["x_rows"], e["s_rows"]), e["q_rows"])
+    assert np.array_equal(ref.dequantize_e4m3(e["q_scaled"], float(e["scale"])), e["dq_scaled"])
+
+
+def test_encode_matches_torch_cast_live():
+    g = np.random.default_rng(7)
+    bits = g.integers(0, 2 ** 32, size=1_000_000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = np.where(np.isfinite(x), x, np.float32(1.0))
+    near = (g.standard_normal(500_000) * np.exp2(g.integers(-12, 10, 500_000))).astype(np.float32)
+    for v in (x, near):
+        t = torch.from_numpy(v).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        assert np.array_equal(ref.e4m3_encode(v), t)
+
+
+@pytest.mark.slow
+def test_encode_matches_torch_cast_dense():
+    """All fp32 patterns of every binade that maps into e4m3's range, subsampled
+    by a stride coprime to the mantissa grid."""
+    for e in range(110, 137):
+        base = np.uint32(e << 23)
+        m = np.arange(0, 1 << 23, 7, dtype=np.uint32)
+        v = (base | m).view(np.float32)
+        v = np.concatenate([v, -v])
+        t = torch.from_numpy(v).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        assert np.array_equal(ref.e4m3_encode(v), t), f"binade {e}"
+
+
+def test_encode_special_values():
+    v = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 448.0, 464.0, 1e30, 2.0 ** -10], np.float32)
+    q = ref.e4m3_encode(v)
+    assert list(q[:4]) == [0x00, 0x80, 0x7E, 0xFE]
+    assert q[4] & 0x7F == 0x7F
+    assert list(q[5:8]) == [0x7E, 0x7E, 0x7E]
+    assert q[8] == 0x00                        # 2^-10 < half the smallest subnormal
+
+
+# ------------------------------------------------------------------ INT8 / INT4 quantizers
+
+
+def test_quantize_int8_matches_golden():
+    d = golden("quant_int8")
+    q, s = ref.quantize_int8(d["w"])
+    assert np.array_equal(q, d["w_q"]) and np.array_equal(s.view(np.uint32), d["scale"].view(np.uint32))
+    assert (q[3] == 0).all() and s[3] == np.float32(1e-8)
+
+
+@pytest.mark.parametrize("gs", [16, 32, 64, 128])
+def test_quantize_int4_matches_golden(gs):
+    d = golden("quant_int4")
+    p, s = ref.quantize_int4(d[f"w_g{gs}"], gs)
+    assert np.array_equal(p, d[f"packed_g{gs}"])
+    assert np.array_equal(s.view(np.uint32), d[f"scale_g{gs}"].view(np.uint32))
+    assert (ref.unpack_int4(p)[2, :gs] == 8).all()  # all-zero group -> stored nibble 8
+
+
+def test_quantizers_match_torch_live():
+    g = torch.Generator().manual_seed(11)
+    w = torch.randn(96, 384, generator=g) * 0.02
+    scale = (w.abs().amax(dim=1) / 127.0).clamp(min=1e-8)
+    wq = torch.round(w / scale[:, None]).clamp(-127, 127).to(torch.int8)
+    q, s = ref.quantize_int8(w.numpy())
+    assert np.array_equal(q, wq.numpy()) and np.array_equal(s, scale.numpy())
+    gq = w.reshape(96, 3, 128)
+    s4 = (gq.abs().amax(dim=2) / 7.0).clamp(min=1e-8)
+    q4 = (torch.round(gq / s4[:, :, None]).clamp(-8, 7) + 8).reshape(96, 384).to(torch.uint8)
+    p4 = (q4[:, 0::2] | (q4[:, 1::2] << 4))
+    p, s = ref.quantize_int4(w.numpy(), 128)
+    assert np.array_equal(p, p4.numpy()) and np.array_equal(s, s4.numpy())
+
+
+def test_roundtrip_error_bounded():
+    """test_quantize.py:16-28: |w - dequant(quant(w))| <= scale / 2."""
+    g = np.random.default_rng(0)
+    w = g.standard_normal((64, 48)).astype(np.float32)
+    q, s = ref.quantize_int8(w)
+    assert (np.abs(w - ref.dequantize_int8(q, s)) <= s[:, None] / 2 + 1e-6).all()
+    w = g.standard_normal((32, 64)).astype(np.float32)
+    p, s = ref.quantize_int4(w, 16)
+    bound = np.repeat(s, 16, axis=1) / 2 + 1e-6
+    assert (np.abs(w - ref.dequantize_int4(p, s, 16)) <= bound).all()
+
+
+def test_dequantize_int4_brute_force():
+    g = np.random.default_rng(1)
+    p = g.integers(0, 256, size=(3, 8), dtype=np.uint8)
+    s = g.random((3, 4), dtype=np.float32) + 0.5
+    w = ref.dequantize_int4(p, s, 4)
+    for n in range(3):
+        for k in range(16):
+            byte = int(p[n, k // 2])
+            nib = byte & 15 if k % 2 == 0 else byte >> 4
+            assert w[n, k] == np.float32((nib - 8) * s[n, k // 4])
+
+
+# ------------------------------------------------------------------ GEMM oracles
+
+
+def _brute(a, w):
+    M, K = a.shape
+    N = w.shape[0]
+    y = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            y[m, n] = sum(float(a[m, k]) * float(w[n, k]) for k in range(K))
+    return y
+
+
+def test_int8_matmul_brute_force():
+    g = np.random.default_rng(2)
+    a = g.standard_normal((3, 7)).astype(np.float32)
+    q = g.integers(-127, 128, size=(5, 7)).astype(np.int8)
+    s = (g.random(5) + 0.1).astype(np.float32)
+    y = ref.int8_matmul(a, q, s)
+    yb = _brute(a, q.astype(np.float64)) * s[None, :]
+    assert np.allclose(y, yb, rtol=1e-5, atol=1e-5)
+
+
+def test_int4_matmul_brute_force():
+    g = np.random.default_rng(3)
+    a = g.standard_normal((2, 8)).astype(np.float32)
+    p = g.integers(0, 256, size=(3, 4), dtype=np.uint8)
+    s = (g.random((3, 2)) + 0.1).astype(np.float32)
+    wd = np.zeros((3, 8))
+    for n in range(3):
+        for k in range(8):
+            nib = (int(p[n, k // 2]) >> (4 * (k % 2))) & 15
+            wd[n, k] = (nib - 8) * float(s[n, k // 4])
+    assert np.allclose(ref.int4_matmul(a, p, s, 4), _brute(a, wd), rtol=1e-5, atol=1e-5)
+
+
+def test_int8_dgrad_brute_force():
+    g = np.random.default_rng(4)
+    dy = g.standard_normal((3, 5)).astype(np.float32)
+    q = g.integers(-127, 128, size=(5, 6)).astype(np.int8)
+    s = (g.random(5) + 0.1).astype(np.float32)
+    dx = np.zeros((3, 6))
+    for m in range(3):
+        for k in range(6):
+            dx[m, k] = sum(float(dy[m, n]) * float(s[n]) * float(q[n, k]) for n in range(5))
+    assert np.allclose(ref.int8_dgrad(dy, q, s), dx, rtol=1e-5, atol=1e-5)
+
+
+def test_fp8_matmul_brute_force_per_row_scales():
+    g = np.random.default_rng(5)
+    ab = g.integers(0, 256, size=(3, 9), dtype=np.uint8)
+    bb = g.integers(0, 256, size=(4, 9), dtype=np.uint8)
+    sa = (g.random(3) + 0.1).astype(np.float32)
+    sb = (g.random(4) + 0.1).astype(np.float32)
+    dec = lambda b: 0.0 if (b & 0x7F) == 0x7F else float(ref.E4M3_TABLE[b])  # noqa: E731
+    y = np.zeros((3, 4))
+    for m in range(3):
+        for n in range(4):
+            y[m, n] = sum(dec(ab[m, k]) * dec(bb[n, k]) for k in range(9)) * float(sa[m]) * float(sb[n])
+    assert np.allclose(ref.fp8_matmul(ab, bb, sa, sb), y, rtol=1e-5, atol=1e-6)
+
+
+def test_fp8_matmul_matches_golden():
+    d = golden("fp8_small")
+    for t in ("t1", "t2", "t3"):
+        y = ref.fp8_matmul(d[f"{t}_a"], d[f"{t}_b"], float(d[f"{t}_sa"]), float(d[f"{t}_sb"]))
+        assert np.allclose(y, d[f"{t}_y"], rtol=1e-5, atol=1e-5)
+
+
+def test_int8_config_a_matches_golden():
+    d = golden("gemm_int8_config_a")
+    ok, worst = ref.close_fp32(ref.int8_matmul(d["x"], d["w_q"], d["scale"]), d["y"])
+    assert ok and worst < 0.05
+
+
+def test_int4_small_matches_golden():
+    d = golden("gemm_int4_small")
+    for t in ("t1", "t2", "t3", "g128"):
+        y = ref.int4_matmul(d[f"{t}_a"], d[f"{t}_packed"], d[f"{t}_scale"], int(d[f"{t}_gs"]))
+        assert np.allclose(y, d[f"{t}_y"], rtol=1e-5, atol=1e-5)
+
+
+def test_grouped_matches_per_expert_loop():
+    g = np.random.default_rng(6)
+    E, N, K, gs = 3, 10, 64, 32
+    p = g.integers(0, 256, size=(E, N, K // 2), dtype=np.uint8)
+    s = (g.random((E, N, K // gs)) + 0.1).astype(np.float32)
+    off = np.array([0, 4, 4, 9])
+    a = g.standard_normal((9, K)).astype(np.float32)
+    y = ref.grouped_int4_matmul(a, p, s, off, gs)
+    assert np.allclose(y[:4], ref.int4_matmul(a[:4], p[0], s[0], gs))
+    assert np.allclose(y[4:9], ref.int4_matmul(a[4:9], p[2], s[2], gs))
+
+
+def test_routing_matches_golden():
+    d = golden("route_small")
+    w, ex = ref.route_topk(d["logits"], 2)
+    assert np.array_equal(ex, d["experts"]) and np.allclose(w, d["weights"], rtol=1e-6, atol=1e-7)
+    tok, counts, pos = ref.sort_by_expert(d["experts"], 8)
+    assert np.array_equal(tok, d["token_of_slot"]) and np.array_equal(counts, d["counts"])
+    assert np.array_equal(pos, d["pos"])
+
+
+def test_tolerance_helpers():
+    ref_ = np.array([1.0, -2.0, 0.0], np.float32)
+    assert ref.close_bf16(ref_ + 0.009, ref_)[0] and not ref.close_bf16(ref_ + 0.05, ref_)[0]
+    assert ref.close_fp32(ref_ * (1 + 2 ** -11), ref_)[0]
+    assert not ref.close_fp32(ref_ * (1 + 2 ** -7), ref_)[0]
+
+
+# ------------------------------------------------------------------ planted mistakes
+
+
+def test_planted_mistakes_fail_the_pins():
+    d = golden("quant_int4")
+    w = d["w_g32"]
+    # nibble order swapped (odd k in the low nibble)
+    q = (np.clip(np.rint(w.reshape(32, 8, 32) / d["scale_g32"][:, :, None]), -8, 7) + 8)
+    q = q.reshape(32, 256).astype(np.uint8)
+    swapped = (q[:, 1::2] | (q[:, 0::2] << 4)).astype(np.uint8)
+    assert not np.array_equal(swapped, d["packed_g32"])
+    # offset 7 instead of 8 in the dequantizer changes the GEMM beyond tolerance
+    gm = golden("gemm_int4_small")
+    p, s, a = gm["g128_packed"], gm["g128_scale"], gm["g128_a"]
+    wrong = ((ref.unpack_int4(p).astype(np.float32) - 7).reshape(40, 4, 128) * s[:, :, None]).reshape(40, 512)
+    assert not ref.close_fp32(a @ wrong.T, gm["g128_y"])[0]
+    # transposed operand / scale applied per column instead of per row
+    da = golden("gemm_int8_config_a")
+    bad = da["x"] @ (da["w_q"].astype(np.float32) * da["scale"][:8, None].mean()).T
+    assert not ref.close_fp32(bad, da["y"])[0]
+    # e4m3 rounding ties away from zero instead of to even
+    e = golden("e4m3_encode")
+    x = e["x_boundary"].astype(np.float64)
+    a_ = np.minimum(np.abs(x), 448)
+    hi = np.minimum(np.searchsorted(ref._POS_VALUES, a_), 126)
+    lo = np.maximum(hi - 1, 0)
+    away = np.where(ref._POS_VALUES[hi] - a_ <= a_ - ref._POS_VALUES[lo], hi, lo)
+    finite = np.isfinite(x)
+    assert not np.array_equal(away[finite].astype(np.uint8), e["q_boundary"][finite] & 0x7F)
