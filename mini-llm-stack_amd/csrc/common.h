@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "../../include/mls.h"
 
@@ -58,6 +59,50 @@ __device__ __forceinline__ void store4(T* dst, float v0, float v1, float v2, flo
                                pack2_bits(from_f32<T>(v2), from_f32<T>(v3)));
     *reinterpret_cast<uint2*>(dst) = u;
   }
+}
+
+// v moved across lanes by a DPP pattern (CTRL = dpp_ctrl encoding).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+namespace detail {
+// Halves the live values per step: lanes with lane & BIT keep the upper half,
+// the others the lower half, each adding its xor-partner's copy. With one value
+// left, the lane bits BIT..0 are summed (lowest first, so the mirror patterns
+// pair lanes that already hold the sums of their quads / octets).
+template <int N, int BIT>
+__device__ __forceinline__ void reduce_split(float* v, int lane) {
+  if constexpr (N > 1) {
+    constexpr int H = N / 2;
+    const bool upper = (lane & BIT) != 0;
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      const float send = upper ? v[i] : v[i + H];
+      const float keep = upper ? v[i + H] : v[i];
+      v[i] = keep + __shfl_xor(send, BIT, 64);
+    }
+    reduce_split<H, BIT / 2>(v, lane);
+  } else {
+    if constexpr (BIT >= 1) v[0] += dpp_mov<0xB1>(v[0]);   // quad_perm [1,0,3,2]: lane ^ 1
+    if constexpr (BIT >= 2) v[0] += dpp_mov<0x4E>(v[0]);   // quad_perm [2,3,0,1]: lane ^ 2
+    if constexpr (BIT >= 4) v[0] += dpp_mov<0x141>(v[0]);  // row_half_mirror: the other quad
+    if constexpr (BIT >= 8) v[0] += dpp_mov<0x140>(v[0]);  // row_mirror: the other octet
+    if constexpr (BIT >= 16) v[0] += __shfl_xor(v[0], 16, 64);
+    if constexpr (BIT >= 32) v[0] += __shfl_xor(v[0], 32, 64);
+  }
+}
+}  // namespace detail
+
+// Sums V per-lane partials over the wavefront in one pass (V a power of two, <= 64).
+// Afterwards v[0] of lane L holds the total of partial index L / (64 / V); the
+// other entries of v are clobbered.
+template <int V>
+__device__ __forceinline__ void wave_reduce_many(float (&v)[V]) {
+  static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
+  detail::reduce_split<V, 32>(v, threadIdx.x & 63);
 }
 
 // Sum over the 64 lanes of a wavefront; every lane receives the total.

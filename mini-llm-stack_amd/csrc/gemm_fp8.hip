@@ -1,17 +1,31 @@
-// e4m3 x e4m3 -> fp32-accumulated GEMM with inline scales (kernels/fp8_matmul.py:50-81),
-// on the gfx950 fp8 MFMA (v_mfma_f32_16x16x128_f8f6f4 with both operands OCP e4m3).
+// e4m3 x e4m3 GEMM with inline scales (kernels/fp8_matmul.py:50-81).
 //
+// Two datapaths, chosen by the caller:
+//   exact  (default): both operands widened to bf16 (exact) and multiplied on the
+//          bf16 MFMA, whose fp32 accumulation matches an fp32 GEMM of the decoded
+//          operands (gemm_mfma16.hip);
+//   native (MLS_FP8_NATIVE): the raw e4m3 bytes go to the fp8 MFMA
+//          (v_mfma_f32_16x16x128_f8f6f4), twice the peak rate. That instruction adds
+//          each aligned group of 8 products keeping 13 bits below the largest and
+//          rounds toward -inf, so rows whose products span more than ~2^13 in a group
+//          (outliers) differ from the fp32 result by up to ~2^-13 of the group maximum
+//          per group.
+//
+// Native kernel:
 // Block tile 256 (m) x 256 (n) x 128 (k); 4 wavefronts in 2 x 2, each owning a
 // 128 x 128 sub-tile = 8 x 8 MFMA tiles (256 fp32 accumulators per lane). Both
 // operands are K-contiguous ("NT"): a stage is 256 rows x 128 bytes per operand,
 // staged global -> registers -> LDS with the 16-byte chunk index XOR-swizzled by
-// (row & 7), double-buffered with one barrier per stage. The B tile is the MFMA
+// row & 7, double-buffered with one barrier per stage. The lanes of k-block g of an
+// operand take 16-byte chunks g and g + 4 of the 128-byte row (any k order is valid
+// when both operands use it); with the row & 7 swizzle these reads, and the staging
+// writes, measured free of LDS bank conflicts on gfx950. The B tile is the MFMA
 // "A" operand so each lane ends with 4 consecutive n of one m: the epilogue
 // applies sa[m] * sb[n] and stores 4 outputs at once.
 //
 // Shapes outside the fast path (K % 128 != 0, small or unaligned operands) run
 // a one-thread-per-output kernel that decodes with the reference's NaN -> 0 rule.
-#include "common.h"
+#include "wq.h"
 
 namespace mls {
 
@@ -74,7 +88,7 @@ __global__ __launch_bounds__(256) void fp8_gemm_mfma_kernel(
   // through buffer descriptors covering only this tile's valid rows, so rows past
   // M or N read as zeros; the stage offset k0 travels in the scalar offset.
   const int srow = tid >> 3, skc = tid & 7;
-  const int lds0 = srow * 8 + (skc ^ (srow & 7));
+  const int lds0 = srow * 8 + (skc ^ (srow & 7));  // (srow + 32 i) & 7 is the same
   const int rows_a = min(BM, M - m0), rows_b = min(BN, N - n0);
   const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a + (int64_t)m0 * lda), (short)0, (int)(rows_a * lda), 0x00020000);
@@ -109,7 +123,7 @@ __global__ __launch_bounds__(256) void fp8_gemm_mfma_kernel(
   MLS_FP8_STORE(0)
   __syncthreads();
 
-  const int lr = lane & 15, lk = lane >> 4;  // operand row, 32-byte k block
+  const int lr = lane & 15, lk = lane >> 4;  // operand row, k block (chunks lk and lk + 4)
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
     if (kt + 1 < nk) { MLS_FP8_LOAD((kt + 1) * BK) }
@@ -119,16 +133,16 @@ __global__ __launch_bounds__(256) void fp8_gemm_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int row = wn0 + i * 16 + lr, sw = row & 7;
-      const uint4 lo = bs[row * 8 + ((2 * lk) ^ sw)];
-      const uint4 hi = bs[row * 8 + ((2 * lk + 1) ^ sw)];
+      const uint4 lo = bs[row * 8 + (lk ^ sw)];
+      const uint4 hi = bs[row * 8 + ((lk + 4) ^ sw)];
       bop[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
                      (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int row = wm0 + j * 16 + lr, sw = row & 7;
-      const uint4 lo = as[row * 8 + ((2 * lk) ^ sw)];
-      const uint4 hi = as[row * 8 + ((2 * lk + 1) ^ sw)];
+      const uint4 lo = as[row * 8 + (lk ^ sw)];
+      const uint4 hi = as[row * 8 + ((lk + 4) ^ sw)];
       const i32x8 aop = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
                          (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 #pragma unroll
@@ -169,20 +183,22 @@ __global__ __launch_bounds__(256) void fp8_gemm_mfma_kernel(
 }
 
 template <typename CT>
-static int launch_fp8(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, float sa,
-                      const float* sap, int64_t sas, float sb, const float* sbp, int64_t sbs,
-                      void* c, int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+static int launch_generic(const Fp8Args& f) {
+  hipLaunchKernelGGL(fp8_gemm_generic_kernel<CT>, dim3((unsigned)cdiv(f.M * f.N, 256)), dim3(256), 0,
+                     f.stream, f.a, f.lda, f.b, f.ldb, f.sa, f.sap, f.sas, f.sb, f.sbp, f.sbs,
+                     (CT*)f.c, f.ldc, f.M, f.N, f.K);
+  return check_launch("mls_fp8_gemm(generic)");
+}
+
+template <typename CT>
+static int launch_native(const Fp8Args& f) {
   // buffer descriptors address at most 2^31 bytes per 256-row tile
-  const bool fast = K >= 128 && K % 128 == 0 && M >= 64 && N >= 64 && aligned(a, 16) &&
-                    aligned(b, 16) && lda % 16 == 0 && ldb % 16 == 0 && aligned(c, 16) &&
-                    M < (1 << 30) && N < (1 << 30) && lda * 256 < (1ll << 31) &&
-                    ldb * 256 < (1ll << 31);
-  if (!fast) {
-    hipLaunchKernelGGL(fp8_gemm_generic_kernel<CT>, dim3((unsigned)cdiv(M * N, 256)), dim3(256), 0,
-                       st, a, lda, b, ldb, sa, sap, sas, sb, sbp, sbs, (CT*)c, ldc, M, N, K);
-    return check_launch("mls_fp8_gemm(generic)");
-  }
-  const int mt = (int)cdiv(M, 256), nt = (int)cdiv(N, 256);
+  const bool fast = f.K >= 128 && f.K % 128 == 0 && f.M >= 64 && f.N >= 64 && aligned(f.a, 16) &&
+                    aligned(f.b, 16) && f.lda % 16 == 0 && f.ldb % 16 == 0 && aligned(f.c, 16) &&
+                    f.M < (1 << 30) && f.N < (1 << 30) && f.lda * 256 < (1ll << 31) &&
+                    f.ldb * 256 < (1ll << 31);
+  if (!fast) return MLS_ERR_UNSUPPORTED;
+  const int mt = (int)cdiv(f.M, 256), nt = (int)cdiv(f.N, 256);
   const size_t lds = 2 * 2 * 256 * 128;
   auto kern = fp8_gemm_mfma_kernel<CT>;
   static bool attr_set = false;
@@ -192,9 +208,10 @@ static int launch_fp8(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t l
       return fail(MLS_ERR_HIP, "mls_fp8_gemm: cannot reserve %zu bytes of LDS", lds);
     attr_set = true;
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)(mt * nt)), dim3(256), lds, st, a, lda, b, ldb, sa, sap,
-                     sas, sb, sbp, sbs, (CT*)c, ldc, (int)M, (int)N, (int)K, mt, nt);
-  return check_launch("mls_fp8_gemm");
+  hipLaunchKernelGGL(kern, dim3((unsigned)(mt * nt)), dim3(256), lds, f.stream, f.a, f.lda, f.b,
+                     f.ldb, f.sa, f.sap, f.sas, f.sb, f.sbp, f.sbs, (CT*)f.c, f.ldc, (int)f.M,
+                     (int)f.N, (int)f.K, mt, nt);
+  return check_launch("mls_fp8_gemm(native)");
 }
 
 }  // namespace mls
@@ -204,17 +221,28 @@ using namespace mls;
 extern "C" int mls_fp8_gemm(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb, float sa,
                             const float* sa_ptr, int64_t sa_stride, float sb, const float* sb_ptr,
                             int64_t sb_stride, void* c, int c_dt, int64_t ldc, int64_t M, int64_t N,
-                            int64_t K, mls_stream_t stream) {
+                            int64_t K, int flags, mls_stream_t stream) {
   if (M < 0 || N < 0 || K < 0)
     return fail(MLS_ERR_ARG, "mls_fp8_gemm: negative size M=%lld N=%lld K=%lld", (long long)M,
                 (long long)N, (long long)K);
   if (!is_float_dt(c_dt)) return fail(MLS_ERR_ARG, "mls_fp8_gemm: bad output dtype %d", c_dt);
+  if (flags & ~MLS_FP8_NATIVE) return fail(MLS_ERR_ARG, "mls_fp8_gemm: unknown flags 0x%x", flags);
   if (M == 0 || N == 0) return MLS_OK;
   if (!a || !b || !c) return fail(MLS_ERR_ARG, "mls_fp8_gemm: null pointer");
   if (lda < K || ldb < K || ldc < N || sa_stride < 0 || sb_stride < 0)
     return fail(MLS_ERR_ARG, "mls_fp8_gemm: bad leading dimension or scale stride");
-  hipStream_t st = (hipStream_t)stream;
-  if (c_dt == MLS_F32) return launch_fp8<float>(a, lda, b, ldb, sa, sa_ptr, sa_stride, sb, sb_ptr, sb_stride, c, ldc, M, N, K, st);
-  if (c_dt == MLS_F16) return launch_fp8<_Float16>(a, lda, b, ldb, sa, sa_ptr, sa_stride, sb, sb_ptr, sb_stride, c, ldc, M, N, K, st);
-  return launch_fp8<__bf16>(a, lda, b, ldb, sa, sa_ptr, sa_stride, sb, sb_ptr, sb_stride, c, ldc, M, N, K, st);
+  const Fp8Args f{a, lda, b, ldb, sa, sa_ptr, sa_stride, sb, sb_ptr, sb_stride, c, c_dt, ldc, M, N, K,
+                  (hipStream_t)stream};
+  int rc = MLS_ERR_UNSUPPORTED;
+  if (flags & MLS_FP8_NATIVE) {
+    if (c_dt == MLS_F32) rc = launch_native<float>(f);
+    else if (c_dt == MLS_F16) rc = launch_native<_Float16>(f);
+    else rc = launch_native<__bf16>(f);
+  } else {
+    rc = launch_fp8_exact(f);
+  }
+  if (rc != MLS_ERR_UNSUPPORTED) return rc;
+  if (c_dt == MLS_F32) return launch_generic<float>(f);
+  if (c_dt == MLS_F16) return launch_generic<_Float16>(f);
+  return launch_generic<__bf16>(f);
 }

@@ -1,0 +1,472 @@
+// Tiled GEMMs on the 16-bit MFMA (v_mfma_f32_16x16x32_{bf16,f16}), one engine for
+//   - weight-only INT8 / INT4 prefill: bf16/fp16 activations x dequantized weights,
+//   - the per-expert (grouped) INT4 variant for MoE,
+//   - the exact e4m3 GEMM: both e4m3 operands widened to bf16 (exact) on the way
+//     into LDS.
+// The 16-bit MFMAs add the exact products with fp32 precision, so every result
+// here is what an fp32 GEMM of the dequantized / decoded operands gives, up to
+// fp32 summation order. (gfx950's fp8 MFMAs instead add each group of 8 products
+// with 13 bits below the largest, rounding toward -inf: gemm_fp8.hip.)
+//
+// Block tile BM (rows m of A) x BN (rows n of B) x 64 (k), 256 threads as WM x WN
+// wavefronts. Per k-stage every thread prefetches its share of the next stage
+// (16-byte buffer loads; rows past the tile's valid range read as zeros) into
+// registers, runs the MFMAs of the current stage out of LDS, widens its
+// prefetched chunks to 16-bit floats (INT8: exact integers; INT4: exact v - 8;
+// e4m3: exact values via v_cvt_scalef32_pk_bf16_fp8) and stores them into the other
+// LDS buffer; one barrier per stage. LDS rows are 64 k = 128 bytes; the 16-byte
+// chunk index is XOR-ed with row & 7, which measured free of bank conflicts on
+// gfx950 for both the staging writes and the MFMA operand reads of this kernel.
+//
+// The B tile is the MFMA "A" operand, so each lane's accumulator holds 4
+// consecutive n of one m and the epilogue writes 4 outputs per store. Scales:
+// INT8 per n in the epilogue; INT4 per (n, group) on fp32 partial sums at every
+// group boundary; e4m3 per m and per n (or per tensor) in the epilogue.
+#include "wq.h"
+
+namespace mls {
+
+enum { A_RAW16 = 0, A_E4M3 = 1 };
+enum { B_INT8 = 0, B_INT4 = 1, B_E4M3 = 2 };
+
+struct Mfma16Params {
+  const void* a;
+  int64_t lda;  // elements of A's storage type (16-bit, or bytes for e4m3)
+  const uint8_t* b;
+  int64_t ldb;  // bytes
+  const void* s;  // INT8 [N] / INT4 [N][G] scales
+  int s_dt;
+  int64_t ld_sn, ld_sg;
+  int group;
+  float sa, sb;  // e4m3 per-tensor scales (used when the pointers are null)
+  const float* sap;
+  const float* sbp;
+  int64_t sas, sbs;
+  void* c;
+  int64_t ldc;
+  int M, N, K;
+  int n_tiles, m_tiles;
+  const int32_t* seg_off;  // grouped: expert row offsets [E + 1]
+  int E;
+  int64_t b_estride, s_estride;  // grouped: bytes / scale elements between experts
+};
+
+template <typename T> struct Mfma16;
+template <> struct Mfma16<__bf16> {
+  __device__ static __forceinline__ f32x4 mma(const uint4& a, const uint4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    bf16x2 v;
+    v.x = (__bf16)lo;
+    v.y = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+template <> struct Mfma16<_Float16> {
+  __device__ static __forceinline__ f32x4 mma(const uint4& a, const uint4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    f16x2 v;
+    v.x = (_Float16)lo;
+    v.y = (_Float16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+__device__ __forceinline__ int swz(int row) { return row & 7; }
+
+__device__ __forceinline__ float scale_at(const void* s, int s_dt, int64_t i) {
+  return s_dt == MLS_F16 ? (float)((const _Float16*)s)[i] : ((const float*)s)[i];
+}
+
+__device__ __forceinline__ float u8f(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xFFu); }
+
+// 16 INT8 weights -> 16 exact 16-bit floats (8 dwords, k order).
+template <typename MT>
+__device__ __forceinline__ void widen_int8(const uint4& q, uint32_t* o) {
+  const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t u = d[t] ^ 0x80808080u;  // q + 128
+    o[2 * t + 0] = Mfma16<MT>::pack2(u8f(u, 0) - 128.0f, u8f(u, 1) - 128.0f);
+    o[2 * t + 1] = Mfma16<MT>::pack2(u8f(u, 2) - 128.0f, u8f(u, 3) - 128.0f);
+  }
+}
+
+// 32 INT4 weights (even k in the low nibble) -> 32 exact values v - 8 (16 dwords).
+template <typename MT>
+__device__ __forceinline__ void widen_int4(const uint4& q, uint32_t* o) {
+  const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t lo = d[t] & 0x0F0F0F0Fu;         // k = 8t + 0, 2, 4, 6
+    const uint32_t hi = (d[t] >> 4) & 0x0F0F0F0Fu;  // k = 8t + 1, 3, 5, 7
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      o[4 * t + b] = Mfma16<MT>::pack2(u8f(lo, b) - 8.0f, u8f(hi, b) - 8.0f);
+  }
+}
+
+// 16 e4m3 bytes -> 16 bf16 (8 dwords, k order); exact: e4m3 is a subset of bf16.
+__device__ __forceinline__ void widen_e4m3(const uint4& q, uint32_t* o) {
+  const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    o[2 * t + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[t], 1.0f, false));
+    o[2 * t + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[t], 1.0f, true));
+  }
+}
+
+template <int AKIND, int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN,
+          bool GROUPED>
+__global__ __launch_bounds__(256) void mfma16_gemm_kernel(const Mfma16Params p) {
+  constexpr int BK = 64;
+  constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  constexpr int TM = WTM / 16, TN = WTN / 16;  // MFMA tiles per wave
+  static_assert(WM * WN == 4 && TM >= 1 && TN >= 1, "bad wave layout");
+  constexpr int A_ESZ = AKIND == A_RAW16 ? 2 : 1;
+  constexpr int A_CPR = BK * A_ESZ / 16;                  // 16-byte chunks per row per stage
+  constexpr int B_CPR = BKIND == B_INT4 ? 2 : 4;
+  constexpr int A_CH = BM * A_CPR, B_CH = BN * B_CPR;
+  constexpr int A_PT = (A_CH + 255) / 256;
+  static_assert(B_CH % 256 == 0, "BN too small for the weight staging");
+  constexpr int B_PT = B_CH / 256;
+  constexpr int A_RSTEP = 256 / A_CPR, B_RSTEP = 256 / B_CPR;
+  constexpr bool GS = BKIND == B_INT4;  // group scales on fp32 partial sums
+
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint4* As = reinterpret_cast<uint4*>(smem);  // [2][BM][8] 16-byte chunks
+  uint4* Bs = As + 2 * BM * 8;                  // [2][BN][8]
+  float* sS = reinterpret_cast<float*>(Bs + 2 * BN * 8);  // INT4: [2][2][BN]
+
+  // ---- which tile: consecutive logical ids share a B tile and sit on one XCD
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int nt = L / p.m_tiles, mt = L % p.m_tiles;
+  int row_hi = p.M, m0;
+  const uint8_t* bmat = p.b;
+  const void* smat = p.s;
+  if constexpr (GROUPED) {
+    int e = 0, cum = 0, row_lo = 0;
+    for (; e < p.E; ++e) {
+      const int lo = p.seg_off[e], hi = p.seg_off[e + 1];
+      const int t = (hi - lo + BM - 1) / BM;
+      if (mt < cum + t) {
+        row_lo = lo;
+        row_hi = hi;
+        break;
+      }
+      cum += t;
+    }
+    if (e == p.E) return;  // surplus block
+    m0 = row_lo + (mt - cum) * BM;
+    bmat += (int64_t)e * p.b_estride;
+    smat = (const uint8_t*)smat + (int64_t)e * p.s_estride * (p.s_dt == MLS_F16 ? 2 : 4);
+  } else {
+    m0 = mt * BM;
+  }
+  const int n0 = nt * BN;
+  const int N = p.N;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+
+  // ---- staging descriptors
+  const int rows_a = min(BM, row_hi - m0), rows_b = min(BN, N - n0);
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint8_t*)p.a + (int64_t)m0 * p.lda * A_ESZ), (short)0,
+      (int)(rows_a * p.lda * A_ESZ), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(bmat + (int64_t)n0 * p.ldb), (short)0, (int)(rows_b * p.ldb), 0x00020000);
+  const int a_row0 = tid / A_CPR, a_cc = tid % A_CPR;
+  const int b_row0 = tid / B_CPR, b_cc = tid % B_CPR;
+  int a_off[A_PT], b_off[B_PT];
+#pragma unroll
+  for (int i = 0; i < A_PT; ++i) a_off[i] = (a_row0 + A_RSTEP * i) * (int)p.lda * A_ESZ + a_cc * 16;
+#pragma unroll
+  for (int i = 0; i < B_PT; ++i) b_off[i] = (b_row0 + B_RSTEP * i) * (int)p.ldb + b_cc * 16;
+  const bool a_on = A_CH >= 256 || tid < A_CH;
+  const int64_t s_row = (int64_t)min(n0 + tid, N - 1) * p.ld_sn;
+
+  uint4 ra[A_PT], rb[B_PT];
+  float rs0 = 0.f, rs1 = 0.f;
+
+  auto load = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < A_PT; ++i)
+      if (a_on)
+        ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsa, a_off[i], k0 * A_ESZ, 0));
+#pragma unroll
+    for (int i = 0; i < B_PT; ++i)
+      rb[i] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(rsb, b_off[i], BKIND == B_INT4 ? k0 / 2 : k0, 0));
+    if constexpr (GS) {
+      if (tid < BN) {
+        rs0 = scale_at(smat, p.s_dt, s_row + (int64_t)(k0 / p.group) * p.ld_sg);
+        rs1 = scale_at(smat, p.s_dt, s_row + (int64_t)((k0 + 32) / p.group) * p.ld_sg);
+      }
+    }
+  };
+  auto store = [&](int buf) __attribute__((always_inline)) {
+    uint4* as = As + buf * BM * 8;
+    uint4* bs = Bs + buf * BN * 8;
+#pragma unroll
+    for (int i = 0; i < A_PT; ++i) {
+      if (!a_on) continue;
+      const int row = a_row0 + A_RSTEP * i;
+      if constexpr (AKIND == A_RAW16) {
+        as[row * 8 + (a_cc ^ swz(row))] = ra[i];
+      } else {
+        uint32_t o[8];
+        widen_e4m3(ra[i], o);
+        as[row * 8 + ((2 * a_cc + 0) ^ swz(row))] = make_uint4(o[0], o[1], o[2], o[3]);
+        as[row * 8 + ((2 * a_cc + 1) ^ swz(row))] = make_uint4(o[4], o[5], o[6], o[7]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_PT; ++i) {
+      const int row = b_row0 + B_RSTEP * i;
+      if constexpr (BKIND == B_INT4) {
+        uint32_t o[16];
+        widen_int4<MT>(rb[i], o);
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          bs[row * 8 + ((4 * b_cc + h) ^ swz(row))] =
+              make_uint4(o[4 * h + 0], o[4 * h + 1], o[4 * h + 2], o[4 * h + 3]);
+      } else {
+        uint32_t o[8];
+        if constexpr (BKIND == B_INT8) widen_int8<MT>(rb[i], o);
+        else widen_e4m3(rb[i], o);
+        bs[row * 8 + ((2 * b_cc + 0) ^ swz(row))] = make_uint4(o[0], o[1], o[2], o[3]);
+        bs[row * 8 + ((2 * b_cc + 1) ^ swz(row))] = make_uint4(o[4], o[5], o[6], o[7]);
+      }
+    }
+    if constexpr (GS) {
+      if (tid < BN) {
+        sS[(buf * 2 + 0) * BN + tid] = rs0;
+        sS[(buf * 2 + 1) * BN + tid] = rs1;
+      }
+    }
+  };
+
+  f32x4 acc[TN][TM];
+  f32x4 accg[GS ? TN : 1][GS ? TM : 1];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (GS) {
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int j = 0; j < TM; ++j) accg[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int nk = p.K / BK;
+  load(0);
+  store(0);
+  __syncthreads();
+
+  const int lr = lane & 15, lk = lane >> 4;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    const int k0 = kt * BK;
+    if (kt + 1 < nk) load(k0 + BK);
+    const uint4* as = As + buf * BM * 8;
+    const uint4* bs = Bs + buf * BN * 8;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int ch = ks * 4 + lk;
+      uint4 bop[TN], aop[TM];
+#pragma unroll
+      for (int i = 0; i < TN; ++i) {
+        const int row = wn0 + i * 16 + lr;
+        bop[i] = bs[row * 8 + (ch ^ swz(row))];
+      }
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        const int row = wm0 + j * 16 + lr;
+        aop[j] = as[row * 8 + (ch ^ swz(row))];
+      }
+      if constexpr (GS) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+          for (int j = 0; j < TM; ++j) accg[i][j] = Mfma16<MT>::mma(bop[i], aop[j], accg[i][j]);
+        if ((k0 + 32 * (ks + 1)) % p.group == 0) {  // group ends: acc += s[n] * partial
+          const float* sc = sS + (buf * 2 + ks) * BN + wn0 + 4 * lk;
+#pragma unroll
+          for (int i = 0; i < TN; ++i) {
+            const float4 s4 = *reinterpret_cast<const float4*>(sc + i * 16);
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+              acc[i][j][0] = fmaf(s4.x, accg[i][j][0], acc[i][j][0]);
+              acc[i][j][1] = fmaf(s4.y, accg[i][j][1], acc[i][j][1]);
+              acc[i][j][2] = fmaf(s4.z, accg[i][j][2], acc[i][j][2]);
+              acc[i][j][3] = fmaf(s4.w, accg[i][j][3], acc[i][j][3]);
+              accg[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+          for (int j = 0; j < TM; ++j) acc[i][j] = Mfma16<MT>::mma(bop[i], aop[j], acc[i][j]);
+      }
+    }
+    if (kt + 1 < nk) store(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: acc[i][j][r] = C[m = m0+wm0+16j+lr][n = n0+wn0+16i+4lk+r]
+  OT* c = static_cast<OT*>(p.c);
+#pragma unroll
+  for (int i = 0; i < TN; ++i) {
+    const int nb = n0 + wn0 + i * 16 + 4 * lk;
+    float sn[4] = {1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int n = min(nb + r, N - 1);
+      if constexpr (BKIND == B_INT8) sn[r] = scale_at(smat, p.s_dt, n);
+      if constexpr (BKIND == B_E4M3) sn[r] = p.sbp ? p.sbp[(int64_t)n * p.sbs] : p.sb;
+    }
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int m = m0 + wm0 + j * 16 + lr;
+      if (m >= row_hi) continue;
+      float sm = 1.f;
+      if constexpr (BKIND == B_E4M3) sm = p.sap ? p.sap[(int64_t)m * p.sas] : p.sa;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        v[r] = BKIND == B_E4M3 ? acc[i][j][r] * (sm * sn[r]) : acc[i][j][r] * sn[r];
+      OT* dst = c + (int64_t)m * p.ldc + nb;
+      if (nb + 3 < N && (p.ldc % 4) == 0) {
+        store4<OT>(dst, v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (nb + r < N) dst[r] = from_f32<OT>(v[r]);
+      }
+    }
+  }
+}
+
+template <int AKIND, int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN,
+          bool GROUPED>
+static int launch16(Mfma16Params p, hipStream_t st) {
+  p.n_tiles = (int)cdiv(p.N, BN);
+  const size_t lds = (size_t)2 * (BM + BN) * 8 * 16 + (BKIND == B_INT4 ? (size_t)2 * 2 * BN * 4 : 0);
+  auto kern = mfma16_gemm_kernel<AKIND, BKIND, MT, OT, BM, BN, WM, WN, GROUPED>;
+  static bool attr_set = false;  // raise the dynamic LDS limit once per instantiation
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return fail(MLS_ERR_HIP, "mfma16 GEMM: cannot reserve %zu bytes of LDS", lds);
+    attr_set = true;
+  }
+  const int64_t blocks = (int64_t)p.n_tiles * p.m_tiles;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, st, p);
+  return check_launch("mfma16 GEMM");
+}
+
+// Row-tile height for a dense GEMM: fewest (rounds of 256 blocks) x (BM + 128),
+// where the 128 stands for the per-tile cost of staging and widening the B tile,
+// which does not shrink with BM. Ties go to the taller tile.
+static int pick_bm(int64_t M, int64_t N, int max_bm) {
+  const int64_t nt = cdiv(N, 256);
+  int best = 16;
+  int64_t best_cost = INT64_MAX;
+  for (int bm = 16; bm <= max_bm; bm *= 2) {
+    if (bm > 16 && M <= bm / 2) break;
+    const int64_t cost = cdiv(nt * cdiv(M, bm), 256) * (bm + 128);
+    if (cost <= best_cost) {
+      best_cost = cost;
+      best = bm;
+    }
+  }
+  return best;
+}
+
+template <int AKIND, int BKIND, typename MT, typename OT>
+static int dense16(Mfma16Params p, hipStream_t st) {
+  constexpr int MAXBM = BKIND == B_INT4 ? 128 : 256;
+  const int bm = pick_bm(p.M, p.N, MAXBM);
+  p.m_tiles = (int)cdiv(p.M, bm);
+  switch (bm) {
+    case 256:
+      if constexpr (MAXBM >= 256) return launch16<AKIND, BKIND, MT, OT, 256, 256, 2, 2, false>(p, st);
+      else return MLS_ERR_UNSUPPORTED;
+    case 128: return launch16<AKIND, BKIND, MT, OT, 128, 256, 2, 2, false>(p, st);
+    case 64: return launch16<AKIND, BKIND, MT, OT, 64, 256, 1, 4, false>(p, st);
+    case 32: return launch16<AKIND, BKIND, MT, OT, 32, 256, 1, 4, false>(p, st);
+    default: return launch16<AKIND, BKIND, MT, OT, 16, 256, 1, 4, false>(p, st);
+  }
+}
+
+// One 256-row tile of each operand is addressed through a 32-bit buffer descriptor.
+static bool tile_fits(int64_t a_row_bytes, int64_t b_row_bytes) {
+  return a_row_bytes * 256 < (1ll << 31) && b_row_bytes * 256 < (1ll << 31);
+}
+
+int launch_gemm_wq_mfma(int wbits, const WqArgs& w) {
+  if (w.a_dt != MLS_F16 && w.a_dt != MLS_BF16) return MLS_ERR_UNSUPPORTED;
+  if (w.K % 64 != 0) return MLS_ERR_UNSUPPORTED;
+  if (wbits == 4 && w.group % 32 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(w.a, 16) || w.lda % 8 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(w.w, 16) || w.ldw % 16 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(w.c, 8)) return MLS_ERR_UNSUPPORTED;
+  if (w.M > 0x3FFFFFFF || w.N > 0x3FFFFFFF || w.K > 0x3FFFFFFF) return MLS_ERR_UNSUPPORTED;
+  if (!tile_fits(w.lda * 2, w.ldw)) return MLS_ERR_UNSUPPORTED;
+  Mfma16Params p{};
+  p.a = w.a; p.lda = w.lda; p.b = w.w; p.ldb = w.ldw;
+  p.s = w.s; p.s_dt = w.s_dt; p.ld_sn = w.ld_sn; p.ld_sg = w.ld_sg; p.group = w.group;
+  p.c = w.c; p.ldc = w.ldc; p.M = (int)w.M; p.N = (int)w.N; p.K = (int)w.K;
+  if (wbits == 4) {
+    return w.a_dt == MLS_BF16 ? dense16<A_RAW16, B_INT4, __bf16, __bf16>(p, w.stream)
+                              : dense16<A_RAW16, B_INT4, _Float16, _Float16>(p, w.stream);
+  }
+  return w.a_dt == MLS_BF16 ? dense16<A_RAW16, B_INT8, __bf16, __bf16>(p, w.stream)
+                            : dense16<A_RAW16, B_INT8, _Float16, _Float16>(p, w.stream);
+}
+
+int launch_grouped_int4(const GroupedArgs& g) {
+  const WqArgs& w = g.base;
+  if (w.a_dt != MLS_F16 && w.a_dt != MLS_BF16) return MLS_ERR_UNSUPPORTED;
+  if (w.K % 64 != 0 || w.group % 32 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(w.a, 16) || w.lda % 8 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(w.w, 16) || w.ldw % 16 != 0 || g.w_estride % 16 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(w.c, 8)) return MLS_ERR_UNSUPPORTED;
+  if (!tile_fits(w.lda * 2, w.ldw)) return MLS_ERR_UNSUPPORTED;
+  constexpr int BM = 128;
+  Mfma16Params p{};
+  p.a = w.a; p.lda = w.lda; p.b = w.w; p.ldb = w.ldw;
+  p.s = w.s; p.s_dt = w.s_dt; p.ld_sn = w.ld_sn; p.ld_sg = w.ld_sg; p.group = w.group;
+  p.c = w.c; p.ldc = w.ldc; p.M = (int)w.M; p.N = (int)w.N; p.K = (int)w.K;
+  p.seg_off = g.seg_off; p.E = g.E; p.b_estride = g.w_estride; p.s_estride = g.s_estride;
+  // upper bound on sum_e ceil(rows_e / BM) without reading the device offsets
+  p.m_tiles = (int)(cdiv(w.M, BM) + g.E);
+  return w.a_dt == MLS_BF16 ? launch16<A_RAW16, B_INT4, __bf16, __bf16, BM, 256, 2, 2, true>(p, w.stream)
+                            : launch16<A_RAW16, B_INT4, _Float16, _Float16, BM, 256, 2, 2, true>(p, w.stream);
+}
+
+int launch_fp8_exact(const Fp8Args& f) {
+  if (f.K % 64 != 0 || f.M < 16 || f.N < 16) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(f.a, 16) || !aligned(f.b, 16) || f.lda % 16 != 0 || f.ldb % 16 != 0)
+    return MLS_ERR_UNSUPPORTED;
+  if (!aligned(f.c, 16) || !tile_fits(f.lda, f.ldb)) return MLS_ERR_UNSUPPORTED;
+  if (f.M > 0x3FFFFFFF || f.N > 0x3FFFFFFF || f.K > 0x3FFFFFFF) return MLS_ERR_UNSUPPORTED;
+  Mfma16Params p{};
+  p.a = f.a; p.lda = f.lda; p.b = f.b; p.ldb = f.ldb;
+  p.sa = f.sa; p.sap = f.sap; p.sas = f.sas; p.sb = f.sb; p.sbp = f.sbp; p.sbs = f.sbs;
+  p.c = f.c; p.ldc = f.ldc; p.M = (int)f.M; p.N = (int)f.N; p.K = (int)f.K;
+  if (f.c_dt == MLS_F32) return dense16<A_E4M3, B_E4M3, __bf16, float>(p, f.stream);
+  if (f.c_dt == MLS_F16) return dense16<A_E4M3, B_E4M3, __bf16, _Float16>(p, f.stream);
+  return dense16<A_E4M3, B_E4M3, __bf16, __bf16>(p, f.stream);
+}
+
+}  // namespace mls

@@ -66,47 +66,36 @@ struct XSlot {
   static constexpr int NV = F32 ? KC : KC / 2;       // registers per chunk of x
 };
 
-// Loads the lane's x values for chunk c of row m (zeros when out of range) into
-// xr[NV] in the layout the dot products expect, and returns their sum.
+// Loads the lane's x values for chunk c (a valid chunk index) into xr[NV] in the
+// layout the dot products expect and returns their sum.
 template <int WBITS, typename AT>
-__device__ __forceinline__ float load_x_chunk(const AT* __restrict__ xrow, bool valid, int c,
-                                              uint32_t* xr) {
+__device__ __forceinline__ float load_x_chunk(const AT* __restrict__ xrow, int c, uint32_t* xr) {
   using S = XSlot<WBITS, AT>;
   constexpr int KC = S::KC;
   if constexpr (S::F32) {
     float sum = 0.0f;
-    if (valid) {
-      const float4* src = reinterpret_cast<const float4*>(xrow + (int64_t)c * KC);
+    const float4* src = reinterpret_cast<const float4*>(xrow + (int64_t)c * KC);
 #pragma unroll
-      for (int q = 0; q < KC / 4; ++q) {
-        const float4 v = src[q];
-        xr[4 * q + 0] = __float_as_uint(v.x);
-        xr[4 * q + 1] = __float_as_uint(v.y);
-        xr[4 * q + 2] = __float_as_uint(v.z);
-        xr[4 * q + 3] = __float_as_uint(v.w);
-        sum += (v.x + v.y) + (v.z + v.w);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < KC; ++q) xr[q] = 0u;
+    for (int q = 0; q < KC / 4; ++q) {
+      const float4 v = src[q];
+      xr[4 * q + 0] = __float_as_uint(v.x);
+      xr[4 * q + 1] = __float_as_uint(v.y);
+      xr[4 * q + 2] = __float_as_uint(v.z);
+      xr[4 * q + 3] = __float_as_uint(v.w);
+      sum += (v.x + v.y) + (v.z + v.w);
     }
     return sum;
   } else {
     using H = Half16<AT>;
     uint32_t d[KC / 2];
-    if (valid) {
-      const uint4* src = reinterpret_cast<const uint4*>(xrow + (int64_t)c * KC);
+    const uint4* src = reinterpret_cast<const uint4*>(xrow + (int64_t)c * KC);
 #pragma unroll
-      for (int q = 0; q < KC / 8; ++q) {
-        const uint4 v = src[q];
-        d[4 * q + 0] = v.x;
-        d[4 * q + 1] = v.y;
-        d[4 * q + 2] = v.z;
-        d[4 * q + 3] = v.w;
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < KC / 2; ++q) d[q] = 0u;
+    for (int q = 0; q < KC / 8; ++q) {
+      const uint4 v = src[q];
+      d[4 * q + 0] = v.x;
+      d[4 * q + 1] = v.y;
+      d[4 * q + 2] = v.z;
+      d[4 * q + 3] = v.w;
     }
     if constexpr (WBITS == 4) {
       // sub-block b holds k 8b..8b+7 as pairs (x0,x1)(x2,x3)(x4,x5)(x6,x7); the
@@ -192,10 +181,19 @@ constexpr float code_offset() {
   else return Half16<AT>::OFF4;
 }
 
-template <int WBITS, typename AT, int MT, int CPL, int R>
+template <typename ST>
+__device__ __forceinline__ float scale_value(const ST* s, int64_t i) {
+  return to_f32(s[i]);
+}
+
+// Every load is unconditional: indices past the matrix are clamped to valid rows
+// and chunks, so the loads are independent and all issue before the first wait.
+// Chunks past K contribute nothing (their term is selected away); rows past N or
+// M are computed on clamped data and never stored.
+template <int WBITS, typename AT, typename ST, int MT, int CPL, int R>
 __global__ __launch_bounds__(256) void gemv_wq_kernel(
     const AT* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw,
-    const void* __restrict__ s, int s_dt, int64_t ld_sn, int64_t ld_sg, int group,
+    const ST* __restrict__ s, int64_t ld_sn, int64_t ld_sg, int group,
     AT* __restrict__ y, int64_t ldy, int M, int N, int K) {
   using S = XSlot<WBITS, AT>;
   constexpr int KC = S::KC, NV = S::NV;
@@ -210,99 +208,129 @@ __global__ __launch_bounds__(256) void gemv_wq_kernel(
   float sc[R][CPL];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int n = n0 + r;
+    const int64_t n = min(n0 + r, N - 1);
+    const uint4* wrow = reinterpret_cast<const uint4*>(w + n * ldw);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const int c = lane + 64 * j;
-      const bool ok = n < N && c < nchunks;
-      wv[r][j] = ok ? reinterpret_cast<const uint4*>(w + (int64_t)n * ldw)[c] : make_uint4(0, 0, 0, 0);
+      const int c = min(lane + 64 * j, nchunks - 1);
+      wv[r][j] = wrow[c];
       if constexpr (WBITS == 4)
-        sc[r][j] = ok ? load_scale(s, s_dt, (int64_t)n * ld_sn + (int64_t)((c * KC) / group) * ld_sg)
-                      : 0.0f;
+        sc[r][j] = scale_value(s, n * ld_sn + (int64_t)((c * KC) / group) * ld_sg);
     }
   }
 
-  // 2. the lane's x slice for MT rows
+  // 2. the lane's x slice for MT rows (zeros past K)
   uint32_t xr[MT][CPL][NV];
   float osx[MT][CPL];
 #pragma unroll
   for (int mi = 0; mi < MT; ++mi) {
-    const int m = m0 + mi;
-    const AT* xrow = x + (int64_t)(m < M ? m : 0) * ldx;
+    const AT* xrow = x + (int64_t)min(m0 + mi, M - 1) * ldx;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = lane + 64 * j;
-      osx[mi][j] = OFF * load_x_chunk<WBITS, AT>(xrow, m < M && c < nchunks, c, xr[mi][j]);
+      osx[mi][j] = OFF * load_x_chunk<WBITS, AT>(xrow, min(c, nchunks - 1), xr[mi][j]);
     }
   }
 
   // 3. dot products
-  float part[MT][R];
+  float part[MT * R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
 #pragma unroll
-    for (int mi = 0; mi < MT; ++mi) part[mi][r] = 0.0f;
+    for (int mi = 0; mi < MT; ++mi) {
+      float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-#pragma unroll
-      for (int mi = 0; mi < MT; ++mi) {
-        const float d = chunk_dot<WBITS, AT>(wv[r][j], xr[mi][j]) - osx[mi][j];
-        if constexpr (WBITS == 4) part[mi][r] = fmaf(sc[r][j], d, part[mi][r]);
-        else part[mi][r] += d;
+      for (int j = 0; j < CPL; ++j) {
+        float d = chunk_dot<WBITS, AT>(wv[r][j], xr[mi][j]) - osx[mi][j];
+        if (64 * (j + 1) > nchunks && lane + 64 * j >= nchunks) d = 0.0f;  // past K
+        if constexpr (WBITS == 4) acc = fmaf(sc[r][j], d, acc);
+        else acc += d;
       }
+      part[mi * R + r] = acc;
     }
   }
 
-  // 4. reduce across the wavefront and store
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    const int n = n0 + r;
-    float sn = 1.0f;
-    if constexpr (WBITS == 8) sn = n < N ? load_scale(s, s_dt, n) : 0.0f;
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi) {
-      const float v = wave_sum(part[mi][r]);
-      const int m = m0 + mi;
-      if (lane == 0 && n < N && m < M) y[(int64_t)m * ldy + n] = from_f32<AT>(v * sn);
+  // 4. reduce all MT*R partials across the wavefront at once; lane L then holds
+  //    the total of partial L / (64 / (MT*R))
+  constexpr int V = MT * R;
+  wave_reduce_many<V>(part);
+  if (lane % (64 / V) == 0) {
+    const int idx = lane / (64 / V);
+    const int mi = idx / R, r = idx % R;
+    const int m = m0 + mi, n = n0 + r;
+    if (m < M && n < N) {
+      float v = part[0];
+      if constexpr (WBITS == 8) v *= scale_value(s, n);
+      y[(int64_t)m * ldy + n] = from_f32<AT>(v);
     }
   }
 }
 
-template <int WBITS, typename AT, int MT, int CPL>
-static void launch_one(const WqArgs& p) {
-  constexpr int R = CPL >= 8 ? 1 : 8 / CPL;
+template <int WBITS, typename AT, typename ST, int MT, int CPL, int R>
+static void launch_r(const WqArgs& p) {
   const dim3 grid((unsigned)cdiv(p.N, 4 * R), (unsigned)cdiv(p.M, MT));
-  hipLaunchKernelGGL((gemv_wq_kernel<WBITS, AT, MT, CPL, R>), grid, dim3(256), 0, p.stream,
-                     (const AT*)p.a, p.lda, p.w, p.ldw, p.s, p.s_dt, p.ld_sn, p.ld_sg, p.group,
+  hipLaunchKernelGGL((gemv_wq_kernel<WBITS, AT, ST, MT, CPL, R>), grid, dim3(256), 0, p.stream,
+                     (const AT*)p.a, p.lda, p.w, p.ldw, (const ST*)p.s, p.ld_sn, p.ld_sg, p.group,
                      (AT*)p.c, p.ldc, (int)p.M, (int)p.N, (int)p.K);
+}
+
+// Rows per wavefront: by default enough that each lane has 8 weight chunks in
+// flight (R * CPL = 8); MLS_GEMV_ROWS (1, 2, 4 or 8) overrides it for tuning.
+static int gemv_rows_override() {
+  static const int v = [] {
+    const char* e = getenv("MLS_GEMV_ROWS");
+    const int r = e ? atoi(e) : 0;
+    return (r == 1 || r == 2 || r == 4 || r == 8) ? r : 0;
+  }();
+  return v;
+}
+
+template <int WBITS, typename AT, typename ST, int MT, int CPL>
+static void launch_one(const WqArgs& p) {
+  constexpr int RDEF = CPL >= 8 ? 1 : 8 / CPL;
+  int r = gemv_rows_override();
+  if (r == 0 || MT * r > 32) r = RDEF;
+  switch (r) {
+    case 1: return launch_r<WBITS, AT, ST, MT, CPL, 1>(p);
+    case 2: return launch_r<WBITS, AT, ST, MT, CPL, 2>(p);
+    case 4: return launch_r<WBITS, AT, ST, MT, CPL, 4>(p);
+    default:
+      if constexpr (MT * 8 <= 32) return launch_r<WBITS, AT, ST, MT, CPL, 8>(p);
+      else return launch_r<WBITS, AT, ST, MT, CPL, RDEF>(p);
+  }
 }
 
 // Picks MT (rows of x per block) for a given CPL so that the x slice fits in
 // 128 registers: MT * CPL * NV <= 128.
-template <int WBITS, typename AT, int CPL>
+template <int WBITS, typename AT, typename ST, int CPL>
 static int dispatch_mt(const WqArgs& p) {
   constexpr int NV = XSlot<WBITS, AT>::NV;
   constexpr int MAXMT = 128 / (CPL * NV);
   if constexpr (MAXMT < 1) {
     return MLS_ERR_UNSUPPORTED;
   } else {
-    if (p.M == 1 || MAXMT < 2) launch_one<WBITS, AT, 1, CPL>(p);
-    else if (p.M == 2 || MAXMT < 4) launch_one<WBITS, AT, (MAXMT >= 2 ? 2 : 1), CPL>(p);
-    else launch_one<WBITS, AT, (MAXMT >= 4 ? 4 : 1), CPL>(p);
+    if (p.M == 1 || MAXMT < 2) launch_one<WBITS, AT, ST, 1, CPL>(p);
+    else if (p.M == 2 || MAXMT < 4) launch_one<WBITS, AT, ST, (MAXMT >= 2 ? 2 : 1), CPL>(p);
+    else launch_one<WBITS, AT, ST, (MAXMT >= 4 ? 4 : 1), CPL>(p);
     return MLS_OK;
   }
 }
 
-template <int WBITS, typename AT>
+template <int WBITS, typename AT, typename ST>
 static int dispatch_cpl(const WqArgs& p) {
   constexpr int KC = XSlot<WBITS, AT>::KC;
   const int64_t cpl = cdiv(p.K / KC, 64);
-  if (cpl <= 1) return dispatch_mt<WBITS, AT, 1>(p);
-  if (cpl <= 2) return dispatch_mt<WBITS, AT, 2>(p);
-  if (cpl <= 4) return dispatch_mt<WBITS, AT, 4>(p);
-  if (cpl <= 8) return dispatch_mt<WBITS, AT, 8>(p);
-  if (cpl <= 16) return dispatch_mt<WBITS, AT, 16>(p);
+  if (cpl <= 1) return dispatch_mt<WBITS, AT, ST, 1>(p);
+  if (cpl <= 2) return dispatch_mt<WBITS, AT, ST, 2>(p);
+  if (cpl <= 4) return dispatch_mt<WBITS, AT, ST, 4>(p);
+  if (cpl <= 8) return dispatch_mt<WBITS, AT, ST, 8>(p);
+  if (cpl <= 16) return dispatch_mt<WBITS, AT, ST, 16>(p);
   return MLS_ERR_UNSUPPORTED;
+}
+
+template <int WBITS, typename AT>
+static int dispatch_st(const WqArgs& p) {
+  return p.s_dt == MLS_F16 ? dispatch_cpl<WBITS, AT, _Float16>(p) : dispatch_cpl<WBITS, AT, float>(p);
 }
 
 int launch_gemv_wq(int wbits, const WqArgs& p) {
@@ -314,13 +342,13 @@ int launch_gemv_wq(int wbits, const WqArgs& p) {
   if (!aligned(p.a, 16) || (p.lda * esz) % 16 != 0) return MLS_ERR_UNSUPPORTED;
   if (p.N > 0x7FFFFFFF / 2 || p.M > 4 * 65535) return MLS_ERR_UNSUPPORTED;  // grid.y = M / MT
   if (wbits == 4) {
-    if (p.a_dt == MLS_F32) return dispatch_cpl<4, float>(p);
-    if (p.a_dt == MLS_F16) return dispatch_cpl<4, _Float16>(p);
-    return dispatch_cpl<4, __bf16>(p);
+    if (p.a_dt == MLS_F32) return dispatch_st<4, float>(p);
+    if (p.a_dt == MLS_F16) return dispatch_st<4, _Float16>(p);
+    return dispatch_st<4, __bf16>(p);
   }
-  if (p.a_dt == MLS_F32) return dispatch_cpl<8, float>(p);
-  if (p.a_dt == MLS_F16) return dispatch_cpl<8, _Float16>(p);
-  return dispatch_cpl<8, __bf16>(p);
+  if (p.a_dt == MLS_F32) return dispatch_st<8, float>(p);
+  if (p.a_dt == MLS_F16) return dispatch_st<8, _Float16>(p);
+  return dispatch_st<8, __bf16>(p);
 }
 
 // ------------------------------------------------------------------ generic path

@@ -42,4 +42,26 @@ struct GroupedArgs {
 };
 int launch_grouped_int4(const GroupedArgs& p);
 
+// e4m3 x e4m3 GEMM arguments (scales: pointer with a row stride, or the scalar).
+struct Fp8Args {
+  const uint8_t* a;
+  int64_t lda;
+  const uint8_t* b;
+  int64_t ldb;
+  float sa;
+  const float* sap;
+  int64_t sas;
+  float sb;
+  const float* sbp;
+  int64_t sbs;
+  void* c;
+  int c_dt;
+  int64_t ldc;
+  int64_t M, N, K;
+  hipStream_t stream;
+};
+
+// Exact e4m3 GEMM: operands widened to bf16 on the way into LDS, bf16 MFMA.
+int launch_fp8_exact(const Fp8Args& f);
+
 }  // namespace mls

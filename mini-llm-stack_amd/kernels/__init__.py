@@ -24,6 +24,7 @@ LIB_PATH = Path(os.environ.get("MLS_LIB") or
 
 MLS_F32, MLS_F16, MLS_BF16 = 0, 1, 2
 MLS_OK, MLS_ERR_ARG, MLS_ERR_UNSUPPORTED, MLS_ERR_HIP = 0, -1, -2, -3
+MLS_FP8_NATIVE = 1
 
 _LIB = None
 
@@ -43,7 +44,7 @@ SIGNATURES = {
                        _I64, _I64, _I64, _P], _I),
     "mls_int8_dgrad": ([_P, _I, _I64, _P, _I64, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P], _I),
     "mls_fp8_gemm": ([_P, _I64, _P, _I64, _F, _P, _I64, _F, _P, _I64, _P, _I, _I64,
-                      _I64, _I64, _I64, _P], _I),
+                      _I64, _I64, _I64, _I, _P], _I),
     "mls_int4_grouped_gemm": ([_P, _I, _I64, _P, _I, _I64, _P, _I64, _I64, _P, _I, _I64,
                                _I64, _I64, _I, _P, _I, _I64, _I64, _I64, _P], _I),
 }

@@ -80,14 +80,16 @@ def test_zero_sized_calls_are_noops():
     L = kernels.load_library()
     assert L.mls_int8_gemm(NULL, 0, 0, NULL, 0, NULL, 0, NULL, 0, 0, 0, 5, 5, NULL) == 0
     assert L.mls_e4m3_decode(NULL, NULL, 0, NULL) == 0
-    assert L.mls_fp8_gemm(NULL, 0, NULL, 0, 1.0, NULL, 0, 1.0, NULL, 0, NULL, 0, 0, 0, 0, 8, NULL) == 0
+    assert L.mls_fp8_gemm(NULL, 0, NULL, 0, 1.0, NULL, 0, 1.0, NULL, 0, NULL, 0, 0, 0, 0, 8, 0, NULL) == 0
 
 
 def test_fp8_and_codec_reject():
     L = kernels.load_library()
-    assert L.mls_fp8_gemm(1, 64, 1, 64, 1.0, NULL, 0, 1.0, NULL, 0, 1, 9, 8, 4, 8, 64, NULL) == \
+    assert L.mls_fp8_gemm(1, 64, 1, 64, 1.0, NULL, 0, 1.0, NULL, 0, 1, 9, 8, 4, 8, 64, 0, NULL) == \
         kernels.MLS_ERR_ARG
-    assert L.mls_fp8_gemm(1, 32, 1, 64, 1.0, NULL, 0, 1.0, NULL, 0, 1, 0, 8, 4, 8, 64, NULL) == \
+    assert L.mls_fp8_gemm(1, 32, 1, 64, 1.0, NULL, 0, 1.0, NULL, 0, 1, 0, 8, 4, 8, 64, 0, NULL) == \
+        kernels.MLS_ERR_ARG
+    assert L.mls_fp8_gemm(1, 64, 1, 64, 1.0, NULL, 0, 1.0, NULL, 0, 1, 0, 8, 4, 8, 64, 4, NULL) == \
         kernels.MLS_ERR_ARG
     assert L.mls_e4m3_decode(1, 1, -3, NULL) == kernels.MLS_ERR_ARG
     assert L.mls_e4m3_encode(1, 5, 2, 2, 2, 1.0, NULL, 0, 1, 2, NULL) == kernels.MLS_ERR_ARG

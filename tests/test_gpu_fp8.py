@@ -1,4 +1,10 @@
-"""gfx950 e4m3 GEMM (native fp8 MFMA) vs the decode-then-fp32-matmul oracle."""
+"""gfx950 e4m3 GEMM vs the decode-then-fp32-matmul oracle.
+
+The default datapath (bf16 MFMA on exactly widened operands) is held to the
+BASELINE tolerances. The native fp8-MFMA datapath (native=True) adds each group of
+8 products with 13 bits below the largest, rounding toward -inf: it is held to the
+same tolerance on data without outliers, to |Δ| <= 2^-9 max(|ref|, rms(ref)) on
+outlier-heavy data, and its group rounding is pinned by a known-answer test."""
 
 from __future__ import annotations
 
@@ -52,42 +58,64 @@ def _operands(M, N, K, seed, per_row, outliers=False):
     return ab, bb, sa, sb
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 96, 128), (256, 256, 256), (300, 200, 384), (1024, 512, 1024)])
+@pytest.mark.parametrize("native", [False, True])
+@pytest.mark.parametrize("M,N,K", [(64, 96, 128), (256, 256, 256), (300, 200, 384), (1024, 512, 1024),
+                                   (17, 33, 192)])
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16])
-def test_mfma_path(dev, M, N, K, out_dtype):
+def test_mfma_paths(dev, M, N, K, out_dtype, native):
     ab, bb, sa, sb = _operands(M, N, K, M + N + K, per_row=False)
-    out = fp8_matmul(ab.to(dev), bb.to(dev), sa, sb, out_dtype=out_dtype)
+    out = fp8_matmul(ab.to(dev), bb.to(dev), sa, sb, out_dtype=out_dtype, native=native)
     assert out.dtype == out_dtype
-    _check(out, ref.fp8_matmul(ab.numpy(), bb.numpy(), sa, sb), f"fp8 {M}x{N}x{K}")
+    _check(out, ref.fp8_matmul(ab.numpy(), bb.numpy(), sa, sb), f"fp8 {M}x{N}x{K} native={native}")
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 96, 128), (300, 200, 384), (5, 7, 48)])
-def test_per_row_scales(dev, M, N, K):
+def test_per_row_scales_with_outliers(dev, M, N, K):
     ab, bb, sa, sb = _operands(M, N, K, 3 * M + N, per_row=True, outliers=True)
+    want = ref.fp8_matmul(ab.numpy(), bb.numpy(), sa.numpy(), sb.numpy())
     out = fp8_matmul(ab.to(dev), bb.to(dev), sa.to(dev), sb.to(dev), out_dtype=torch.float32)
-    _check(out, ref.fp8_matmul(ab.numpy(), bb.numpy(), sa.numpy(), sb.numpy()), "per-row")
+    _check(out, want, "per-row exact")
+    nat = fp8_matmul(ab.to(dev), bb.to(dev), sa.to(dev), sb.to(dev), out_dtype=torch.float32, native=True)
+    ok, worst = ref.close_fp32(nat.cpu().numpy(), want)
+    assert ok, f"per-row native: worst {worst:.3g}"
 
 
-def test_zero_dim_tensor_scales(dev):
-    ab, bb, sa, sb = _operands(128, 128, 256, 1, per_row=False)
-    out = fp8_matmul(ab.to(dev), bb.to(dev), torch.tensor(sa, device=dev), torch.tensor(sb, device=dev))
-    _check(out, ref.fp8_matmul(ab.numpy(), bb.numpy(), sa, sb), "0-d scales")
+def test_exact_path_widens_every_byte(dev):
+    """Every finite e4m3 byte goes through the hardware e4m3 -> bf16 widening of the
+    exact datapath: A = the 254 finite bytes, B = identity, C = their values."""
+    codes = np.array([b for b in range(256) if b & 0x7F != 0x7F], dtype=np.uint8)
+    K = 256
+    a = np.zeros((64, K), np.uint8)
+    a[0, :len(codes)] = codes
+    b = np.zeros((K, K), np.uint8)
+    b[np.arange(K), np.arange(K)] = 0x38                        # e4m3 1.0
+    out = fp8_matmul(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), 1.0, 1.0)
+    got = out[0, :len(codes)].cpu().numpy()
+    assert np.array_equal(got, ref.e4m3_decode(codes))   # -0.0 sums to +0.0
 
 
-def test_quantize_then_matmul_on_device(dev):
-    """quantize_e4m3 on the device feeds fp8_matmul (the FP8Linear forward)."""
-    g = torch.Generator().manual_seed(4)
-    a, b = torch.randn(128, 256, generator=g), torch.randn(192, 256, generator=g)
-    sa, sb = float(a.abs().amax()) / E4M3_MAX, float(b.abs().amax()) / E4M3_MAX
-    ab, bb = quantize_e4m3(a.to(dev), sa), quantize_e4m3(b.to(dev), sb)
-    assert np.array_equal(ab.cpu().numpy(), ref.quantize_e4m3(a.numpy(), sa))
-    _check(fp8_matmul(ab, bb, sa, sb), ref.fp8_matmul(ab.cpu().numpy(), bb.cpu().numpy(), sa, sb), "q+mm")
+def test_native_group_rounding_known_answer(dev):
+    """The fp8 MFMA adds 8 consecutive products with 13 bits below the largest,
+    toward -inf: 256*256 + 1*1 in one group loses the 1; in the next group it survives.
+    The default datapath keeps it."""
+    K = 128
+
+    def operand(j):
+        a = np.zeros((64, K), np.float32)
+        a[:, 0], a[:, j] = 256.0, 1.0
+        return torch.from_numpy(ref.e4m3_encode(a)).to(dev)
+
+    def native(j):
+        x = operand(j)
+        return float(fp8_matmul(x, x, 1.0, 1.0, native=True)[0, 0])
+
+    assert native(1) == 65536.0 and native(7) == 65536.0
+    assert native(8) == 65537.0
+    x = operand(1)
+    assert float(fp8_matmul(x, x, 1.0, 1.0)[0, 0]) == 65537.0
 
 
-def test_config_d(dev):
-    """BASELINE configs[3]: A [4096, 8192], B [8192, 8192], 1% outliers x20, per-row
-    e4m3 scales, bf16 output; every output vs torch fp32 matmul of the decoded operands,
-    sampled rows vs the CPU oracle."""
+def _config_d(dev):
     M, N, K = 4096, 8192, 8192
     g = torch.Generator(device=dev).manual_seed(0)
     a = torch.randn(M, K, generator=g, device=dev)
@@ -100,12 +128,32 @@ def test_config_d(dev):
     sb = b.abs().amax(dim=1) / E4M3_MAX
     bb = quantize_e4m3(b, sb[:, None])
     del b
-    out = fp8_matmul(ab, bb, sa, sb, out_dtype=torch.bfloat16)
     da = ab.view(torch.float8_e4m3fn).float()
     db = bb.view(torch.float8_e4m3fn).float()
     want = (da @ db.t().contiguous()) * (sa[:, None] * sb[None, :])
-    err = (out.float() - want).abs() - (1e-2 + 1e-2 * want.abs())
-    assert float(err.max()) <= 0, f"config D worst excess {float(err.max()):.3g}"
+    return ab, bb, sa, sb, want
+
+
+def test_config_d(dev):
+    """BASELINE configs[3]: A [4096, 8192], B [8192, 8192], 1% outliers x20, per-row
+    e4m3 scales, bf16 output; every output vs torch fp32 matmul of the decoded operands
+    (rtol = atol = 1e-2), sampled rows vs the CPU oracle."""
+    ab, bb, sa, sb, want = _config_d(dev)
+    out = fp8_matmul(ab, bb, sa, sb, out_dtype=torch.bfloat16)
     rows = [0, 2049, 4095]
     _check(out[rows], ref.fp8_matmul(ab[rows].cpu().numpy(), bb.cpu().numpy(), sa[rows].cpu().numpy(),
                                      sb.cpu().numpy()), "config D rows")
+    err = (out.float() - want).abs() - (1e-2 + 1e-2 * want.abs())
+    worst = int(err.argmax())
+    m, n = divmod(worst, want.shape[1])
+    assert float(err.max()) <= 0, (f"config D worst excess {float(err.max()):.3g} at ({m}, {n}): "
+                                   f"out {float(out[m, n]):.6g} want {float(want[m, n]):.6g}")
+
+
+def test_config_d_native_error_bound(dev):
+    """Config D on the fp8 matrix cores: within 2^-9 max(|ref|, rms(ref)) everywhere."""
+    ab, bb, sa, sb, want = _config_d(dev)
+    out = fp8_matmul(ab, bb, sa, sb, out_dtype=torch.float32, native=True)
+    rms = float(want.pow(2).mean().sqrt())
+    excess = (out - want).abs() - 2.0 ** -9 * torch.maximum(want.abs(), torch.tensor(rms, device=dev))
+    assert float(excess.max()) <= 0, f"native config D excess {float(excess.max()):.3g} (rms {rms:.4g})"

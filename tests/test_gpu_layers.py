@@ -18,7 +18,7 @@ torch.backends.cuda.matmul.allow_tf32 = False
 
 
 def _close(out, want, what):
-    o, w = out.float().cpu().numpy(), want.float().cpu().numpy()
+    o, w = out.detach().float().cpu().numpy(), want.detach().float().cpu().numpy()
     ok, worst = ref.close_fp32(o, w) if out.dtype == torch.float32 else ref.close_bf16(o, w)
     assert ok, f"{what}: worst {worst:.3g}"
 
