@@ -12,7 +12,8 @@ HIP events; value = algorithmic bytes x K / elapsed.
 
 The other BASELINE configs (INT4 M = 4 / 16, the INT8 GEMV target, INT8 prefill,
 FP8 e4m3 GEMM, INT4 MoE grouped GEMM) are reported under "extra" with the same
-protocol. cpu_baseline times the reference's CPU algorithm (the numpy
+protocol, followed by a 256 MiB streaming copy (the bandwidth a plain elementwise
+kernel reaches on this GPU). cpu_baseline times the reference's CPU algorithm (the numpy
 restatement in oracle/: dequantize, then fp32 matmul) on the host for a bounded
 sample of the headline workload.
 """
@@ -189,6 +190,20 @@ def moe_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=128):
                 counts=counts.tolist())
 
 
+def copy_calibration(dev, steps: int, warmup: int, nbytes: int = 256 << 20):
+    """A plain streaming kernel of known traffic (torch's elementwise bitwise_not over
+    int32: reads nbytes, writes nbytes). Its rocprofv3 FETCH_SIZE / WRITE_SIZE
+    readings calibrate those counters to bytes, and its rate is the HBM bandwidth a
+    simple streaming kernel reaches on this GPU."""
+    import torch
+    copies = 4
+    srcs = [torch.full((nbytes // 4,), i + 1, dtype=torch.int32, device=dev) for i in range(copies)]
+    dst = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+    fns = [lambda s=s: torch.bitwise_not(s, out=dst) for s in srcs]
+    ms = time_steps(fns, warmup, steps)
+    return dict(ms=ms, bytes=2 * nbytes, flops=0, copies=copies)
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 
@@ -268,7 +283,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--only", default=None,
                     help="run one workload: int4_gemv, int4_m4, int4_m16, int8_gemv, int8_prefill, "
-                         "fp8_gemm, fp8_native, moe_int4")
+                         "fp8_gemm, fp8_native, moe_int4, copy (counter calibration)")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
@@ -304,6 +319,7 @@ def main(argv=None) -> int:
                                                      r["bytes"] / (r["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                                   "segments": r["counts"]}))(
             moe_int4(dev, small, 4)),
+        "copy": lambda: _hbm_row("copy_256MiB", copy_calibration(dev, small, 4)),
     }
     if args.only:
         log(f"running {args.only}")
@@ -318,7 +334,7 @@ def main(argv=None) -> int:
     extra = []
     if not args.no_extra:
         for k in ("int4_m4", "int4_m16", "int8_gemv", "int8_prefill", "fp8_gemm", "fp8_native",
-                  "moe_int4"):
+                  "moe_int4", "copy"):
             log(f"{k} ...")
             row = runners[k]()
             log(json.dumps(row))
