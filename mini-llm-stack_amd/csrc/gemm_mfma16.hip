@@ -8,11 +8,12 @@
 // fp32 summation order. (gfx950's fp8 MFMAs instead add each group of 8 products
 // with 13 bits below the largest, rounding toward -inf: gemm_fp8.hip.)
 //
-// Block tile BM (rows m of A) x BN (rows n of B) x 64 (k), 256 threads as WM x WN
-// wavefronts. Per k-stage every thread prefetches its share of the next stage
-// (16-byte buffer loads; rows past the tile's valid range read as zeros) into
-// registers, runs the MFMAs of the current stage out of LDS, widens its
-// prefetched chunks to 16-bit floats (INT8: exact integers; INT4: exact v - 8;
+// Block tile BM (rows m of A) x BN (rows n of B) x 64 (k), WM x WN wavefronts (4, or
+// 8 = two per SIMD so that one wavefront's memory waits overlap the other's MFMAs).
+// Per k-stage every thread issues the loads of its share of the stage after next
+// (16-byte buffer loads; rows past the tile's valid range read as zeros) into one of
+// two register sets, runs the MFMAs of the current stage out of LDS, widens the
+// chunks of the next stage (loaded one stage earlier) to 16-bit floats (INT8: exact integers; INT4: exact v - 8;
 // e4m3: exact values via v_cvt_scalef32_pk_bf16_fp8) and stores them into the other
 // LDS buffer; one barrier per stage. LDS rows are 64 k = 128 bytes; the 16-byte
 // chunk index is XOR-ed with row & 7, which measured free of bank conflicts on
@@ -122,20 +123,22 @@ __device__ __forceinline__ void widen_e4m3(const uint4& q, uint32_t* o) {
 }
 
 template <int AKIND, int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN,
-          bool GROUPED>
-__global__ __launch_bounds__(256) void mfma16_gemm_kernel(const Mfma16Params p) {
+          bool GROUPED, bool DEEP>
+__global__ __launch_bounds__(64 * WM * WN) void mfma16_gemm_kernel(const Mfma16Params p) {
   constexpr int BK = 64;
+  constexpr int NT = 64 * WM * WN;             // threads per block
   constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
   constexpr int TM = WTM / 16, TN = WTN / 16;  // MFMA tiles per wave
-  static_assert(WM * WN == 4 && TM >= 1 && TN >= 1, "bad wave layout");
+  static_assert((WM * WN == 4 || WM * WN == 8) && TM >= 1 && TN >= 1, "bad wave layout");
   constexpr int A_ESZ = AKIND == A_RAW16 ? 2 : 1;
   constexpr int A_CPR = BK * A_ESZ / 16;                  // 16-byte chunks per row per stage
   constexpr int B_CPR = BKIND == B_INT4 ? 2 : 4;
   constexpr int A_CH = BM * A_CPR, B_CH = BN * B_CPR;
-  constexpr int A_PT = (A_CH + 255) / 256;
-  static_assert(B_CH % 256 == 0, "BN too small for the weight staging");
-  constexpr int B_PT = B_CH / 256;
-  constexpr int A_RSTEP = 256 / A_CPR, B_RSTEP = 256 / B_CPR;
+  constexpr int A_PT = (A_CH + NT - 1) / NT;
+  static_assert(B_CH % NT == 0, "BN too small for the weight staging");
+  static_assert(!(BKIND == B_INT4) || BN <= NT, "one thread per group scale");
+  constexpr int B_PT = B_CH / NT;
+  constexpr int A_RSTEP = NT / A_CPR, B_RSTEP = NT / B_CPR;
   constexpr bool GS = BKIND == B_INT4;  // group scales on fp32 partial sums
 
   extern __shared__ __align__(16) uint8_t smem[];
@@ -188,13 +191,18 @@ __global__ __launch_bounds__(256) void mfma16_gemm_kernel(const Mfma16Params p) 
   for (int i = 0; i < A_PT; ++i) a_off[i] = (a_row0 + A_RSTEP * i) * (int)p.lda * A_ESZ + a_cc * 16;
 #pragma unroll
   for (int i = 0; i < B_PT; ++i) b_off[i] = (b_row0 + B_RSTEP * i) * (int)p.ldb + b_cc * 16;
-  const bool a_on = A_CH >= 256 || tid < A_CH;
+  const bool a_on = A_CH >= NT || tid < A_CH;
   const int64_t s_row = (int64_t)min(n0 + tid, N - 1) * p.ld_sn;
 
-  uint4 ra[A_PT], rb[B_PT];
-  float rs0 = 0.f, rs1 = 0.f;
+  // DEEP: two register sets of prefetched chunks; the loads of stage s go to set s & 1
+  // two stages before the stage is computed, so every load has two stages of MFMA work
+  // to arrive in. Otherwise one set, loaded one stage ahead (for tiles whose
+  // accumulators leave no room for a second set).
+  uint4 ra0[A_PT], rb0[B_PT], ra1[A_PT], rb1[B_PT];
+  float rs00 = 0.f, rs01 = 0.f, rs10 = 0.f, rs11 = 0.f;
 
-  auto load = [&](int k0) __attribute__((always_inline)) {
+  auto load = [&](uint4 (&ra)[A_PT], uint4 (&rb)[B_PT], float& rs0, float& rs1, int k0)
+      __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < A_PT; ++i)
       if (a_on)
@@ -205,12 +213,14 @@ __global__ __launch_bounds__(256) void mfma16_gemm_kernel(const Mfma16Params p) 
           uint4, __builtin_amdgcn_raw_buffer_load_b128(rsb, b_off[i], BKIND == B_INT4 ? k0 / 2 : k0, 0));
     if constexpr (GS) {
       if (tid < BN) {
-        rs0 = scale_at(smat, p.s_dt, s_row + (int64_t)(k0 / p.group) * p.ld_sg);
-        rs1 = scale_at(smat, p.s_dt, s_row + (int64_t)((k0 + 32) / p.group) * p.ld_sg);
+        const int kc = min(k0, p.K - BK);  // a stage past the end reuses the last scales
+        rs0 = scale_at(smat, p.s_dt, s_row + (int64_t)(kc / p.group) * p.ld_sg);
+        rs1 = scale_at(smat, p.s_dt, s_row + (int64_t)((kc + 32) / p.group) * p.ld_sg);
       }
     }
   };
-  auto store = [&](int buf) __attribute__((always_inline)) {
+  auto store = [&](const uint4 (&ra)[A_PT], const uint4 (&rb)[B_PT], float rs0, float rs1, int buf)
+      __attribute__((always_inline)) {
     uint4* as = As + buf * BM * 8;
     uint4* bs = Bs + buf * BN * 8;
 #pragma unroll
@@ -265,20 +275,13 @@ __global__ __launch_bounds__(256) void mfma16_gemm_kernel(const Mfma16Params p) 
       for (int j = 0; j < TM; ++j) accg[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  const int nk = p.K / BK;
-  load(0);
-  store(0);
-  __syncthreads();
-
   const int lr = lane & 15, lk = lane >> 4;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    const int k0 = kt * BK;
-    if (kt + 1 < nk) load(k0 + BK);
+  // MFMAs of one stage out of LDS buffer `buf` (k0 = first k of the stage)
+  auto compute = [&](int buf, int k0, int ks_lo = 0, int ks_hi = 2) __attribute__((always_inline)) {
     const uint4* as = As + buf * BM * 8;
     const uint4* bs = Bs + buf * BN * 8;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = ks_lo; ks < ks_hi; ++ks) {
       const int ch = ks * 4 + lk;
       uint4 bop[TN], aop[TM];
 #pragma unroll
@@ -318,8 +321,46 @@ __global__ __launch_bounds__(256) void mfma16_gemm_kernel(const Mfma16Params p) 
           for (int j = 0; j < TM; ++j) acc[i][j] = Mfma16<MT>::mma(bop[i], aop[j], acc[i][j]);
       }
     }
-    if (kt + 1 < nk) store(buf ^ 1);
+  };
+
+  // Stage s is computed from LDS buffer s & 1, filled at the end of stage s - 1.
+  const int nk = p.K / BK;
+  if constexpr (DEEP) {
+    // register set s & 1 holds stage s; the loads of stage s + 2 are issued at the start of s
+    load(ra0, rb0, rs00, rs01, 0);
+    if (nk > 1) load(ra1, rb1, rs10, rs11, BK);
+    store(ra0, rb0, rs00, rs01, 0);
     __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+      if (kt + 2 < nk) load(ra0, rb0, rs00, rs01, (kt + 2) * BK);
+      compute(0, kt * BK);
+      if (kt + 1 < nk) store(ra1, rb1, rs10, rs11, 1);
+      __syncthreads();
+      if (kt + 1 >= nk) break;
+      if (kt + 3 < nk) load(ra1, rb1, rs10, rs11, (kt + 3) * BK);
+      compute(1, (kt + 1) * BK);
+      if (kt + 2 < nk) store(ra0, rb0, rs00, rs01, 0);
+      __syncthreads();
+    }
+  } else {
+    // The next stage's chunks are widened and stored between the two k-halves of the
+    // current stage, so that work overlaps the MFMAs still in flight instead of
+    // running alone before the barrier. The loads and the store run unconditionally:
+    // in the last stage they fetch k >= K (buffer loads return zeros past the
+    // operand, group-scale indices are clamped) into the buffer nobody reads again.
+    load(ra0, rb0, rs00, rs01, 0);
+    store(ra0, rb0, rs00, rs01, 0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int buf = kt & 1;
+      load(ra0, rb0, rs00, rs01, (kt + 1) * BK);
+      compute(buf, kt * BK, 0, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      store(ra0, rb0, rs00, rs01, buf ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(buf, kt * BK, 1, 2);
+      __syncthreads();
+    }
   }
 
   // ---- epilogue: acc[i][j][r] = C[m = m0+wm0+16j+lr][n = n0+wn0+16i+4lk+r]
@@ -356,12 +397,20 @@ __global__ __launch_bounds__(256) void mfma16_gemm_kernel(const Mfma16Params p) 
   }
 }
 
+// Two stages of register prefetch where the accumulators leave room for them: 8-wave
+// blocks (two wavefronts per SIMD, 256 registers each) with at most 64 x 64 wave tiles.
+template <int BM, int BN, int WM, int WN>
+constexpr bool deep_prefetch() {
+  return WM * WN == 8 && (BM / WM) * (BN / WN) <= 64 * 64;
+}
+
 template <int AKIND, int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN,
           bool GROUPED>
 static int launch16(Mfma16Params p, hipStream_t st) {
   p.n_tiles = (int)cdiv(p.N, BN);
   const size_t lds = (size_t)2 * (BM + BN) * 8 * 16 + (BKIND == B_INT4 ? (size_t)2 * 2 * BN * 4 : 0);
-  auto kern = mfma16_gemm_kernel<AKIND, BKIND, MT, OT, BM, BN, WM, WN, GROUPED>;
+  auto kern = mfma16_gemm_kernel<AKIND, BKIND, MT, OT, BM, BN, WM, WN, GROUPED,
+                                 deep_prefetch<BM, BN, WM, WN>()>;
   static bool attr_set = false;  // raise the dynamic LDS limit once per instantiation
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -370,7 +419,7 @@ static int launch16(Mfma16Params p, hipStream_t st) {
     attr_set = true;
   }
   const int64_t blocks = (int64_t)p.n_tiles * p.m_tiles;
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, st, p);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * WM * WN), lds, st, p);
   return check_launch("mfma16 GEMM");
 }
 
@@ -392,16 +441,34 @@ static int pick_bm(int64_t M, int64_t N, int max_bm) {
   return best;
 }
 
+// Tuning overrides for sweeps: MLS_MFMA_WAVES = 4 or 8 wavefronts per block (default 8:
+// two per SIMD, so one wavefront's memory waits overlap the other's MFMAs), MLS_MFMA_BM =
+// forced row-tile height (16 .. 256).
+static int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
+
 template <int AKIND, int BKIND, typename MT, typename OT>
 static int dense16(Mfma16Params p, hipStream_t st) {
   constexpr int MAXBM = BKIND == B_INT4 ? 128 : 256;
-  const int bm = pick_bm(p.M, p.N, MAXBM);
+  static const int waves = env_int("MLS_MFMA_WAVES", 8);
+  static const int force_bm = env_int("MLS_MFMA_BM", 0);
+  int bm = pick_bm(p.M, p.N, MAXBM);
+  if (force_bm >= 16 && force_bm <= MAXBM && (force_bm & (force_bm - 1)) == 0) bm = force_bm;
   p.m_tiles = (int)cdiv(p.M, bm);
+  const bool w8 = waves == 8;
   switch (bm) {
     case 256:
-      if constexpr (MAXBM >= 256) return launch16<AKIND, BKIND, MT, OT, 256, 256, 2, 2, false>(p, st);
-      else return MLS_ERR_UNSUPPORTED;
-    case 128: return launch16<AKIND, BKIND, MT, OT, 128, 256, 2, 2, false>(p, st);
+      if constexpr (MAXBM >= 256) {
+        return w8 ? launch16<AKIND, BKIND, MT, OT, 256, 256, 2, 4, false>(p, st)
+                  : launch16<AKIND, BKIND, MT, OT, 256, 256, 2, 2, false>(p, st);
+      } else {
+        return MLS_ERR_UNSUPPORTED;
+      }
+    case 128:
+      return w8 ? launch16<AKIND, BKIND, MT, OT, 128, 256, 2, 4, false>(p, st)
+                : launch16<AKIND, BKIND, MT, OT, 128, 256, 2, 2, false>(p, st);
     case 64: return launch16<AKIND, BKIND, MT, OT, 64, 256, 1, 4, false>(p, st);
     case 32: return launch16<AKIND, BKIND, MT, OT, 32, 256, 1, 4, false>(p, st);
     default: return launch16<AKIND, BKIND, MT, OT, 16, 256, 1, 4, false>(p, st);
@@ -450,6 +517,10 @@ int launch_grouped_int4(const GroupedArgs& g) {
   p.seg_off = g.seg_off; p.E = g.E; p.b_estride = g.w_estride; p.s_estride = g.s_estride;
   // upper bound on sum_e ceil(rows_e / BM) without reading the device offsets
   p.m_tiles = (int)(cdiv(w.M, BM) + g.E);
+  static const bool w8 = env_int("MLS_MFMA_WAVES", 8) == 8;
+  if (w8)
+    return w.a_dt == MLS_BF16 ? launch16<A_RAW16, B_INT4, __bf16, __bf16, BM, 256, 2, 4, true>(p, w.stream)
+                              : launch16<A_RAW16, B_INT4, _Float16, _Float16, BM, 256, 2, 4, true>(p, w.stream);
   return w.a_dt == MLS_BF16 ? launch16<A_RAW16, B_INT4, __bf16, __bf16, BM, 256, 2, 2, true>(p, w.stream)
                             : launch16<A_RAW16, B_INT4, _Float16, _Float16, BM, 256, 2, 2, true>(p, w.stream);
 }
