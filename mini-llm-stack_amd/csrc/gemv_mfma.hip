@@ -1,0 +1,287 @@
+// Skinny weight-only GEMM (2 <= M <= 16, 16-bit activations) on the 16-bit MFMA.
+//
+// One v_mfma_f32_16x16x32 multiplies 16 weight rows n by all M (<= 16) activation
+// rows at once, so the weights stream from HBM exactly once whatever M is. (The
+// VALU GEMV keeps x in registers and re-reads the weights for every 4 rows of x.)
+//
+// Block = WAVES wavefronts on the same R x 16 weight rows; wavefront w takes a
+// contiguous share of the K steps and the partial sums meet in LDS at the end.
+// A step is one 16-byte weight load per lane per 16-row tile: 128 k for INT4
+// (lane quarter q holds k [32q, 32q + 32) of the step), 64 k for INT8 ([16q, 16q+16)).
+// Loads of up to U steps are issued before any arithmetic.
+//
+// Weights enter the MFMA without a subtract: an INT4 nibble v is OR-ed into the
+// mantissa of bf16 128.0 / fp16 1024.0 (exact 128 + v / 1024 + v), an INT8 byte q as
+// the exact integer q + 128. The offset is removed with the per-row sums of x, which
+// one more MFMA against an all-ones operand produces in the same accumulator layout:
+//   sum_k x (v - 8) = sum_k x (128 + v) - 136 sum_k x          (bf16; fp16: 1024, 1032).
+// INT4 group scales multiply each step's partial sums (groups are multiples of 128);
+// the INT8 row scale multiplies the reduced total.
+//
+// MFMA operands: weights are the "A" operand (rows n), x the "B" operand (columns m),
+// so lane l accumulates D[n = 4 (l / 16) + i][m = l % 16], i = 0..3. Inside an INT4
+// dword the nibbles are taken in k order 0,4,1,5,2,6,3,7 (one v_and_or per pair) and x
+// is permuted to the same order with v_perm; INT8 and x stay in natural order.
+#include <stdio.h>
+
+#include "wq.h"
+
+namespace mls {
+
+namespace {
+
+template <typename AT> struct Mx;
+template <> struct Mx<__bf16> {
+  static constexpr uint32_t MAGIC = 0x43004300u;  // bf16 (128, 128)
+  static constexpr float OFF4 = 136.0f;
+  static constexpr uint32_t ONE2 = 0x3F803F80u;   // bf16 (1, 1)
+  __device__ static __forceinline__ f32x4 mma(const uint4& a, const uint4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  // two exact small integers held in fp32 -> packed bf16 (truncation is exact here)
+  __device__ static __forceinline__ uint32_t pack_int(float lo, float hi) {
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo),
+                                 0x07060302u);
+  }
+};
+template <> struct Mx<_Float16> {
+  static constexpr uint32_t MAGIC = 0x64006400u;  // fp16 (1024, 1024)
+  static constexpr float OFF4 = 1032.0f;
+  static constexpr uint32_t ONE2 = 0x3C003C00u;   // fp16 (1, 1)
+  __device__ static __forceinline__ f32x4 mma(const uint4& a, const uint4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t pack_int(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+  }
+};
+
+template <typename ST> __device__ __forceinline__ float ld_scale(const ST* s, int64_t i) {
+  return (float)s[i];
+}
+
+// INT4: the 8 nibbles of dword d (k = 0..7, even k low) -> MFMA operand in k order
+// 0,4,1,5,2,6,3,7, each value the exact MAGIC + v.
+template <typename AT>
+__device__ __forceinline__ uint4 nib_operand(uint32_t d) {
+  constexpr uint32_t M = Mx<AT>::MAGIC, F = 0x000F000Fu;
+  return make_uint4((d & F) | M, ((d >> 4) & F) | M, ((d >> 8) & F) | M, ((d >> 12) & F) | M);
+}
+
+// x chunk (8 16-bit values, k order 0..7) -> k order 0,4,1,5,2,6,3,7
+__device__ __forceinline__ uint4 x_perm(const uint4& v) {
+  return make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                    __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
+}
+
+// INT8: 8 bytes (two dwords, k order) -> 8 exact 16-bit values q + 128
+template <typename AT>
+__device__ __forceinline__ uint4 byte_operand(uint32_t d0, uint32_t d1) {
+  const uint32_t u = d0 ^ 0x80808080u, v = d1 ^ 0x80808080u;
+  return make_uint4(Mx<AT>::pack_int((float)(u & 0xFFu), (float)((u >> 8) & 0xFFu)),
+                    Mx<AT>::pack_int((float)((u >> 16) & 0xFFu), (float)(u >> 24)),
+                    Mx<AT>::pack_int((float)(v & 0xFFu), (float)((v >> 8) & 0xFFu)),
+                    Mx<AT>::pack_int((float)((v >> 16) & 0xFFu), (float)(v >> 24)));
+}
+
+template <int WBITS, typename AT, typename ST, int R, int WAVES, int U>
+// One wavefront per SIMD is the design point (a grid of N / 16 blocks of WAVES
+// wavefronts), so the compiler may spend registers on keeping a chunk's loads in flight.
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemv_mfma_kernel(
+    const AT* __restrict__ a, int64_t lda, const uint8_t* __restrict__ w, int64_t ldw,
+    const ST* __restrict__ s, int64_t ld_sn, int64_t ld_sg, int group, AT* __restrict__ c,
+    int64_t ldc, int M, int N, int K) {
+  constexpr int KB = WBITS == 4 ? 128 : 64;  // k per step
+  constexpr int NMF = WBITS == 4 ? 4 : 2;    // MFMAs per step and 16-row tile
+  __shared__ f32x4 red[WAVES][R][64];
+
+  const int lane = threadIdx.x & 63;
+  // wave-uniform by construction; readfirstlane lets the compiler keep the step
+  // offsets in scalar registers (buffer-load soffset) instead of a waterfall loop
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int n_base = blockIdx.x * (16 * R);
+  const int rows_w = min(16 * R, N - n_base);
+  const int nsteps = K / KB;
+  const int s_lo = (int)((int64_t)nsteps * wave / WAVES);
+  const int s_hi = (int)((int64_t)nsteps * (wave + 1) / WAVES);
+
+  // rows of x past M and weight rows past N read as zeros
+  const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a, (short)0, (int)(M * lda * (int64_t)sizeof(AT)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(w + (int64_t)n_base * ldw), (short)0, (int)(rows_w * ldw), 0x00020000);
+  // this lane's byte offsets inside a step (x row m = r)
+  const int x_off = r * (int)lda * (int)sizeof(AT) + (WBITS == 4 ? 64 * q : 32 * q);
+  int w_off[R];
+#pragma unroll
+  for (int t = 0; t < R; ++t) w_off[t] = (16 * t + r) * (int)ldw + 16 * q;
+  // scale rows of this lane's accumulators: n = n_base + 16 t + 4 q + i
+  int64_t s_row[R][4];
+#pragma unroll
+  for (int t = 0; t < R; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_row[t][i] = (int64_t)min(n_base + 16 * t + 4 * q + i, N - 1) * ld_sn;
+
+  const uint4 ones = make_uint4(Mx<AT>::ONE2, Mx<AT>::ONE2, Mx<AT>::ONE2, Mx<AT>::ONE2);
+  const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[R];
+#pragma unroll
+  for (int t = 0; t < R; ++t) acc[t] = zero;
+  f32x4 xsum = zero;  // INT8: sum_k x over this wave's steps
+
+  for (int s0 = s_lo; s0 < s_hi; s0 += U) {
+    uint4 wv[U][R], xv[U][NMF];
+    float sc[WBITS == 4 ? U : 1][R][4];
+    // All loads of the chunk first, and no branch between them and the MFMAs (a
+    // conditional step lets the compiler sink its loads to the use and serialise the
+    // chunk). A step past this wave's range re-reads its last step's weights and
+    // reads x at an offset beyond the buffer, i.e. zeros, so it adds nothing.
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool live = s0 + u < s_hi;  // wave-uniform
+      const int st = live ? s0 + u : s_hi - 1;
+      const int xs_off = live ? st * KB * (int)sizeof(AT) : 0x7FFFFFF0;
+#pragma unroll
+      for (int t = 0; t < R; ++t)
+        wv[u][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, w_off[t], st * 64, 0));
+#pragma unroll
+      for (int j = 0; j < NMF; ++j)
+        xv[u][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rsx, x_off + 16 * j, xs_off, 0));
+      if constexpr (WBITS == 4) {
+        const int64_t g = (int64_t)(st * KB / group) * ld_sg;
+#pragma unroll
+        for (int t = 0; t < R; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sc[u][t][i] = ld_scale(s, s_row[t][i] + g);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if constexpr (WBITS == 4) {
+        uint4 xo[NMF];
+#pragma unroll
+        for (int j = 0; j < NMF; ++j) xo[j] = x_perm(xv[u][j]);
+        f32x4 xs = zero;
+#pragma unroll
+        for (int j = 0; j < NMF; ++j) xs = Mx<AT>::mma(ones, xo[j], xs);
+#pragma unroll
+        for (int t = 0; t < R; ++t) {
+          const uint32_t d[4] = {wv[u][t].x, wv[u][t].y, wv[u][t].z, wv[u][t].w};
+          f32x4 pp = zero;
+#pragma unroll
+          for (int j = 0; j < NMF; ++j) pp = Mx<AT>::mma(nib_operand<AT>(d[j]), xo[j], pp);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(sc[u][t][i], fmaf(-Mx<AT>::OFF4, xs[i], pp[i]), acc[t][i]);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < NMF; ++j) xsum = Mx<AT>::mma(ones, xv[u][j], xsum);
+#pragma unroll
+        for (int t = 0; t < R; ++t) {
+          acc[t] = Mx<AT>::mma(byte_operand<AT>(wv[u][t].x, wv[u][t].y), xv[u][0], acc[t]);
+          acc[t] = Mx<AT>::mma(byte_operand<AT>(wv[u][t].z, wv[u][t].w), xv[u][1], acc[t]);
+        }
+      }
+    }
+  }
+  if constexpr (WBITS == 8) {
+#pragma unroll
+    for (int t = 0; t < R; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(-128.0f, xsum[i], acc[t][i]);
+  }
+
+  // ---- sum the wavefronts' partial results, scale (INT8), store
+#pragma unroll
+  for (int t = 0; t < R; ++t) red[wave][t][lane] = acc[t];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < R * 64; idx += 64 * WAVES) {
+    const int t = idx / 64, l = idx % 64;
+    f32x4 v = red[0][t][l];
+#pragma unroll
+    for (int ww = 1; ww < WAVES; ++ww) v += red[ww][t][l];
+    const int m = l & 15, nb = n_base + 16 * t + 4 * (l >> 4);
+    if (m >= M || nb >= N) continue;
+    if constexpr (WBITS == 8) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] *= ld_scale(s, (int64_t)min(nb + i, N - 1) * ld_sn);
+    }
+    AT* dst = c + (int64_t)m * ldc + nb;
+    if (nb + 3 < N && ((uintptr_t)dst & 7) == 0) {
+      store4<AT>(dst, v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (nb + i < N) dst[i] = from_f32<AT>(v[i]);
+    }
+  }
+}
+
+// Tuning override for sweeps: MLS_GEMV_MFMA = "R,WAVES" (R in 1, 2; WAVES in 4, 8, 16).
+int env_pair(int& r, int& waves) {
+  const char* v = getenv("MLS_GEMV_MFMA");
+  if (!v || !*v) return 0;
+  return sscanf(v, "%d,%d", &r, &waves) == 2;
+}
+
+template <int WBITS, typename AT, typename ST, int R, int WAVES>
+int launch_one(const WqArgs& p) {
+  constexpr int U = 8;
+  const int64_t blocks = cdiv(p.N, 16 * R);
+  hipLaunchKernelGGL((gemv_mfma_kernel<WBITS, AT, ST, R, WAVES, U>), dim3((unsigned)blocks),
+                     dim3(64 * WAVES), 0, p.stream, static_cast<const AT*>(p.a), p.lda, p.w, p.ldw,
+                     static_cast<const ST*>(p.s), p.ld_sn, p.ld_sg, p.group, static_cast<AT*>(p.c),
+                     p.ldc, (int)p.M, (int)p.N, (int)p.K);
+  return MLS_OK;
+}
+
+template <int WBITS, typename AT, typename ST>
+int launch_shape(const WqArgs& p) {
+  constexpr int KB = WBITS == 4 ? 128 : 64;
+  const int64_t nsteps = p.K / KB;
+  int r = 1, waves = nsteps >= 64 ? 8 : 4;  // about 8 steps (one chunk) per wavefront
+  if (nsteps >= 128) waves = 16;
+  env_pair(r, waves);
+  if (r == 2) {
+    if (waves == 16) return launch_one<WBITS, AT, ST, 2, 16>(p);
+    if (waves == 8) return launch_one<WBITS, AT, ST, 2, 8>(p);
+    return launch_one<WBITS, AT, ST, 2, 4>(p);
+  }
+  if (waves == 16) return launch_one<WBITS, AT, ST, 1, 16>(p);
+  if (waves == 8) return launch_one<WBITS, AT, ST, 1, 8>(p);
+  return launch_one<WBITS, AT, ST, 1, 4>(p);
+}
+
+template <int WBITS, typename AT>
+int launch_st(const WqArgs& p) {
+  return p.s_dt == MLS_F16 ? launch_shape<WBITS, AT, _Float16>(p) : launch_shape<WBITS, AT, float>(p);
+}
+
+}  // namespace
+
+int launch_gemv_mfma(int wbits, const WqArgs& p) {
+  static const bool enabled = [] {
+    const char* v = getenv("MLS_GEMV_MFMA");
+    return !(v && v[0] == '0' && v[1] == 0);
+  }();
+  if (!enabled) return MLS_ERR_UNSUPPORTED;
+  if (p.a_dt != MLS_BF16 && p.a_dt != MLS_F16) return MLS_ERR_UNSUPPORTED;
+  if (p.M < 1 || p.M > 16) return MLS_ERR_UNSUPPORTED;
+  const int KB = wbits == 4 ? 128 : 64;
+  if (p.K % KB != 0) return MLS_ERR_UNSUPPORTED;
+  if (wbits == 4 && p.group % 128 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(p.a, 16) || (p.lda * 2) % 16 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(p.w, 16) || p.ldw % 16 != 0) return MLS_ERR_UNSUPPORTED;
+  // 32-bit buffer offsets: 16 rows of x and a 32-row weight tile
+  // (and the past-the-end x offset 0x7FFFFFF0 added to an x offset must not wrap)
+  if (16 * p.lda * 2 >= (1ll << 31) || 32 * p.ldw >= (1ll << 31)) return MLS_ERR_UNSUPPORTED;
+  if (p.N > 0x7FFFFFFF - 32 || p.K > 0x3FFFFFFF) return MLS_ERR_UNSUPPORTED;
+  if (wbits == 4) return p.a_dt == MLS_BF16 ? launch_st<4, __bf16>(p) : launch_st<4, _Float16>(p);
+  return p.a_dt == MLS_BF16 ? launch_st<8, __bf16>(p) : launch_st<8, _Float16>(p);
+}
+
+}  // namespace mls

@@ -26,6 +26,10 @@ struct WqArgs {
 // when the shape or alignment is outside its fast path.
 int launch_gemv_wq(int wbits, const WqArgs& p);
 
+// MFMA skinny GEMM for M <= 16 and 16-bit activations (weights read once for all M).
+// MLS_ERR_UNSUPPORTED outside its fast path.
+int launch_gemv_mfma(int wbits, const WqArgs& p);
+
 // MFMA tiled GEMM for 16-bit activations. MLS_ERR_UNSUPPORTED outside its fast path.
 int launch_gemm_wq_mfma(int wbits, const WqArgs& p);
 

@@ -40,7 +40,8 @@ int run(const char* fn, int wbits, const WqArgs& p) {
   if (p.K > 0) {
     const bool small_m = p.a_dt == MLS_F32 || p.M <= 16;
     if (small_m) {
-      rc = launch_gemv_wq(wbits, p);
+      if (p.M >= 2 && p.a_dt != MLS_F32) rc = launch_gemv_mfma(wbits, p);
+      if (rc == MLS_ERR_UNSUPPORTED) rc = launch_gemv_wq(wbits, p);
     } else {
       rc = launch_gemm_wq_mfma(wbits, p);
       if (rc == MLS_ERR_UNSUPPORTED) rc = launch_gemv_wq(wbits, p);

@@ -129,6 +129,47 @@ def test_gemv_long_k(dev):
            ref.int8_matmul(a2.float().numpy(), q.cpu().numpy(), s8.cpu().numpy()), "int8 K=11008")
 
 
+# --------------------------------------------------------------- skinny MFMA path (2 <= M <= 16)
+
+@pytest.mark.parametrize("M,N,K,gs,dtype", [
+    (2, 4096, 4096, 128, torch.bfloat16),     # config B shape
+    (16, 1000, 1152, 128, torch.bfloat16),    # N not a multiple of 16; 9 steps over 4 wavefronts
+    (7, 333, 768, 256, torch.float16),        # group of two steps, odd M, ragged N
+    (16, 4096, 14336, 128, torch.bfloat16),   # 112 steps: 16 wavefronts, chunks with tails
+    (3, 48, 128, 128, torch.bfloat16),        # a single step: three wavefronts have none
+])
+def test_skinny_int4(dev, M, N, K, gs, dtype):
+    a, p, s, want = _int4_setup(dev, M, N, K, gs, 500 + M, dtype)
+    _check(int4_matmul(a, p, s, gs), want, f"skinny int4 M={M} N={N} K={K} g{gs}")
+
+
+def test_skinny_int4_f32_scales_strided_rows(dev):
+    M, N, K, gs = 5, 512, 1024, 128
+    a, w = _data(M, N, K, 600, 0.02)
+    p, s = quantize_int4(w.to(dev), gs)  # fp32 scales
+    wide = torch.zeros(M, K + 64, dtype=torch.bfloat16)
+    wide[:, :K] = a.to(torch.bfloat16)
+    x = wide.to(dev)[:, :K]  # lda = K + 64
+    want = ref.int4_matmul(wide[:, :K].float().numpy(), p.cpu().numpy(), s.cpu().numpy(), gs)
+    _check(int4_matmul(x, p, s, gs), want, "skinny int4 fp32 scales, strided rows")
+
+
+@pytest.mark.parametrize("M,N,K,dtype", [
+    (2, 4096, 4096, torch.bfloat16),
+    (16, 1000, 1088, torch.float16),   # 17 steps of 64 k
+    (9, 77, 64, torch.bfloat16),       # one step, ragged N
+    (16, 512, 14336, torch.bfloat16),  # 224 steps: 16 wavefronts, two chunks each
+])
+def test_skinny_int8(dev, M, N, K, dtype):
+    a, w = _data(M, N, K, 700 + M, 0.02)
+    q, s = quantize_int8(w.to(dev))
+    s16 = s.to(torch.float16)
+    ax = a.to(dtype)
+    _check(int8_matmul(ax.to(dev), q, s16),
+           ref.int8_matmul(ax.float().numpy(), q.cpu().numpy(), s16.float().cpu().numpy()),
+           f"skinny int8 M={M} N={N} K={K}")
+
+
 # --------------------------------------------------------------- prefill (MFMA) path
 
 @pytest.mark.parametrize("M,N,K", [(17, 256, 256), (64, 512, 512), (100, 300, 320),
