@@ -59,6 +59,8 @@ __device__ __forceinline__ float ub1(uint32_t v) { return (float)((v >> 8) & 0xF
 __device__ __forceinline__ float ub2(uint32_t v) { return (float)((v >> 16) & 0xFFu); }
 __device__ __forceinline__ float ub3(uint32_t v) { return (float)(v >> 24); }
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 template <int WBITS, typename AT>
 struct XSlot {
   static constexpr bool F32 = sizeof(AT) == 4;
@@ -66,36 +68,48 @@ struct XSlot {
   static constexpr int NV = F32 ? KC : KC / 2;       // registers per chunk of x
 };
 
-// Loads the lane's x values for chunk c (a valid chunk index) into xr[NV] in the
-// layout the dot products expect and returns their sum.
+// The lane's x values for one weight chunk: XQ 16-byte pieces loaded raw, then laid
+// out for the dot products (x_from_raw returns their sum). Loading and unpacking are
+// separate so that every load of the kernel can be issued before the first wait.
 template <int WBITS, typename AT>
-__device__ __forceinline__ float load_x_chunk(const AT* __restrict__ xrow, int c, uint32_t* xr) {
+struct XRaw {
+  static constexpr int XQ = XSlot<WBITS, AT>::KC * (int)sizeof(AT) / 16;
+  uint4 v[XQ];
+};
+
+template <int WBITS, typename AT>
+__device__ __forceinline__ void load_x_raw(const AT* __restrict__ xrow, int c, XRaw<WBITS, AT>& raw) {
+  constexpr int KC = XSlot<WBITS, AT>::KC;
+  const uint4* src = reinterpret_cast<const uint4*>(xrow + (int64_t)c * KC);
+#pragma unroll
+  for (int q = 0; q < XRaw<WBITS, AT>::XQ; ++q) raw.v[q] = src[q];
+}
+
+template <int WBITS, typename AT>
+__device__ __forceinline__ float x_from_raw(const XRaw<WBITS, AT>& raw, uint32_t* xr) {
   using S = XSlot<WBITS, AT>;
   constexpr int KC = S::KC;
   if constexpr (S::F32) {
     float sum = 0.0f;
-    const float4* src = reinterpret_cast<const float4*>(xrow + (int64_t)c * KC);
 #pragma unroll
     for (int q = 0; q < KC / 4; ++q) {
-      const float4 v = src[q];
-      xr[4 * q + 0] = __float_as_uint(v.x);
-      xr[4 * q + 1] = __float_as_uint(v.y);
-      xr[4 * q + 2] = __float_as_uint(v.z);
-      xr[4 * q + 3] = __float_as_uint(v.w);
-      sum += (v.x + v.y) + (v.z + v.w);
+      const uint4 v = raw.v[q];
+      xr[4 * q + 0] = v.x;
+      xr[4 * q + 1] = v.y;
+      xr[4 * q + 2] = v.z;
+      xr[4 * q + 3] = v.w;
+      sum += (__uint_as_float(v.x) + __uint_as_float(v.y)) + (__uint_as_float(v.z) + __uint_as_float(v.w));
     }
     return sum;
   } else {
     using H = Half16<AT>;
     uint32_t d[KC / 2];
-    const uint4* src = reinterpret_cast<const uint4*>(xrow + (int64_t)c * KC);
 #pragma unroll
     for (int q = 0; q < KC / 8; ++q) {
-      const uint4 v = src[q];
-      d[4 * q + 0] = v.x;
-      d[4 * q + 1] = v.y;
-      d[4 * q + 2] = v.z;
-      d[4 * q + 3] = v.w;
+      d[4 * q + 0] = raw.v[q].x;
+      d[4 * q + 1] = raw.v[q].y;
+      d[4 * q + 2] = raw.v[q].z;
+      d[4 * q + 3] = raw.v[q].w;
     }
     if constexpr (WBITS == 4) {
       // sub-block b holds k 8b..8b+7 as pairs (x0,x1)(x2,x3)(x4,x5)(x6,x7); the
@@ -116,6 +130,13 @@ __device__ __forceinline__ float load_x_chunk(const AT* __restrict__ xrow, int c
     for (int q = 0; q < S::NV; ++q) sum = H::dot2(xr[q], H::ONE2, sum);
     return sum;
   }
+}
+
+template <int WBITS, typename AT>
+__device__ __forceinline__ float load_x_chunk(const AT* __restrict__ xrow, int c, uint32_t* xr) {
+  XRaw<WBITS, AT> raw;
+  load_x_raw<WBITS, AT>(xrow, c, raw);
+  return x_from_raw<WBITS, AT>(raw, xr);
 }
 
 // sum_k x_k * u_k over one 16-byte weight chunk, where u_k is the biased code
@@ -203,34 +224,42 @@ __global__ __launch_bounds__(256) void gemv_wq_kernel(
   const int m0 = blockIdx.y * MT;
   const int n0 = (blockIdx.x * 4 + wave) * R;
 
-  // 1. every weight chunk (and INT4 group scale) of this lane, issued up front
+  // 1. the lane's raw x pieces for MT rows first (L2 hits): vector loads complete in
+  //    issue order, so unpacking x below waits for x only, and the dot product of a
+  //    weight chunk waits only for that chunk, overlapping the arrival of the rest
+  XRaw<WBITS, AT> xraw[MT][CPL];
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi) {
+    const AT* xrow = x + (int64_t)min(m0 + mi, M - 1) * ldx;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) load_x_raw<WBITS, AT>(xrow, min(lane + 64 * j, nchunks - 1), xraw[mi][j]);
+  }
+
+  // 2. every weight chunk (and INT4 group scale) of this lane, in the order used
+  //    (non-temporal: every weight byte is used once)
   uint4 wv[R][CPL];
   float sc[R][CPL];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t n = min(n0 + r, N - 1);
-    const uint4* wrow = reinterpret_cast<const uint4*>(w + n * ldw);
+    const u32x4_t* wrow = reinterpret_cast<const u32x4_t*>(w + n * ldw);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = min(lane + 64 * j, nchunks - 1);
-      wv[r][j] = wrow[c];
       if constexpr (WBITS == 4)
         sc[r][j] = scale_value(s, n * ld_sn + (int64_t)((c * KC) / group) * ld_sg);
+      const u32x4_t v = __builtin_nontemporal_load(wrow + c);
+      wv[r][j] = make_uint4(v.x, v.y, v.z, v.w);
     }
   }
+  __builtin_amdgcn_sched_barrier(0);  // all loads above are issued before any wait below
 
-  // 2. the lane's x slice for MT rows (zeros past K)
   uint32_t xr[MT][CPL][NV];
   float osx[MT][CPL];
 #pragma unroll
-  for (int mi = 0; mi < MT; ++mi) {
-    const AT* xrow = x + (int64_t)min(m0 + mi, M - 1) * ldx;
+  for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = lane + 64 * j;
-      osx[mi][j] = OFF * load_x_chunk<WBITS, AT>(xrow, min(c, nchunks - 1), xr[mi][j]);
-    }
-  }
+    for (int j = 0; j < CPL; ++j) osx[mi][j] = OFF * x_from_raw<WBITS, AT>(xraw[mi][j], xr[mi][j]);
 
   // 3. dot products
   float part[MT * R];

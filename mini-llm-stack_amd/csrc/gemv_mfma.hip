@@ -58,6 +58,9 @@ template <> struct Mx<_Float16> {
   }
 };
 
+// buffer-load cache policy: non-temporal (the weights are read once)
+constexpr int kNonTemporal = 2;
+
 template <typename ST> __device__ __forceinline__ float ld_scale(const ST* s, int64_t i) {
   return (float)s[i];
 }
@@ -146,7 +149,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
       const int xs_off = live ? st * KB * (int)sizeof(AT) : 0x7FFFFFF0;
 #pragma unroll
       for (int t = 0; t < R; ++t)
-        wv[u][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, w_off[t], st * 64, 0));
+        wv[u][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, w_off[t], st * 64, kNonTemporal));
 #pragma unroll
       for (int j = 0; j < NMF; ++j)
         xv[u][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
