@@ -12,11 +12,12 @@
 //          per group.
 //
 // Native kernel:
-// Block tile 256 (m) x 256 (n) x 128 (k); 4 wavefronts in 2 x 2, each owning a
-// 128 x 128 sub-tile = 8 x 8 MFMA tiles (256 fp32 accumulators per lane). Both
-// operands are K-contiguous ("NT"): a stage is 256 rows x 128 bytes per operand,
+// Block tile 256 (m) x 256 (n) x 128 (k); 8 wavefronts in 2 x 4 (two per SIMD), each
+// owning a 128 x 64 sub-tile = 8 x 4 MFMA tiles (128 fp32 accumulators per lane).
+// Both operands are K-contiguous ("NT"): a stage is 256 rows x 128 bytes per operand,
 // staged global -> registers -> LDS with the 16-byte chunk index XOR-swizzled by
-// row & 7, double-buffered with one barrier per stage. The lanes of k-block g of an
+// row & 7, double-buffered with one barrier per stage; the next stage is stored
+// between the two halves of the current stage's MFMAs. The lanes of k-block g of an
 // operand take 16-byte chunks g and g + 4 of the 128-byte row (any k order is valid
 // when both operands use it); with the row & 7 swizzle these reads, and the staging
 // writes, measured free of LDS bank conflicts on gfx950. The B tile is the MFMA
@@ -59,14 +60,19 @@ __device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, const 
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-template <typename CT>
-__global__ __launch_bounds__(256) void fp8_gemm_mfma_kernel(
+template <typename CT, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void fp8_gemm_mfma_kernel(
     const uint8_t* __restrict__ a, int64_t lda, const uint8_t* __restrict__ b, int64_t ldb,
     float sa, const float* __restrict__ sap, int64_t sas, float sb,
     const float* __restrict__ sbp, int64_t sbs, CT* __restrict__ c, int64_t ldc, int M, int N,
     int K, int m_tiles, int n_tiles) {
   constexpr int BM = 256, BN = 256, BK = 128;
-  constexpr int GM = 4;  // m-tiles per group in the tile order
+  constexpr int NT = 64 * WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+  constexpr int TM = WTM / 16, TN = WTN / 16;
+  constexpr int PT = BM * 8 / NT;  // 16-byte chunks per thread and operand
+  constexpr int GM = 4;            // m-tiles per group in the tile order
+  static_assert(TM % 2 == 0 && PT >= 1, "tile split");
   extern __shared__ __align__(16) uint8_t smem[];
   uint4* As = reinterpret_cast<uint4*>(smem);  // [2][BM][8] 16-byte chunks
   uint4* Bs = As + 2 * BM * 8;                  // [2][BN][8]
@@ -81,89 +87,99 @@ __global__ __launch_bounds__(256) void fp8_gemm_mfma_kernel(
   const int m0 = mt * BM, n0 = nt * BN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm0 = (wave >> 1) * 128, wn0 = (wave & 1) * 128;
+  const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
 
-  // each thread stages chunks q = tid + 256 i (i < 8) of both operands: row q / 8 =
-  // srow + 32 i, chunk q % 8 = skc; the swizzled LDS slot is lds0 + 256 i. Loads go
-  // through buffer descriptors covering only this tile's valid rows, so rows past
+  // each thread stages chunks q = tid + NT i (i < PT) of both operands: row q / 8 =
+  // srow + (NT / 8) i, chunk q % 8 = skc; the swizzled LDS slot is lds0 + NT i. Loads
+  // go through buffer descriptors covering only this tile's valid rows, so rows past
   // M or N read as zeros; the stage offset k0 travels in the scalar offset.
   const int srow = tid >> 3, skc = tid & 7;
-  const int lds0 = srow * 8 + (skc ^ (srow & 7));  // (srow + 32 i) & 7 is the same
+  const int lds0 = srow * 8 + (skc ^ (srow & 7));  // (srow + (NT / 8) i) & 7 is the same
   const int rows_a = min(BM, M - m0), rows_b = min(BN, N - n0);
   const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a + (int64_t)m0 * lda), (short)0, (int)(rows_a * lda), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(b + (int64_t)n0 * ldb), (short)0, (int)(rows_b * ldb), 0x00020000);
-  int a_off[8], b_off[8];
+  int a_off[PT], b_off[PT];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    a_off[i] = (srow + 32 * i) * (int)lda + skc * 16;
-    b_off[i] = (srow + 32 * i) * (int)ldb + skc * 16;
+  for (int i = 0; i < PT; ++i) {
+    a_off[i] = (srow + (NT / 8) * i) * (int)lda + skc * 16;
+    b_off[i] = (srow + (NT / 8) * i) * (int)ldb + skc * 16;
   }
-  uint4 ra[8], rb[8];
-#define MLS_FP8_LOAD(k0)                                                                  \
-  _Pragma("unroll") for (int i = 0; i < 8; ++i) {                                         \
-    ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsa, a_off[i], (k0), 0)); \
-    rb[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsb, b_off[i], (k0), 0)); \
-  }
-#define MLS_FP8_STORE(buf)                                              \
-  _Pragma("unroll") for (int i = 0; i < 8; ++i) {                       \
-    As[(buf) * BM * 8 + lds0 + 256 * i] = ra[i];                        \
-    Bs[(buf) * BN * 8 + lds0 + 256 * i] = rb[i];                        \
-  }
+  uint4 ra[PT], rb[PT];
+  auto load = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      ra[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsa, a_off[i], k0, 0));
+      rb[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsb, b_off[i], k0, 0));
+    }
+  };
+  auto store = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+      As[buf * BM * 8 + lds0 + NT * i] = ra[i];
+      Bs[buf * BN * 8 + lds0 + NT * i] = rb[i];
+    }
+  };
 
-  f32x4 acc[8][8];
+  f32x4 acc[TN][TM];
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < TN; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int nk = K / BK;
-  MLS_FP8_LOAD(0)
-  MLS_FP8_STORE(0)
-  __syncthreads();
+    for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int lr = lane & 15, lk = lane >> 4;  // operand row, k block (chunks lk and lk + 4)
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) { MLS_FP8_LOAD((kt + 1) * BK) }
+  auto operand = [&](const uint4* base, int row) __attribute__((always_inline)) {
+    const int sw = row & 7;
+    const uint4 lo = base[row * 8 + (lk ^ sw)];
+    const uint4 hi = base[row * 8 + ((lk + 4) ^ sw)];
+    return i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  };
+  i32x8 bop[TN];
+  // MFMAs of m-subtiles [j_lo, j_hi) of the stage in LDS buffer `buf` (the weight
+  // operands are read with the first half)
+  auto compute = [&](int buf, int j_lo, int j_hi) __attribute__((always_inline)) {
     const uint4* as = As + buf * BM * 8;
     const uint4* bs = Bs + buf * BN * 8;
-    i32x8 bop[8];
+    if (j_lo == 0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int row = wn0 + i * 16 + lr, sw = row & 7;
-      const uint4 lo = bs[row * 8 + (lk ^ sw)];
-      const uint4 hi = bs[row * 8 + ((lk + 4) ^ sw)];
-      bop[i] = i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                     (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+      for (int i = 0; i < TN; ++i) bop[i] = operand(bs, wn0 + i * 16 + lr);
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int row = wm0 + j * 16 + lr, sw = row & 7;
-      const uint4 lo = as[row * 8 + (lk ^ sw)];
-      const uint4 hi = as[row * 8 + ((lk + 4) ^ sw)];
-      const i32x8 aop = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w,
-                         (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    for (int j = j_lo; j < j_hi; ++j) {
+      const i32x8 aop = operand(as, wm0 + j * 16 + lr);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i][j] = mfma_fp8(bop[i], aop, acc[i][j]);
+      for (int i = 0; i < TN; ++i) acc[i][j] = mfma_fp8(bop[i], aop, acc[i][j]);
     }
-    if (kt + 1 < nk) { MLS_FP8_STORE(buf ^ 1) }
+  };
+
+  // stage s from LDS buffer s & 1; the next stage is loaded at the start of s (past the
+  // end: harmless reads, zeros beyond the operands) and stored between the two halves
+  // of the stage's MFMAs, overlapping the MFMAs still in flight
+  const int nk = K / BK;
+  load(0);
+  store(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    load((kt + 1) * BK);
+    compute(buf, 0, TM / 2);
+    __builtin_amdgcn_sched_barrier(0);
+    store(buf ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(buf, TM / 2, TM);
     __syncthreads();
   }
 
-#undef MLS_FP8_LOAD
-#undef MLS_FP8_STORE
-
   // epilogue: acc[i][j][r] = C[m = m0+wm0+16j+lr][n = n0+wn0+16i+4lk+r]
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < TN; ++i) {
     const int nb = n0 + wn0 + i * 16 + 4 * lk;
     float sbn[4];
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) sbn[rr] = sbp ? (nb + rr < N ? sbp[(int64_t)(nb + rr) * sbs] : 0.f) : sb;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < TM; ++j) {
       const int m = m0 + wm0 + j * 16 + lr;
       if (m >= M) continue;
       const float sam = sap ? sap[(int64_t)m * sas] : sa;
@@ -190,6 +206,24 @@ static int launch_generic(const Fp8Args& f) {
   return check_launch("mls_fp8_gemm(generic)");
 }
 
+template <typename CT, int WM, int WN>
+static int launch_native_w(const Fp8Args& f) {
+  const int mt = (int)cdiv(f.M, 256), nt = (int)cdiv(f.N, 256);
+  const size_t lds = 2 * 2 * 256 * 128;
+  auto kern = fp8_gemm_mfma_kernel<CT, WM, WN>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return fail(MLS_ERR_HIP, "mls_fp8_gemm: cannot reserve %zu bytes of LDS", lds);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)(mt * nt)), dim3(64 * WM * WN), lds, f.stream, f.a, f.lda,
+                     f.b, f.ldb, f.sa, f.sap, f.sas, f.sb, f.sbp, f.sbs, (CT*)f.c, f.ldc, (int)f.M,
+                     (int)f.N, (int)f.K, mt, nt);
+  return check_launch("mls_fp8_gemm(native)");
+}
+
 template <typename CT>
 static int launch_native(const Fp8Args& f) {
   // buffer descriptors address at most 2^31 bytes per 256-row tile
@@ -198,20 +232,13 @@ static int launch_native(const Fp8Args& f) {
                     f.M < (1 << 30) && f.N < (1 << 30) && f.lda * 256 < (1ll << 31) &&
                     f.ldb * 256 < (1ll << 31);
   if (!fast) return MLS_ERR_UNSUPPORTED;
-  const int mt = (int)cdiv(f.M, 256), nt = (int)cdiv(f.N, 256);
-  const size_t lds = 2 * 2 * 256 * 128;
-  auto kern = fp8_gemm_mfma_kernel<CT>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess)
-      return fail(MLS_ERR_HIP, "mls_fp8_gemm: cannot reserve %zu bytes of LDS", lds);
-    attr_set = true;
-  }
-  hipLaunchKernelGGL(kern, dim3((unsigned)(mt * nt)), dim3(256), lds, f.stream, f.a, f.lda, f.b,
-                     f.ldb, f.sa, f.sap, f.sas, f.sb, f.sbp, f.sbs, (CT*)f.c, f.ldc, (int)f.M,
-                     (int)f.N, (int)f.K, mt, nt);
-  return check_launch("mls_fp8_gemm(native)");
+  // MLS_FP8_WAVES = 4 (one wavefront per SIMD, 128 x 128 wave tiles) or 8 (default:
+  // two per SIMD, 128 x 64 wave tiles), for tuning sweeps
+  static const bool w8 = [] {
+    const char* e = getenv("MLS_FP8_WAVES");
+    return !(e && e[0] == '4');
+  }();
+  return w8 ? launch_native_w<CT, 2, 4>(f) : launch_native_w<CT, 2, 2>(f);
 }
 
 }  // namespace mls
