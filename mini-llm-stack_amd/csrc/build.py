@@ -60,7 +60,9 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda s: compile_one(s, verbose), SOURCES))
     tmp = OUT.with_suffix(".so.tmp")
-    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(tmp),
+    # --no-undefined: a kernel whose host-side launch stub was not emitted must fail
+    # the build here, not the first dlopen
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-Wl,--no-undefined", "-o", str(tmp),
            *map(str, objs)]
     if verbose:
         print(" ".join(cmd), flush=True)

@@ -198,6 +198,132 @@ __global__ __launch_bounds__(64 * WM * WN) void fp8_gemm_mfma_kernel(
   }
 }
 
+// Same tiles and LDS layout, with the stages brought into LDS by buffer loads that
+// write LDS directly (buffer_load_dwordx4 ... lds): no staging registers and no
+// ds_write instructions. Lane l of a wavefront writes the 16 bytes at LDS slot
+// base + l, so each lane loads the global chunk that belongs in that slot under the
+// row & 7 swizzle.
+// one buffer_load_dwordx4 ... lds: lane l's 16 bytes go to LDS at lds + 16 l
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff,
+                                           soff, 0, 0);
+}
+
+template <typename CT, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void fp8_gemm_dma_kernel(
+    const uint8_t* __restrict__ a, int64_t lda, const uint8_t* __restrict__ b, int64_t ldb,
+    float sa, const float* __restrict__ sap, int64_t sas, float sb,
+    const float* __restrict__ sbp, int64_t sbs, CT* __restrict__ c, int64_t ldc, int M, int N,
+    int K, int m_tiles, int n_tiles) {
+  constexpr int BM = 256, BN = 256, BK = 128;
+  constexpr int NW = WM * WN;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 16, TN = WTN / 16;
+  constexpr int SLOTS = BM * 8;           // 16-byte slots per operand and stage
+  constexpr int PW = SLOTS / (64 * NW);  // loads per wavefront and operand
+  constexpr int GM = 4;
+  static_assert(PW >= 1 && SLOTS % (64 * NW) == 0, "slots");
+  __shared__ __align__(16) uint4 lds[4 * SLOTS];  // A0 | B0 | A1 | B1
+
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int per_group = GM * n_tiles;
+  const int g = L / per_group, first_m = g * GM;
+  const int gsz = min(m_tiles - first_m, GM);
+  const int r = L % per_group;
+  const int mt = first_m + r % gsz, nt = r / gsz;
+  const int m0 = mt * BM, n0 = nt * BN;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+
+  const int rows_a = min(BM, M - m0), rows_b = min(BN, N - n0);
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a + (int64_t)m0 * lda), (short)0, (int)(rows_a * lda), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(b + (int64_t)n0 * ldb), (short)0, (int)(rows_b * ldb), 0x00020000);
+  // slot s = (wave * PW + i) * 64 + lane holds row s / 8, logical chunk (s % 8) ^ (row & 7)
+  int a_off[PW], b_off[PW];
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int s = (wave * PW + i) * 64 + lane, row = s >> 3, lc = (s & 7) ^ (row & 7);
+    a_off[i] = row * (int)lda + lc * 16;
+    b_off[i] = row * (int)ldb + lc * 16;
+  }
+  auto dma = [&](uint4* as, uint4* bs, int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      lds_load16(rsa, as + (wave * PW + i) * 64, a_off[i], k0);
+      lds_load16(rsb, bs + (wave * PW + i) * 64, b_off[i], k0);
+    }
+  };
+
+  f32x4 acc[TN][TM];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int lr = lane & 15, lk = lane >> 4;
+  auto operand = [&](const uint4* base, int row) __attribute__((always_inline)) {
+    const int sw = row & 7;
+    const uint4 lo = base[row * 8 + (lk ^ sw)];
+    const uint4 hi = base[row * 8 + ((lk + 4) ^ sw)];
+    return i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  };
+  // Stage s lives in buffer s & 1. Each stage first reads all of its operands into
+  // registers, then issues the loads of stage s + 1 into the other buffer, then runs
+  // its MFMAs: the loads complete under the MFMAs, and the wait the compiler places
+  // for them before the next LDS read falls after this stage's closing barrier anyway.
+  const int nk = K / BK;
+  dma(lds, lds + SLOTS, 0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const uint4* const as = lds + (kt & 1) * 2 * SLOTS;
+    const uint4* const bs = as + SLOTS;
+    uint4* const an = lds + ((kt & 1) ^ 1) * 2 * SLOTS;
+    i32x8 bop[TN], aop[TM];
+#pragma unroll
+    for (int i = 0; i < TN; ++i) bop[i] = operand(bs, wn0 + i * 16 + lr);
+#pragma unroll
+    for (int j = 0; j < TM; ++j) aop[j] = operand(as, wm0 + j * 16 + lr);
+    __builtin_amdgcn_sched_barrier(0);
+    dma(an, an + SLOTS, (kt + 1) * BK);  // past the end: harmless reads
+    __builtin_amdgcn_sched_barrier(0);   // issued before the MFMAs, not after them
+#pragma unroll
+    for (int j = 0; j < TM; ++j)
+#pragma unroll
+      for (int i = 0; i < TN; ++i) acc[i][j] = mfma_fp8(bop[i], aop[j], acc[i][j]);
+    __builtin_amdgcn_sched_barrier(0);  // the MFMAs stay ahead of the barrier's wait
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < TN; ++i) {
+    const int nb = n0 + wn0 + i * 16 + 4 * lk;
+    float sbn[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) sbn[rr] = sbp ? (nb + rr < N ? sbp[(int64_t)(nb + rr) * sbs] : 0.f) : sb;
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int m = m0 + wm0 + j * 16 + lr;
+      if (m >= M) continue;
+      const float sam = sap ? sap[(int64_t)m * sas] : sa;
+      CT* dst = c + (int64_t)m * ldc + nb;
+      const float v0 = acc[i][j][0] * (sam * sbn[0]), v1 = acc[i][j][1] * (sam * sbn[1]);
+      const float v2 = acc[i][j][2] * (sam * sbn[2]), v3 = acc[i][j][3] * (sam * sbn[3]);
+      if (nb + 3 < N && (ldc % 4) == 0) {
+        store4<CT>(dst, v0, v1, v2, v3);
+      } else {
+        if (nb + 0 < N) dst[0] = from_f32<CT>(v0);
+        if (nb + 1 < N) dst[1] = from_f32<CT>(v1);
+        if (nb + 2 < N) dst[2] = from_f32<CT>(v2);
+        if (nb + 3 < N) dst[3] = from_f32<CT>(v3);
+      }
+    }
+  }
+}
+
 template <typename CT>
 static int launch_generic(const Fp8Args& f) {
   hipLaunchKernelGGL(fp8_gemm_generic_kernel<CT>, dim3((unsigned)cdiv(f.M * f.N, 256)), dim3(256), 0,
@@ -224,6 +350,15 @@ static int launch_native_w(const Fp8Args& f) {
   return check_launch("mls_fp8_gemm(native)");
 }
 
+template <typename CT, int WM, int WN>
+static int launch_native_dma(const Fp8Args& f) {
+  const int mt = (int)cdiv(f.M, 256), nt = (int)cdiv(f.N, 256);
+  hipLaunchKernelGGL((fp8_gemm_dma_kernel<CT, WM, WN>), dim3((unsigned)(mt * nt)), dim3(64 * WM * WN), 0,
+                     f.stream, f.a, f.lda, f.b, f.ldb, f.sa, f.sap, f.sas, f.sb, f.sbp, f.sbs, (CT*)f.c,
+                     f.ldc, (int)f.M, (int)f.N, (int)f.K, mt, nt);
+  return check_launch("mls_fp8_gemm(native)");
+}
+
 template <typename CT>
 static int launch_native(const Fp8Args& f) {
   // buffer descriptors address at most 2^31 bytes per 256-row tile
@@ -238,6 +373,11 @@ static int launch_native(const Fp8Args& f) {
     const char* e = getenv("MLS_FP8_WAVES");
     return !(e && e[0] == '4');
   }();
+  static const bool dma = [] {  // MLS_FP8_DMA = 0: register-staged stores instead of LDS DMA
+    const char* e = getenv("MLS_FP8_DMA");
+    return !(e && e[0] == '0');
+  }();
+  if (dma) return w8 ? launch_native_dma<CT, 2, 4>(f) : launch_native_dma<CT, 2, 2>(f);
   return w8 ? launch_native_w<CT, 2, 4>(f) : launch_native_w<CT, 2, 2>(f);
 }
 
