@@ -397,6 +397,276 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_gemm_kernel(const Mfma16P
   }
 }
 
+// ---------------------------------------------------------------------------
+// Weight-only GEMM with the activation tile brought into LDS by buffer loads that
+// write LDS directly (buffer_load_dwordx4 ... lds): 16-bit activations need no
+// widening, so their stage costs no staging registers and no ds_write. Lane l of a
+// wavefront fills LDS slot base + l and loads the global chunk that belongs there
+// under the row & 7 swizzle. The weights are still staged through registers (widened
+// to 16-bit on the way). Per stage s, in this order:
+//   1. store stage s + 1's weights (loaded during stage s - 1) into the other buffer,
+//   2. issue the loads of stage s + 2's weights,
+//   3. read every operand of stage s from LDS,
+//   4. issue the activation loads of stage s + 1 into the other buffer,
+//   5. the MFMAs, then the barrier.
+// The compiler keeps LDS reads behind pending LDS-direct loads; with this order the
+// only such wait is the barrier's own, after the MFMAs have covered the load.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff,
+                                           soff, 0, 0);
+}
+
+template <int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN, bool GROUPED>
+__global__ __launch_bounds__(64 * WM * WN) void mfma16_adma_kernel(const Mfma16Params p) {
+  constexpr int BK = 64;
+  constexpr int NW = WM * WN, NT = 64 * NW;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 16, TN = WTN / 16;
+  static_assert(BKIND == B_INT8 || BKIND == B_INT4, "weight-only");
+  constexpr int PW = BM * 8 / (64 * NW);  // activation loads per wavefront and stage
+  static_assert(PW >= 1 && BM * 8 % (64 * NW) == 0, "activation slots");
+  constexpr int B_CPR = BKIND == B_INT4 ? 2 : 4;
+  constexpr int B_CH = BN * B_CPR;
+  static_assert(B_CH % NT == 0, "BN too small for the weight staging");
+  constexpr int B_PT = B_CH / NT;
+  constexpr int B_RSTEP = NT / B_CPR;
+  constexpr bool GS = BKIND == B_INT4;
+  static_assert(!GS || BN <= NT, "one thread per group scale");
+
+  extern __shared__ __align__(16) uint8_t smem[];
+  uint4* As = reinterpret_cast<uint4*>(smem);  // [2][BM][8]
+  uint4* Bs = As + 2 * BM * 8;                  // [2][BN][8]
+  float* sS = reinterpret_cast<float*>(Bs + 2 * BN * 8);  // INT4: [2][2][BN]
+
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int nt = L / p.m_tiles, mt = L % p.m_tiles;
+  int row_hi = p.M, m0;
+  const uint8_t* bmat = p.b;
+  const void* smat = p.s;
+  if constexpr (GROUPED) {
+    int e = 0, cum = 0, row_lo = 0;
+    for (; e < p.E; ++e) {
+      const int lo = p.seg_off[e], hi = p.seg_off[e + 1];
+      const int tcount = (hi - lo + BM - 1) / BM;
+      if (mt < cum + tcount) {
+        row_lo = lo;
+        row_hi = hi;
+        break;
+      }
+      cum += tcount;
+    }
+    if (e == p.E) return;  // surplus block
+    m0 = row_lo + (mt - cum) * BM;
+    bmat += (int64_t)e * p.b_estride;
+    smat = (const uint8_t*)smat + (int64_t)e * p.s_estride * (p.s_dt == MLS_F16 ? 2 : 4);
+  } else {
+    m0 = mt * BM;
+  }
+  const int n0 = nt * BN;
+  const int N = p.N;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+
+  const int rows_a = min(BM, row_hi - m0), rows_b = min(BN, N - n0);
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint8_t*)p.a + (int64_t)m0 * p.lda * 2), (short)0, (int)(rows_a * p.lda * 2),
+      0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(bmat + (int64_t)n0 * p.ldb), (short)0, (int)(rows_b * p.ldb), 0x00020000);
+  // activation slot s = (wave * PW + i) * 64 + lane: row s / 8, logical chunk (s % 8) ^ (row & 7)
+  int a_off[PW];
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int s = (wave * PW + i) * 64 + lane, row = s >> 3, lc = (s & 7) ^ (row & 7);
+    a_off[i] = row * (int)p.lda * 2 + lc * 16;
+  }
+  const int b_row0 = tid / B_CPR, b_cc = tid % B_CPR;
+  int b_off[B_PT];
+#pragma unroll
+  for (int i = 0; i < B_PT; ++i) b_off[i] = (b_row0 + B_RSTEP * i) * (int)p.ldb + b_cc * 16;
+  const int64_t s_row = (int64_t)min(n0 + tid, N - 1) * p.ld_sn;
+
+  uint4 rb[B_PT];
+  float rs0 = 0.f, rs1 = 0.f;
+  auto dma_a = [&](int buf, int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < PW; ++i) lds_load16(rsa, As + buf * BM * 8 + (wave * PW + i) * 64, a_off[i], k0 * 2);
+  };
+  auto load_b = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < B_PT; ++i)
+      rb[i] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(rsb, b_off[i], BKIND == B_INT4 ? k0 / 2 : k0, 0));
+    if constexpr (GS) {
+      if (tid < BN) {
+        const int kc = min(k0, p.K - BK);  // a stage past the end reuses the last scales
+        rs0 = scale_at(smat, p.s_dt, s_row + (int64_t)(kc / p.group) * p.ld_sg);
+        rs1 = scale_at(smat, p.s_dt, s_row + (int64_t)((kc + 32) / p.group) * p.ld_sg);
+      }
+    }
+  };
+  auto store_b = [&](int buf) __attribute__((always_inline)) {
+    uint4* bs = Bs + buf * BN * 8;
+#pragma unroll
+    for (int i = 0; i < B_PT; ++i) {
+      const int row = b_row0 + B_RSTEP * i;
+      if constexpr (BKIND == B_INT4) {
+        uint32_t o[16];
+        widen_int4<MT>(rb[i], o);
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          bs[row * 8 + ((4 * b_cc + h) ^ swz(row))] =
+              make_uint4(o[4 * h + 0], o[4 * h + 1], o[4 * h + 2], o[4 * h + 3]);
+      } else {
+        uint32_t o[8];
+        widen_int8<MT>(rb[i], o);
+        bs[row * 8 + ((2 * b_cc + 0) ^ swz(row))] = make_uint4(o[0], o[1], o[2], o[3]);
+        bs[row * 8 + ((2 * b_cc + 1) ^ swz(row))] = make_uint4(o[4], o[5], o[6], o[7]);
+      }
+    }
+    if constexpr (GS) {
+      if (tid < BN) {
+        sS[(buf * 2 + 0) * BN + tid] = rs0;
+        sS[(buf * 2 + 1) * BN + tid] = rs1;
+      }
+    }
+  };
+
+  f32x4 acc[TN][TM];
+  f32x4 accg[GS ? TN : 1][GS ? TM : 1];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (GS) {
+#pragma unroll
+    for (int i = 0; i < TN; ++i)
+#pragma unroll
+      for (int j = 0; j < TM; ++j) accg[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int lr = lane & 15, lk = lane >> 4;
+  const int nk = p.K / BK;
+  // prologue: stage 0 in buffer 0, stage 1's weights in registers
+  dma_a(0, 0);
+  load_b(0);
+  store_b(0);
+  load_b(BK);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    const int k0 = kt * BK;
+    store_b(buf ^ 1);      // stage kt + 1 (past the end: harmless)
+    load_b(k0 + 2 * BK);   // stage kt + 2
+    uint4 aop[2][TM], bop[2][TN];
+    const uint4* as = As + buf * BM * 8;
+    const uint4* bs = Bs + buf * BN * 8;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int ch = ks * 4 + lk;
+#pragma unroll
+      for (int i = 0; i < TN; ++i) {
+        const int row = wn0 + i * 16 + lr;
+        bop[ks][i] = bs[row * 8 + (ch ^ swz(row))];
+      }
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        const int row = wm0 + j * 16 + lr;
+        aop[ks][j] = as[row * 8 + (ch ^ swz(row))];
+      }
+    }
+    float sc[GS ? 2 : 1][GS ? TN : 1][4];
+    if constexpr (GS) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int i = 0; i < TN; ++i) {
+          const float4 s4 = *reinterpret_cast<const float4*>(sS + (buf * 2 + ks) * BN + wn0 + i * 16 + 4 * lk);
+          sc[ks][i][0] = s4.x;
+          sc[ks][i][1] = s4.y;
+          sc[ks][i][2] = s4.z;
+          sc[ks][i][3] = s4.w;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    dma_a(buf ^ 1, k0 + BK);  // stage kt + 1 (past the end: zeros / harmless)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if constexpr (GS) {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+          for (int j = 0; j < TM; ++j) accg[i][j] = Mfma16<MT>::mma(bop[ks][i], aop[ks][j], accg[i][j]);
+        if ((k0 + 32 * (ks + 1)) % p.group == 0) {  // group ends: acc += s[n] * partial
+#pragma unroll
+          for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TM; ++j) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(sc[ks][i][r], accg[i][j][r], acc[i][j][r]);
+              accg[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < TN; ++i)
+#pragma unroll
+          for (int j = 0; j < TM; ++j) acc[i][j] = Mfma16<MT>::mma(bop[ks][i], aop[ks][j], acc[i][j]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the MFMAs stay ahead of the barrier's wait
+    __syncthreads();
+  }
+
+  // ---- epilogue: acc[i][j][r] = C[m = m0+wm0+16j+lr][n = n0+wn0+16i+4lk+r]
+  OT* c = static_cast<OT*>(p.c);
+#pragma unroll
+  for (int i = 0; i < TN; ++i) {
+    const int nb = n0 + wn0 + i * 16 + 4 * lk;
+    float sn[4] = {1.f, 1.f, 1.f, 1.f};
+    if constexpr (BKIND == B_INT8) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sn[r] = scale_at(smat, p.s_dt, min(nb + r, N - 1));
+    }
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int m = m0 + wm0 + j * 16 + lr;
+      if (m >= row_hi) continue;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] * sn[r];
+      OT* dst = c + (int64_t)m * p.ldc + nb;
+      if (nb + 3 < N && (p.ldc % 4) == 0) {
+        store4<OT>(dst, v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (nb + r < N) dst[r] = from_f32<OT>(v[r]);
+      }
+    }
+  }
+}
+
+template <int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN, bool GROUPED>
+static int launch_adma(Mfma16Params p, hipStream_t st) {
+  p.n_tiles = (int)cdiv(p.N, BN);
+  const size_t lds = (size_t)2 * (BM + BN) * 8 * 16 + (BKIND == B_INT4 ? (size_t)2 * 2 * BN * 4 : 0);
+  auto kern = mfma16_adma_kernel<BKIND, MT, OT, BM, BN, WM, WN, GROUPED>;
+  static bool attr_set = false;
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)lds) != hipSuccess)
+      return fail(MLS_ERR_HIP, "mfma16 GEMM: cannot reserve %zu bytes of LDS", lds);
+    attr_set = true;
+  }
+  const int64_t blocks = (int64_t)p.n_tiles * p.m_tiles;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(64 * WM * WN), lds, st, p);
+  return check_launch("mfma16 GEMM");
+}
+
 // Two stages of register prefetch where the accumulators leave room for them: 8-wave
 // blocks (two wavefronts per SIMD, 256 registers each) with at most 64 x 64 wave tiles.
 template <int BM, int BN, int WM, int WN>
@@ -443,7 +713,8 @@ static int pick_bm(int64_t M, int64_t N, int max_bm) {
 
 // Tuning overrides for sweeps: MLS_MFMA_WAVES = 4 or 8 wavefronts per block (default 8:
 // two per SIMD, so one wavefront's memory waits overlap the other's MFMAs), MLS_MFMA_BM =
-// forced row-tile height (16 .. 256).
+// forced row-tile height (16 .. 256), MLS_MFMA_ADMA = 0 stages 16-bit activations
+// through registers instead of loading them straight into LDS.
 static int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
   return v && *v ? atoi(v) : dflt;
@@ -458,6 +729,13 @@ static int dense16(Mfma16Params p, hipStream_t st) {
   if (force_bm >= 16 && force_bm <= MAXBM && (force_bm & (force_bm - 1)) == 0) bm = force_bm;
   p.m_tiles = (int)cdiv(p.M, bm);
   const bool w8 = waves == 8;
+  static const bool adma = env_int("MLS_MFMA_ADMA", 1) != 0;
+  if constexpr (AKIND == A_RAW16) {
+    if (adma && w8 && bm == 256) {
+      if constexpr (MAXBM >= 256) return launch_adma<BKIND, MT, OT, 256, 256, 2, 4, false>(p, st);
+    }
+    if (adma && w8 && bm == 128) return launch_adma<BKIND, MT, OT, 128, 256, 2, 4, false>(p, st);
+  }
   switch (bm) {
     case 256:
       if constexpr (MAXBM >= 256) {
@@ -518,6 +796,10 @@ int launch_grouped_int4(const GroupedArgs& g) {
   // upper bound on sum_e ceil(rows_e / BM) without reading the device offsets
   p.m_tiles = (int)(cdiv(w.M, BM) + g.E);
   static const bool w8 = env_int("MLS_MFMA_WAVES", 8) == 8;
+  static const bool adma = env_int("MLS_MFMA_ADMA", 1) != 0;
+  if (w8 && adma)
+    return w.a_dt == MLS_BF16 ? launch_adma<B_INT4, __bf16, __bf16, BM, 256, 2, 4, true>(p, w.stream)
+                              : launch_adma<B_INT4, _Float16, _Float16, BM, 256, 2, 4, true>(p, w.stream);
   if (w8)
     return w.a_dt == MLS_BF16 ? launch16<A_RAW16, B_INT4, __bf16, __bf16, BM, 256, 2, 4, true>(p, w.stream)
                               : launch16<A_RAW16, B_INT4, _Float16, _Float16, BM, 256, 2, 4, true>(p, w.stream);
