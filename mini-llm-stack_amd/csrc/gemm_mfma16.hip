@@ -23,104 +23,9 @@
 // consecutive n of one m and the epilogue writes 4 outputs per store. Scales:
 // INT8 per n in the epilogue; INT4 per (n, group) on fp32 partial sums at every
 // group boundary; e4m3 per m and per n (or per tensor) in the epilogue.
-#include "wq.h"
+#include "mfma16.h"
 
 namespace mls {
-
-enum { A_RAW16 = 0, A_E4M3 = 1 };
-enum { B_INT8 = 0, B_INT4 = 1, B_E4M3 = 2 };
-
-struct Mfma16Params {
-  const void* a;
-  int64_t lda;  // elements of A's storage type (16-bit, or bytes for e4m3)
-  const uint8_t* b;
-  int64_t ldb;  // bytes
-  const void* s;  // INT8 [N] / INT4 [N][G] scales
-  int s_dt;
-  int64_t ld_sn, ld_sg;
-  int group;
-  float sa, sb;  // e4m3 per-tensor scales (used when the pointers are null)
-  const float* sap;
-  const float* sbp;
-  int64_t sas, sbs;
-  void* c;
-  int64_t ldc;
-  int M, N, K;
-  int n_tiles, m_tiles;
-  const int32_t* seg_off;  // grouped: expert row offsets [E + 1]
-  int E;
-  int64_t b_estride, s_estride;  // grouped: bytes / scale elements between experts
-};
-
-template <typename T> struct Mfma16;
-template <> struct Mfma16<__bf16> {
-  __device__ static __forceinline__ f32x4 mma(const uint4& a, const uint4& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-  }
-  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
-    bf16x2 v;
-    v.x = (__bf16)lo;
-    v.y = (__bf16)hi;
-    return __builtin_bit_cast(uint32_t, v);
-  }
-};
-template <> struct Mfma16<_Float16> {
-  __device__ static __forceinline__ f32x4 mma(const uint4& a, const uint4& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
-                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
-  }
-  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
-    f16x2 v;
-    v.x = (_Float16)lo;
-    v.y = (_Float16)hi;
-    return __builtin_bit_cast(uint32_t, v);
-  }
-};
-
-__device__ __forceinline__ int swz(int row) { return row & 7; }
-
-__device__ __forceinline__ float scale_at(const void* s, int s_dt, int64_t i) {
-  return s_dt == MLS_F16 ? (float)((const _Float16*)s)[i] : ((const float*)s)[i];
-}
-
-__device__ __forceinline__ float u8f(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xFFu); }
-
-// 16 INT8 weights -> 16 exact 16-bit floats (8 dwords, k order).
-template <typename MT>
-__device__ __forceinline__ void widen_int8(const uint4& q, uint32_t* o) {
-  const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const uint32_t u = d[t] ^ 0x80808080u;  // q + 128
-    o[2 * t + 0] = Mfma16<MT>::pack2(u8f(u, 0) - 128.0f, u8f(u, 1) - 128.0f);
-    o[2 * t + 1] = Mfma16<MT>::pack2(u8f(u, 2) - 128.0f, u8f(u, 3) - 128.0f);
-  }
-}
-
-// 32 INT4 weights (even k in the low nibble) -> 32 exact values v - 8 (16 dwords).
-template <typename MT>
-__device__ __forceinline__ void widen_int4(const uint4& q, uint32_t* o) {
-  const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const uint32_t lo = d[t] & 0x0F0F0F0Fu;         // k = 8t + 0, 2, 4, 6
-    const uint32_t hi = (d[t] >> 4) & 0x0F0F0F0Fu;  // k = 8t + 1, 3, 5, 7
-#pragma unroll
-    for (int b = 0; b < 4; ++b)
-      o[4 * t + b] = Mfma16<MT>::pack2(u8f(lo, b) - 8.0f, u8f(hi, b) - 8.0f);
-  }
-}
-
-// 16 e4m3 bytes -> 16 bf16 (8 dwords, k order); exact: e4m3 is a subset of bf16.
-__device__ __forceinline__ void widen_e4m3(const uint4& q, uint32_t* o) {
-  const uint32_t d[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    o[2 * t + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[t], 1.0f, false));
-    o[2 * t + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[t], 1.0f, true));
-  }
-}
 
 template <int AKIND, int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN,
           bool GROUPED, bool DEEP>
@@ -411,10 +316,6 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_gemm_kernel(const Mfma16P
 //   5. the MFMAs, then the barrier.
 // The compiler keeps LDS reads behind pending LDS-direct loads; with this order the
 // only such wait is the barrier's own, after the MFMAs have covered the load.
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds, int voff, int soff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff,
-                                           soff, 0, 0);
-}
 
 template <int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN, bool GROUPED>
 __global__ __launch_bounds__(64 * WM * WN) void mfma16_adma_kernel(const Mfma16Params p) {
@@ -427,8 +328,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_adma_kernel(const Mfma16P
   static_assert(PW >= 1 && BM * 8 % (64 * NW) == 0, "activation slots");
   constexpr int B_CPR = BKIND == B_INT4 ? 2 : 4;
   constexpr int B_CH = BN * B_CPR;
-  static_assert(B_CH % NT == 0, "BN too small for the weight staging");
-  constexpr int B_PT = B_CH / NT;
+  constexpr int B_PT = (B_CH + NT - 1) / NT;  // the last one guarded when B_CH % NT != 0
   constexpr int B_RSTEP = NT / B_CPR;
   constexpr bool GS = BKIND == B_INT4;
   static_assert(!GS || BN <= NT, "one thread per group scale");
@@ -497,7 +397,8 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_adma_kernel(const Mfma16P
   auto load_b = [&](int k0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < B_PT; ++i)
-      rb[i] = __builtin_bit_cast(
+      if (B_CH % NT == 0 || tid + NT * i < B_CH)
+        rb[i] = __builtin_bit_cast(
           uint4, __builtin_amdgcn_raw_buffer_load_b128(rsb, b_off[i], BKIND == B_INT4 ? k0 / 2 : k0, 0));
     if constexpr (GS) {
       if (tid < BN) {
@@ -511,6 +412,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_adma_kernel(const Mfma16P
     uint4* bs = Bs + buf * BN * 8;
 #pragma unroll
     for (int i = 0; i < B_PT; ++i) {
+      if (B_CH % NT != 0 && tid + NT * i >= B_CH) continue;
       const int row = b_row0 + B_RSTEP * i;
       if constexpr (BKIND == B_INT4) {
         uint32_t o[16];
@@ -714,7 +616,8 @@ static int pick_bm(int64_t M, int64_t N, int max_bm) {
 // Tuning overrides for sweeps: MLS_MFMA_WAVES = 4 or 8 wavefronts per block (default 8:
 // two per SIMD, so one wavefront's memory waits overlap the other's MFMAs), MLS_MFMA_BM =
 // forced row-tile height (16 .. 256), MLS_MFMA_ADMA = 0 stages 16-bit activations
-// through registers instead of loading them straight into LDS.
+// through registers instead of loading them straight into LDS, MLS_MFMA_BN = 256 or 192
+// forces the column-tile width of the 256-row weight-only kernel.
 static int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
   return v && *v ? atoi(v) : dflt;
@@ -732,7 +635,17 @@ static int dense16(Mfma16Params p, hipStream_t st) {
   static const bool adma = env_int("MLS_MFMA_ADMA", 1) != 0;
   if constexpr (AKIND == A_RAW16) {
     if (adma && w8 && bm == 256) {
-      if constexpr (MAXBM >= 256) return launch_adma<BKIND, MT, OT, 256, 256, 2, 4, false>(p, st);
+      if constexpr (MAXBM >= 256) {
+        // 256 x 192 tiles when fewer rounds of 256 blocks outweigh the smaller tile:
+        // e.g. 2048 x 11008 is 344 blocks of 256 x 256 (two rounds, the second a
+        // third full) but 464 blocks of 256 x 192 (two rounds, 25% less work each)
+        static const int force_bn = env_int("MLS_MFMA_BN", 0);
+        const int64_t mt = cdiv(p.M, 256);
+        const int64_t c256 = cdiv(mt * cdiv(p.N, 256), 256) * 256, c192 = cdiv(mt * cdiv(p.N, 192), 256) * 192;
+        if (force_bn == 192 || (force_bn != 256 && c192 < c256))
+          return launch_adma<BKIND, MT, OT, 256, 192, 2, 4, false>(p, st);
+        return launch_adma<BKIND, MT, OT, 256, 256, 2, 4, false>(p, st);
+      }
     }
     if (adma && w8 && bm == 128) return launch_adma<BKIND, MT, OT, 128, 256, 2, 4, false>(p, st);
   }

@@ -1,0 +1,137 @@
+// Shared pieces of the 16-bit MFMA GEMM kernels: launch parameters, the MFMA
+// wrappers, the exact widening of INT8 / INT4 / e4m3 chunks to 16-bit floats, the
+// LDS swizzle, and the buffer load that writes LDS directly.
+#pragma once
+
+#include "wq.h"
+
+namespace mls {
+
+enum { A_RAW16 = 0, A_E4M3 = 1 };
+enum { B_INT8 = 0, B_INT4 = 1, B_E4M3 = 2 };
+
+struct Mfma16Params {
+  const void* a;
+  int64_t lda;  // elements of A's storage type (16-bit, or bytes for e4m3)
+  const uint8_t* b;
+  int64_t ldb;  // bytes
+  const void* s;  // INT8 [N] / INT4 [N][G] scales
+  int s_dt;
+  int64_t ld_sn, ld_sg;
+  int group;
+  float sa, sb;  // e4m3 per-tensor scales (used when the pointers are null)
+  const float* sap;
+  const float* sbp;
+  int64_t sas, sbs;
+  void* c;
+  int64_t ldc;
+  int M, N, K;
+  int n_tiles, m_tiles;
+  const int32_t* seg_off;  // grouped: expert row offsets [E + 1]
+  int E;
+  int64_t b_estride, s_estride;  // grouped: bytes / scale elements between experts
+};
+
+template <typename T> struct Mfma16;
+template <> struct Mfma16<__bf16> {
+  __device__ static __forceinline__ f32x4 mma(const uint4& a, const uint4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    bf16x2 v;
+    v.x = (__bf16)lo;
+    v.y = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+template <> struct Mfma16<_Float16> {
+  __device__ static __forceinline__ f32x4 mma(const uint4& a, const uint4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
+    f16x2 v;
+    v.x = (_Float16)lo;
+    v.y = (_Float16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+};
+
+__device__ __forceinline__ int swz(int row) { return row & 7; }
+
+__device__ __forceinline__ float scale_at(const void* s, int s_dt, int64_t i) {
+  return s_dt == MLS_F16 ? (float)((const _Float16*)s)[i] : ((const float*)s)[i];
+}
+
+__device__ __forceinline__ float u8f(uint32_t v, int b) { return (float)((v >> (8 * b)) & 0xFFu); }
+
+// Signed byte b of v as an exact fp32 (one SDWA convert with sign extension).
+template <int B>
+__device__ __forceinline__ float sbyte_f32(uint32_t v) {
+  float r;
+  if constexpr (B == 0)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(v));
+  else if constexpr (B == 1)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(v));
+  else if constexpr (B == 2)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(v));
+  else
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(v));
+  return r;
+}
+
+// Two exact small integers (|v| <= 256) held as fp32 -> one dword of 16-bit floats.
+// bf16: the fp32 of such an integer has zero low 16 bits, so its high half is exact.
+template <typename MT>
+__device__ __forceinline__ uint32_t pack_exact2(float lo, float hi) {
+  if constexpr (sizeof(MT) == 2 && __is_same(MT, _Float16))
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+  else
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, hi), __builtin_bit_cast(uint32_t, lo), 0x07060302u);
+}
+
+// 16 INT8 weights -> 16 exact 16-bit floats (8 dwords, k order): 6 VALU per 4 weights.
+template <typename MT>
+__device__ __forceinline__ void widen_int8(const uint4& q, uint32_t* o) {
+  const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    o[2 * t + 0] = pack_exact2<MT>(sbyte_f32<0>(d[t]), sbyte_f32<1>(d[t]));
+    o[2 * t + 1] = pack_exact2<MT>(sbyte_f32<2>(d[t]), sbyte_f32<3>(d[t]));
+  }
+}
+
+// 32 INT4 weights (even k in the low nibble) -> 32 exact values v - 8 (16 dwords).
+template <typename MT>
+__device__ __forceinline__ void widen_int4(const uint4& q, uint32_t* o) {
+  const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t lo = d[t] & 0x0F0F0F0Fu;         // k = 8t + 0, 2, 4, 6
+    const uint32_t hi = (d[t] >> 4) & 0x0F0F0F0Fu;  // k = 8t + 1, 3, 5, 7
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      o[4 * t + b] = Mfma16<MT>::pack2(u8f(lo, b) - 8.0f, u8f(hi, b) - 8.0f);
+  }
+}
+
+// 16 e4m3 bytes -> 16 bf16 (8 dwords, k order); exact: e4m3 is a subset of bf16.
+__device__ __forceinline__ void widen_e4m3(const uint4& q, uint32_t* o) {
+  const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    o[2 * t + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[t], 1.0f, false));
+    o[2 * t + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[t], 1.0f, true));
+  }
+}
+
+
+// One 16-byte global chunk per lane straight into LDS (buffer_load_dwordx4 ... lds): lane l
+// writes LDS bytes [16 l, 16 l + 16) above `lds`.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff,
+                                           soff, 0, 0);
+}
+
+}  // namespace mls
