@@ -706,6 +706,10 @@ int launch_grouped_int4(const GroupedArgs& g) {
   p.s = w.s; p.s_dt = w.s_dt; p.ld_sn = w.ld_sn; p.ld_sg = w.ld_sg; p.group = w.group;
   p.c = w.c; p.ldc = w.ldc; p.M = (int)w.M; p.N = (int)w.N; p.K = (int)w.K;
   p.seg_off = g.seg_off; p.E = g.E; p.b_estride = g.w_estride; p.s_estride = g.s_estride;
+  // MLS_GROUPED_TILES = 1: the row-tile kernels below instead of one block per expert
+  // row chunk (gemm_grouped.hip)
+  static const bool tiles = env_int("MLS_GROUPED_TILES", 0) != 0;
+  if (!tiles) return launch_grouped_seg(p, w.stream, w.a_dt == MLS_BF16);
   // upper bound on sum_e ceil(rows_e / BM) without reading the device offsets
   p.m_tiles = (int)(cdiv(w.M, BM) + g.E);
   static const bool w8 = env_int("MLS_MFMA_WAVES", 8) == 8;

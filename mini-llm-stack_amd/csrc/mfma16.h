@@ -134,4 +134,7 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds,
                                            soff, 0, 0);
 }
 
+// Grouped INT4 GEMM with one block per (expert row chunk, 128 columns) (gemm_grouped.hip).
+int launch_grouped_seg(const Mfma16Params& p, hipStream_t st, bool bf16);
+
 }  // namespace mls

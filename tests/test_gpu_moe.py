@@ -44,6 +44,25 @@ def test_grouped_small(dev, counts):
     assert torch.equal(out, out2)
 
 
+@pytest.mark.parametrize("gs,dtype", [(32, torch.bfloat16), (64, torch.float16), (256, torch.bfloat16),
+                                      (128, torch.float16)])
+def test_grouped_group_sizes(dev, gs, dtype):
+    """Group boundaries inside a 64-k stage (32), at every stage (64), every fourth stage
+    (256); fp16 activations; ragged N; a segment split over several row chunks."""
+    counts = [7, 170, 0, 33, 96]
+    E, N, K = len(counts), 200, 512
+    P, S = _experts(dev, E, N, K, gs, gs)
+    M = sum(counts)
+    g = torch.Generator().manual_seed(gs)
+    a = torch.randn(M, K, generator=g).to(dtype)
+    out = int4_grouped_matmul(a.to(dev), P, S, torch.tensor(counts, device=dev), gs)
+    assert out.dtype == dtype
+    off = np.concatenate([[0], np.cumsum(counts)])
+    want = ref.grouped_int4_matmul(a.float().numpy(), P.cpu().numpy(), S.float().cpu().numpy(), off, gs)
+    ok, worst = ref.close_bf16(out.float().cpu().numpy(), want)
+    assert ok, f"worst {worst:.3g}"
+
+
 def test_config_e(dev):
     """512 tokens, hidden 4096, 8 experts with W_up [14336, 4096]
     INT4 g128, top-2 softmax routing from logits ~ N(0, 1), expert-sorted segments."""
