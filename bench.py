@@ -11,7 +11,8 @@ HIP graph of back-to-back launches, replayed on the launching stream between
 HIP events; value = algorithmic bytes x K / elapsed.
 
 The other BASELINE configs (INT4 M = 4 / 16, the INT8 GEMV target, INT8 prefill,
-FP8 e4m3 GEMM, INT4 MoE grouped GEMM) are reported under "extra" with the same
+FP8 e4m3 GEMM, INT4 MoE grouped GEMM) and the whole INT4 SwiGLU expert MLP of a
+routed MoE layer (gate/up, down, combine) are reported under "extra" with the same
 protocol, followed by a 256 MiB streaming copy (the bandwidth a plain elementwise
 kernel reaches on this GPU). cpu_baseline times the reference's CPU algorithm (the numpy
 restatement in oracle/: dequantize, then fp32 matmul) on the host for a bounded
@@ -190,6 +191,40 @@ def moe_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=128):
                 counts=counts.tolist())
 
 
+def moe_mlp_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=128):
+    """The whole INT4 SwiGLU expert MLP of a routed MoE layer after dispatch: the fused
+    gate/up launch (silu(x Wg^T) * x Wu^T), the down launch, and the weighted combine
+    back to token order (kernels/moe_routing.py:145-153 with INT4 experts)."""
+    import torch
+    from kernels.moe_grouped import int4_expert_mlp, segment_offsets
+    from kernels.moe_routing import combine_rows, gather_rows, route_topk, sort_by_expert
+    from serve.quantize import quantize_int4
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(T, D, generator=g, device=dev).to(torch.bfloat16)
+    w, ex = route_topk(torch.randn(T, E, generator=g, device=dev), 2)
+    w = w.to(torch.bfloat16)
+    tok, counts, pos = sort_by_expert(ex, E)
+    a = gather_rows(x, tok)
+    off = segment_offsets(counts)
+    copies = 2
+    sets = []
+    for _ in range(copies):
+        mats = []
+        for n, k in ((H, D), (H, D), (D, H)):
+            P, S = [], []
+            for _ in range(E):
+                p, s = quantize_int4(torch.randn(n, k, generator=g, device=dev) * 0.02, gs)
+                P.append(p)
+                S.append(s.to(torch.float16))
+            mats += [torch.stack(P), torch.stack(S)]
+        sets.append(mats)
+    fns = [lambda m=m: combine_rows(int4_expert_mlp(a, off, *m, gs), w, pos) for m in sets]
+    ms = time_steps(fns, warmup, steps)
+    rows = T * 2
+    nbytes = 3 * (E * H * D // 2 + E * H * (D // gs) * 2) + rows * D * 2 * 2 + rows * H * 2 * 2 + T * D * 2
+    return dict(ms=ms, bytes=nbytes, flops=6 * rows * H * D, copies=copies, counts=counts.tolist())
+
+
 def copy_calibration(dev, steps: int, warmup: int, nbytes: int = 256 << 20):
     """A plain streaming kernel of known traffic (torch's elementwise bitwise_not over
     int32: reads nbytes, writes nbytes). Its rocprofv3 FETCH_SIZE / WRITE_SIZE
@@ -283,7 +318,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--only", default=None,
                     help="run one workload: int4_gemv, int4_m4, int4_m16, int8_gemv, int8_prefill, "
-                         "fp8_gemm, fp8_native, moe_int4, copy (counter calibration)")
+                         "fp8_gemm, fp8_native, moe_int4, moe_mlp_int4, copy (counter calibration)")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
@@ -319,6 +354,13 @@ def main(argv=None) -> int:
                                                      r["bytes"] / (r["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                                                   "segments": r["counts"]}))(
             moe_int4(dev, small, 4)),
+        "moe_mlp_int4": lambda: (lambda r: _mfma_row("moe_int4_swiglu_mlp_T512_k2_E8_4096x14336", r,
+                                                     BF16_PEAK_TFLOPS,
+                                                     {"hbm_roofline_frac": round(
+                                                         r["bytes"] / (r["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                                      "launches": "gate/up + down + combine",
+                                                      "segments": r["counts"]}))(
+            moe_mlp_int4(dev, small, 4)),
         "copy": lambda: _hbm_row("copy_256MiB", copy_calibration(dev, small, 4)),
     }
     if args.only:
@@ -334,7 +376,7 @@ def main(argv=None) -> int:
     extra = []
     if not args.no_extra:
         for k in ("int4_m4", "int4_m16", "int8_gemv", "int8_prefill", "fp8_gemm", "fp8_native",
-                  "moe_int4", "copy"):
+                  "moe_int4", "moe_mlp_int4", "copy"):
             log(f"{k} ...")
             row = runners[k]()
             log(json.dumps(row))

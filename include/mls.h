@@ -39,7 +39,7 @@ enum {
   MLS_ERR_HIP = -3          /* a HIP runtime call failed */
 };
 
-#define MLS_ABI_VERSION 1
+#define MLS_ABI_VERSION 2
 
 /* No reference counterpart: version of this ABI (MLS_ABI_VERSION). */
 int mls_abi_version(void);
@@ -146,6 +146,33 @@ int mls_int4_grouped_gemm(const void* a, int a_dt, int64_t lda,
                           int64_t ld_sn, int64_t ld_sg, int group,
                           void* c, int c_dt, int64_t ldc,
                           int64_t N, int64_t K, mls_stream_t stream);
+
+/* ---------------------------------------------------------------- MoE expert MLP */
+
+/* The gate/up half of the quantized SwiGLU expert MLP (train/model.py:127-135,
+ * SwiGLU.forward: w_down(silu(w_gate(x)) * w_up(x)), with w_gate / w_up swapped for
+ * INT4 QuantLinear by serve/quantize.py:110-114) for every expert in one launch:
+ * h[r] = silu(a[r] . dequant(wg_e)^T) * (a[r] . dequant(wu_e)^T) for the rows r of
+ * expert e's segment, fp32 accumulation, one rounding to h_dt (= a_dt, F16 or BF16).
+ * The reference runs this as two QuantLinear calls per expert plus elementwise ops
+ * (moe_routing.py:145-151 loop); here the 2 x H intermediate never reaches memory.
+ * Layouts and seg_off as for mls_int4_grouped_gemm; the up matrices/scales share the
+ * gate's strides. */
+int mls_int4_grouped_gate_up(const void* a, int a_dt, int64_t lda,
+                             const int32_t* seg_off, int E, int64_t M_total,
+                             const uint8_t* wg, const uint8_t* wu, int64_t w_estride, int64_t ldw,
+                             const void* sg, const void* su, int s_dt, int64_t s_estride,
+                             int64_t ld_sn, int64_t ld_sg, int group,
+                             void* h, int h_dt, int64_t ldh,
+                             int64_t H, int64_t K, mls_stream_t stream);
+
+/* Replaces _combine_rows_kernel + combine_rows (kernels/moe_routing.py:52-76, 100-113):
+ * out[t][d] = sum_{s<k} w[t][s] * x[pos[t][s]][d], fp32 accumulation, one rounding;
+ * one block per output row, no atomics. x: x_dt [x_rows][ldx]; out: x_dt; w: w_dt ([T][k]);
+ * pos: int64 [T][k]; a position outside [0, x_rows) contributes nothing. */
+int mls_moe_combine(const void* x, int x_dt, int64_t ldx, int64_t x_rows, const void* w, int w_dt,
+                    const int64_t* pos, int64_t T, int k, void* out, int64_t ldo,
+                    int64_t D, mls_stream_t stream);
 
 #ifdef __cplusplus
 }

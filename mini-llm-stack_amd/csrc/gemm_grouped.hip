@@ -54,9 +54,13 @@ __device__ __forceinline__ void widen_int4x16(const uint4& q, uint32_t* o) {
 // into LDS (G <= 32, contiguous groups). Otherwise each stage loads the scales of its
 // 128 rows; those loads touch one cache line per row, many more L2 requests than the
 // weights themselves, and their latency then dominates the stage.
-template <typename MT, typename OT, int TMX, bool STAB>
+// GU (gate/up of a SwiGLU expert MLP): the block's 128 weight rows are 64 rows of the
+// gate matrix (p.b, p.s) and the same 64 rows of the up matrix (p.b2, p.s2); the
+// epilogue writes h = silu(gate) * up for those 64 columns, from the fp32 accumulators.
+template <typename MT, typename OT, int TMX, bool STAB, bool GU>
 __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params p) {
   constexpr int BN = 128, BK = 64, NT = 256;
+  constexpr int OUTN = GU ? 64 : 128;  // output columns per block
   constexpr int BMX = 32 * TMX, TN = 4;
   constexpr int PW = BMX * 8 / NT;  // activation LDS-direct loads per thread and stage
   static_assert(BMX * 8 % NT == 0, "activation slots");
@@ -89,16 +93,22 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   const int m0 = __builtin_amdgcn_readfirstlane(lo + (chunk - cum) * BMX);
   const int rows = __builtin_amdgcn_readfirstlane(min(BMX, hi - m0));
   const int nsub = (rows + 15) >> 4;  // active 16-row subtiles
+  const int ssz = p.s_dt == MLS_F16 ? 2 : 4;
   const uint8_t* bmat = p.b + (int64_t)e * p.b_estride;
-  const uint8_t* smat = (const uint8_t*)p.s + (int64_t)e * p.s_estride * (p.s_dt == MLS_F16 ? 2 : 4);
-  const int n0 = nt * BN, N = p.N;
+  const uint8_t* smat = (const uint8_t*)p.s + (int64_t)e * p.s_estride * ssz;
+  const int n0 = nt * OUTN, N = p.N;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 15, lk = lane >> 4;
+  if constexpr (GU) {
+    // waves 2 and 3 stage B rows 64 .. 127: the up matrix
+    if (wave >= 2) bmat = p.b2 + (int64_t)e * p.b_estride;
+  }
+  const uint8_t* smat_hi = GU ? (const uint8_t*)p.s2 + (int64_t)e * p.s_estride * ssz : smat;
 
-  const int rows_b = __builtin_amdgcn_readfirstlane(min(BN, N - n0));
+  const int rows_b = __builtin_amdgcn_readfirstlane(min(OUTN, N - n0));
   const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
       (void*)((const uint8_t*)p.a + (int64_t)m0 * p.lda * 2), (short)0, (int)(rows * p.lda * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
@@ -110,10 +120,13 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
     const int t = (wave * PW + i) * 64 + lane, row = t >> 3, lc = (t & 7) ^ (row & 7);
     a_off[i] = row * (int)p.lda * 2 + lc * 16;
   }
-  // weights: thread tid stages row tid / 2, 16-byte column tid % 2 (32 k) of the stage
+  // weights: thread tid stages B row tid / 2 (GU: row (tid / 2) % 64 of its matrix),
+  // 16-byte column tid % 2 (32 k) of the stage
   const int b_row = tid >> 1, b_cc = tid & 1;
-  const int b_off = b_row * (int)p.ldb + b_cc * 16;
-  const int64_t s_row = (int64_t)min(n0 + (tid & (BN - 1)), N - 1) * p.ld_sn;
+  const int b_off = (GU ? (b_row & 63) : b_row) * (int)p.ldb + b_cc * 16;
+  const int s_r = tid & (BN - 1);  // B row whose per-stage scales this thread loads
+  const uint8_t* s_mat = (GU && s_r >= 64) ? smat_hi : smat;
+  const int64_t s_row = (int64_t)min(n0 + (GU ? (s_r & 63) : s_r), N - 1) * p.ld_sn;
 
   // weights of the stage to store next (rb, rs0, rs1) and of the one after (nb, ns0, ns1)
   uint4 rb, nb;
@@ -128,8 +141,8 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
     w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsb, b_off, k0 / 2, 0));
     if constexpr (!STAB) {
       const int kc = min(k0, p.K - BK);  // a stage past the end reuses the last scales
-      s0 = scale_at(smat, p.s_dt, s_row + (int64_t)(kc / p.group) * p.ld_sg) * 0.0625f;
-      s1 = scale_at(smat, p.s_dt, s_row + (int64_t)((kc + 32) / p.group) * p.ld_sg) * 0.0625f;
+      s0 = scale_at(s_mat, p.s_dt, s_row + (int64_t)(kc / p.group) * p.ld_sg) * 0.0625f;
+      s1 = scale_at(s_mat, p.s_dt, s_row + (int64_t)((kc + 32) / p.group) * p.ld_sg) * 0.0625f;
     }
   };
   auto store_b = [&](int buf) __attribute__((always_inline)) {
@@ -161,8 +174,9 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
     const int G = p.K / p.group, ppr = G / 8;
     for (int c = tid; c < BN * ppr; c += 256) {
       const int r = c / ppr, part = c % ppr;
-      const int64_t n = min(n0 + r, N - 1);
-      const uint4 v = *reinterpret_cast<const uint4*>((const _Float16*)smat + n * p.ld_sn + part * 8);
+      const int64_t n = min(n0 + (GU ? (r & 63) : r), N - 1);
+      const uint8_t* sm = (GU && r >= 64) ? smat_hi : smat;
+      const uint4 v = *reinterpret_cast<const uint4*>((const _Float16*)sm + n * p.ld_sn + part * 8);
       const _Float16* h = reinterpret_cast<const _Float16*>(&v);
 #pragma unroll
       for (int t = 0; t < 8; ++t) sT[(part * 8 + t) * BN + r] = h[t];
@@ -262,6 +276,48 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
 
   // ---- epilogue: acc[i][j][r] = C[m = m0 + (2 j + wm) 16 + lr][n = n0 + 64 wn + 16 i + 4 lk + r]
   OT* c = static_cast<OT*>(p.c);
+  if constexpr (GU) {
+    // wavefronts wn = 1 hold the up products: they pass them through LDS (the
+    // activation buffers, free after the loop's last barrier) to the wavefronts wn = 0,
+    // which hold the gate products of the same (m, n) and write silu(gate) * up
+    float* U = reinterpret_cast<float*>(smem);  // [BMX][64]
+    if (wn == 1) {
+#pragma unroll
+      for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TMX; ++j)
+          *reinterpret_cast<f32x4*>(U + ((2 * j + wm) * 16 + lr) * 64 + i * 16 + 4 * lk) = acc[i][j];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    if (wn == 1) return;
+#pragma unroll
+    for (int i = 0; i < TN; ++i) {
+      const int nb = n0 + i * 16 + 4 * lk;
+#pragma unroll
+      for (int j = 0; j < TMX; ++j) {
+        const int ml = (2 * j + wm) * 16 + lr;
+        if (ml >= rows) continue;
+        const f32x4 u = *reinterpret_cast<const f32x4*>(U + ml * 64 + i * 16 + 4 * lk);
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float g = acc[i][j][r];
+          v[r] = g / (1.0f + __expf(-g)) * u[r];
+        }
+        OT* dst = c + (int64_t)(m0 + ml) * p.ldc + nb;
+        if (nb + 3 < N && (p.ldc % 4) == 0) {
+          store4<OT>(dst, v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (nb + r < N) dst[r] = from_f32<OT>(v[r]);
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < TN; ++i) {
     const int nb = n0 + wn * 64 + i * 16 + 4 * lk;
@@ -281,15 +337,15 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   }
 }
 
-template <typename MT, int TMX, bool STAB>
+template <typename MT, int TMX, bool STAB, bool GU>
 static int launch_grouped(Mfma16Params p, hipStream_t st) {
-  constexpr int BMX = 32 * TMX, BN = 128;
-  p.n_tiles = (int)cdiv(p.N, BN);
+  constexpr int BMX = 32 * TMX, BN = 128, OUTN = GU ? 64 : 128;
+  p.n_tiles = (int)cdiv(p.N, OUTN);
   // upper bound on sum_e ceil(rows_e / BMX) without reading the device offsets
   p.m_tiles = (int)(cdiv(p.M, BMX) + p.E);
   const size_t tab = STAB ? (size_t)BN * 32 * 2 : (size_t)2 * 2 * BN * 4;
   const size_t lds = (size_t)2 * (BMX + BN) * 8 * 16 + tab;
-  auto kern = grouped_int4_kernel<MT, MT, TMX, STAB>;
+  auto kern = grouped_int4_kernel<MT, MT, TMX, STAB, GU>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -300,31 +356,33 @@ static int launch_grouped(Mfma16Params p, hipStream_t st) {
   const int64_t blocks = (int64_t)p.n_tiles * p.m_tiles;
   if (blocks > 0x7FFFFFFF) return MLS_ERR_UNSUPPORTED;
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, st, p);
-  return check_launch("grouped INT4 GEMM");
+  return check_launch(GU ? "grouped INT4 gate/up GEMM" : "grouped INT4 GEMM");
+}
+
+template <bool STAB, bool GU>
+static int launch_grouped_tmx(const Mfma16Params& p, hipStream_t st, bool bf16, int tmx) {
+  switch (tmx) {
+    case 5: return bf16 ? launch_grouped<__bf16, 5, STAB, GU>(p, st) : launch_grouped<_Float16, 5, STAB, GU>(p, st);
+    case 4: return bf16 ? launch_grouped<__bf16, 4, STAB, GU>(p, st) : launch_grouped<_Float16, 4, STAB, GU>(p, st);
+    case 3: return bf16 ? launch_grouped<__bf16, 3, STAB, GU>(p, st) : launch_grouped<_Float16, 3, STAB, GU>(p, st);
+    default: return bf16 ? launch_grouped<__bf16, 2, STAB, GU>(p, st) : launch_grouped<_Float16, 2, STAB, GU>(p, st);
+  }
 }
 
 // Row-chunk height: the smallest of 64 / 96 / 128 / 160 rows that holds 1.25x the
 // average segment (routed segments scatter around the average), so a typical expert's
 // rows fit in one chunk and its weights are streamed and widened once.
-template <bool STAB>
-static int launch_grouped_tmx(const Mfma16Params& p, hipStream_t st, bool bf16, int tmx) {
-  switch (tmx) {
-    case 5: return bf16 ? launch_grouped<__bf16, 5, STAB>(p, st) : launch_grouped<_Float16, 5, STAB>(p, st);
-    case 4: return bf16 ? launch_grouped<__bf16, 4, STAB>(p, st) : launch_grouped<_Float16, 4, STAB>(p, st);
-    case 3: return bf16 ? launch_grouped<__bf16, 3, STAB>(p, st) : launch_grouped<_Float16, 3, STAB>(p, st);
-    default: return bf16 ? launch_grouped<__bf16, 2, STAB>(p, st) : launch_grouped<_Float16, 2, STAB>(p, st);
-  }
-}
-
-int launch_grouped_seg(const Mfma16Params& p, hipStream_t st, bool bf16) {
+int launch_grouped_seg(const Mfma16Params& p, hipStream_t st, bool bf16, bool gate_up) {
   const int64_t want = cdiv(p.M * 5, p.E * 4);
   const int tmx = want > 128 ? 5 : want > 96 ? 4 : want > 64 ? 3 : 2;
   // scale table in LDS: fp16 scales, contiguous groups, G a multiple of 8 up to 32,
   // 16-byte aligned rows
   const int64_t G = p.K / p.group;
   const bool stab = p.s_dt == MLS_F16 && p.ld_sg == 1 && G % 8 == 0 && G <= 32 && (p.ld_sn % 8) == 0 &&
-                    (p.s_estride % 8) == 0 && aligned(p.s, 16);
-  return stab ? launch_grouped_tmx<true>(p, st, bf16, tmx) : launch_grouped_tmx<false>(p, st, bf16, tmx);
+                    (p.s_estride % 8) == 0 && aligned(p.s, 16) && (!gate_up || aligned(p.s2, 16));
+  if (gate_up)
+    return stab ? launch_grouped_tmx<true, true>(p, st, bf16, tmx) : launch_grouped_tmx<false, true>(p, st, bf16, tmx);
+  return stab ? launch_grouped_tmx<true, false>(p, st, bf16, tmx) : launch_grouped_tmx<false, false>(p, st, bf16, tmx);
 }
 
 }  // namespace mls

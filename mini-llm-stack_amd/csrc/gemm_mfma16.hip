@@ -709,7 +709,7 @@ int launch_grouped_int4(const GroupedArgs& g) {
   // MLS_GROUPED_TILES = 1: the row-tile kernels below instead of one block per expert
   // row chunk (gemm_grouped.hip)
   static const bool tiles = env_int("MLS_GROUPED_TILES", 0) != 0;
-  if (!tiles) return launch_grouped_seg(p, w.stream, w.a_dt == MLS_BF16);
+  if (!tiles) return launch_grouped_seg(p, w.stream, w.a_dt == MLS_BF16, false);
   // upper bound on sum_e ceil(rows_e / BM) without reading the device offsets
   p.m_tiles = (int)(cdiv(w.M, BM) + g.E);
   static const bool w8 = env_int("MLS_MFMA_WAVES", 8) == 8;
@@ -722,6 +722,22 @@ int launch_grouped_int4(const GroupedArgs& g) {
                               : launch16<A_RAW16, B_INT4, _Float16, _Float16, BM, 256, 2, 4, true>(p, w.stream);
   return w.a_dt == MLS_BF16 ? launch16<A_RAW16, B_INT4, __bf16, __bf16, BM, 256, 2, 2, true>(p, w.stream)
                             : launch16<A_RAW16, B_INT4, _Float16, _Float16, BM, 256, 2, 2, true>(p, w.stream);
+}
+
+int launch_grouped_gate_up(const GroupedArgs& g, const uint8_t* wu, const void* su) {
+  const WqArgs& w = g.base;
+  if (w.a_dt != MLS_F16 && w.a_dt != MLS_BF16) return MLS_ERR_UNSUPPORTED;
+  if (w.K % 64 != 0 || w.group % 32 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(w.a, 16) || w.lda % 8 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(w.w, 16) || !aligned(wu, 16) || w.ldw % 16 != 0 || g.w_estride % 16 != 0)
+    return MLS_ERR_UNSUPPORTED;
+  if (!aligned(w.c, 8) || !tile_fits(w.lda * 2, w.ldw)) return MLS_ERR_UNSUPPORTED;
+  Mfma16Params p{};
+  p.a = w.a; p.lda = w.lda; p.b = w.w; p.ldb = w.ldw; p.b2 = wu;
+  p.s = w.s; p.s2 = su; p.s_dt = w.s_dt; p.ld_sn = w.ld_sn; p.ld_sg = w.ld_sg; p.group = w.group;
+  p.c = w.c; p.ldc = w.ldc; p.M = (int)w.M; p.N = (int)w.N; p.K = (int)w.K;
+  p.seg_off = g.seg_off; p.E = g.E; p.b_estride = g.w_estride; p.s_estride = g.s_estride;
+  return launch_grouped_seg(p, w.stream, w.a_dt == MLS_BF16, true);
 }
 
 int launch_fp8_exact(const Fp8Args& f) {

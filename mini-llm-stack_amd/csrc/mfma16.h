@@ -30,6 +30,8 @@ struct Mfma16Params {
   const int32_t* seg_off;  // grouped: expert row offsets [E + 1]
   int E;
   int64_t b_estride, s_estride;  // grouped: bytes / scale elements between experts
+  const uint8_t* b2;              // grouped gate/up: the up matrix (b is the gate)
+  const void* s2;
 };
 
 template <typename T> struct Mfma16;
@@ -134,7 +136,9 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds,
                                            soff, 0, 0);
 }
 
-// Grouped INT4 GEMM with one block per (expert row chunk, 128 columns) (gemm_grouped.hip).
-int launch_grouped_seg(const Mfma16Params& p, hipStream_t st, bool bf16);
+// Grouped INT4 GEMM with one block per (expert row chunk, 128 columns) (gemm_grouped.hip);
+// gate_up: the gate/up pair of a SwiGLU expert MLP (p.b/p.s gate, p.b2/p.s2 up), output
+// silu(gate) * up.
+int launch_grouped_seg(const Mfma16Params& p, hipStream_t st, bool bf16, bool gate_up);
 
 }  // namespace mls

@@ -45,6 +45,10 @@ struct GroupedArgs {
   int64_t s_estride;      // elements between experts' scales
 };
 int launch_grouped_int4(const GroupedArgs& p);
+// The gate/up pair of a SwiGLU expert MLP over expert-sorted segments: base.w / base.s
+// are the gate matrices, wu / su the up matrices (same strides); base.c receives
+// silu(a Wg^T) * (a Wu^T).
+int launch_grouped_gate_up(const GroupedArgs& p, const uint8_t* wu, const void* su);
 
 // e4m3 x e4m3 GEMM arguments (scales: pointer with a row stride, or the scalar).
 struct Fp8Args {

@@ -98,3 +98,28 @@ extern "C" int mls_int4_grouped_gemm(const void* a, int a_dt, int64_t lda, const
                 "%s: needs K %% 64 == 0, group %% 32 == 0 and 16-byte aligned rows", fn);
   return rc;
 }
+
+extern "C" int mls_int4_grouped_gate_up(const void* a, int a_dt, int64_t lda, const int32_t* seg_off,
+                                        int E, int64_t M_total, const uint8_t* wg, const uint8_t* wu,
+                                        int64_t w_estride, int64_t ldw, const void* sg, const void* su,
+                                        int s_dt, int64_t s_estride, int64_t ld_sn, int64_t ld_sg,
+                                        int group, void* h, int h_dt, int64_t ldh, int64_t H, int64_t K,
+                                        mls_stream_t stream) {
+  const char* fn = "mls_int4_grouped_gate_up";
+  GroupedArgs g{{a, a_dt, lda, wg, ldw, sg, s_dt, ld_sn, ld_sg, group, h, ldh, M_total, H, K,
+                 (hipStream_t)stream},
+                seg_off, E, w_estride, s_estride};
+  int rc = validate(fn, 4, g.base, h_dt);
+  if (rc != MLS_OK) return rc;
+  if (E < 1) return fail(MLS_ERR_ARG, "%s: E=%d < 1", fn, E);
+  if (w_estride < 0 || s_estride < 0) return fail(MLS_ERR_ARG, "%s: negative expert stride", fn);
+  if (M_total == 0 || H == 0) return MLS_OK;
+  if (!seg_off || !wu || !su) return fail(MLS_ERR_ARG, "%s: null pointer", fn);
+  if (a_dt != MLS_F16 && a_dt != MLS_BF16)
+    return fail(MLS_ERR_UNSUPPORTED, "%s: activations must be f16 or bf16", fn);
+  rc = launch_grouped_gate_up(g, wu, su);
+  if (rc == MLS_ERR_UNSUPPORTED)
+    return fail(MLS_ERR_UNSUPPORTED,
+                "%s: needs K %% 64 == 0, group %% 32 == 0 and 16-byte aligned rows", fn);
+  return rc;
+}

@@ -24,6 +24,14 @@ def segment_offsets(counts: torch.Tensor) -> torch.Tensor:
     return off
 
 
+def _offsets(counts_or_offsets: torch.Tensor, E: int, fn: str) -> torch.Tensor:
+    if counts_or_offsets.numel() == E:
+        return segment_offsets(counts_or_offsets)
+    if counts_or_offsets.numel() == E + 1:
+        return counts_or_offsets.reshape(-1).to(torch.int32).contiguous()
+    raise ValueError(f"{fn}: expected {E} counts or {E + 1} offsets, got {counts_or_offsets.numel()}")
+
+
 def int4_grouped_matmul(a_sorted: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor,
                         counts_or_offsets: torch.Tensor, group_size: int) -> torch.Tensor:
     """out[r] = a_sorted[r] @ dequant(w_packed[e], scale[e], group_size).T for every row r
@@ -39,13 +47,7 @@ def int4_grouped_matmul(a_sorted: torch.Tensor, w_packed: torch.Tensor, scale: t
     G = K // group_size
     if tuple(scale.shape) != (E, N, G):
         raise ValueError(f"int4_grouped_matmul: scale shape {tuple(scale.shape)}, expected {(E, N, G)}")
-    if counts_or_offsets.numel() == E:
-        off = segment_offsets(counts_or_offsets)
-    elif counts_or_offsets.numel() == E + 1:
-        off = counts_or_offsets.reshape(-1).to(torch.int32).contiguous()
-    else:
-        raise ValueError(f"int4_grouped_matmul: expected {E} counts or {E + 1} offsets, "
-                         f"got {counts_or_offsets.numel()}")
+    off = _offsets(counts_or_offsets, E, "int4_grouped_matmul")
     adt = dt_code(a_sorted.dtype, "int4_grouped_matmul")
     a = rows(a_sorted)
     w = w_packed if w_packed.is_contiguous() else w_packed.contiguous()
@@ -59,3 +61,53 @@ def int4_grouped_matmul(a_sorted: torch.Tensor, w_packed: torch.Tensor, scale: t
         w.data_ptr(), N * Kh, Kh, s.data_ptr(), sdt, N * G, G, 1, group_size,
         c.data_ptr(), adt, ld(c), N, K, stream(dev)), "int4_grouped_matmul")
     return c
+
+
+def int4_grouped_gate_up(a_sorted: torch.Tensor, wg_packed: torch.Tensor, sg: torch.Tensor,
+                         wu_packed: torch.Tensor, su: torch.Tensor,
+                         counts_or_offsets: torch.Tensor, group_size: int) -> torch.Tensor:
+    """h[r] = silu(a_sorted[r] @ dequant(wg[e]).T) * (a_sorted[r] @ dequant(wu[e]).T) for
+    every row r of expert e's segment: the first half of a SwiGLU expert MLP
+    (train/model.py:127-135) with INT4 gate/up weights, one launch for all experts.
+    wg/wu packed [E, H, K/2], sg/su [E, H, K/group] (same dtype) -> h [M_total, H]."""
+    dev = require_hip("int4_grouped_gate_up", a_sorted, wg_packed, sg, wu_packed, su, counts_or_offsets)
+    for w in (wg_packed, wu_packed):
+        if w.dim() != 3 or w.dtype != torch.uint8:
+            raise ValueError(f"int4_grouped_gate_up: packed weights must be uint8 [E, H, K/2], got "
+                             f"{w.dtype} {tuple(w.shape)}")
+    if wg_packed.shape != wu_packed.shape or sg.shape != su.shape or sg.dtype != su.dtype:
+        raise ValueError("int4_grouped_gate_up: gate and up weights/scales must have equal shapes and dtypes")
+    E, H, Kh = wg_packed.shape
+    M, K = a_sorted.shape
+    assert K % group_size == 0 and K == Kh * 2
+    G = K // group_size
+    if tuple(sg.shape) != (E, H, G):
+        raise ValueError(f"int4_grouped_gate_up: scale shape {tuple(sg.shape)}, expected {(E, H, G)}")
+    off = _offsets(counts_or_offsets, E, "int4_grouped_gate_up")
+    adt = dt_code(a_sorted.dtype, "int4_grouped_gate_up")
+    a = rows(a_sorted)
+    wg = wg_packed if wg_packed.is_contiguous() else wg_packed.contiguous()
+    wu = wu_packed if wu_packed.is_contiguous() else wu_packed.contiguous()
+    if sg.dtype not in (torch.float32, torch.float16):
+        sg, su = sg.to(torch.float32), su.to(torch.float32)
+    sg = sg if sg.is_contiguous() else sg.contiguous()
+    su = su if su.is_contiguous() else su.contiguous()
+    sdt = dt_code(sg.dtype, "int4_grouped_gate_up scale")
+    h = torch.empty(M, H, dtype=a.dtype, device=dev)
+    kernels.check(kernels.lib().mls_int4_grouped_gate_up(
+        a.data_ptr(), adt, ld(a), off.data_ptr(), E, M, wg.data_ptr(), wu.data_ptr(), H * Kh, Kh,
+        sg.data_ptr(), su.data_ptr(), sdt, H * G, G, 1, group_size,
+        h.data_ptr(), adt, ld(h), H, K, stream(dev)), "int4_grouped_gate_up")
+    return h
+
+
+def int4_expert_mlp(a_sorted: torch.Tensor, counts_or_offsets: torch.Tensor,
+                    wg: torch.Tensor, sg: torch.Tensor, wu: torch.Tensor, su: torch.Tensor,
+                    wd: torch.Tensor, sd: torch.Tensor, group_size: int) -> torch.Tensor:
+    """SwiGLU expert MLP w_down(silu(w_gate(x)) * w_up(x)) (train/model.py:127-135) with
+    INT4 weights for every expert's row segment: two launches (gate/up fused with the
+    activation, then down). wd packed [E, D, H/2], sd [E, D, H/group] -> [M_total, D]."""
+    E = wg.shape[0]
+    off = _offsets(counts_or_offsets, E, "int4_expert_mlp")
+    h = int4_grouped_gate_up(a_sorted, wg, sg, wu, su, off, group_size)
+    return int4_grouped_matmul(h, wd, sd, off, group_size)

@@ -7,13 +7,23 @@ GEMM (kernels.moe_grouped). Same conventions as the reference:
   per-expert counts and the inverse permutation (kernels/moe_routing.py:116-130);
 - gather_rows: out[i] = x[idx[i]] (kernels/moe_routing.py:89-97).
 
-These are index bookkeeping on the device (torch ops); the weighted combine of
-expert outputs is outside the quantized-linear path.
+- combine_rows: out[t] = sum_k w[t, k] * expert_out[pos[t, k]], one gfx950 block per
+  output row, no atomics (kernels/moe_routing.py:52-76, 100-113);
+- moe_dispatch_combine: the routed MoE forward (kernels/moe_routing.py:133-153). When
+  the experts are SwiGLU MLPs whose projections are INT4 QuantLinear with stacked
+  buffers (serve.quantize.quantize_model stacks them), the per-expert loop becomes two
+  grouped launches (kernels.moe_grouped.int4_expert_mlp); otherwise each expert module
+  runs on its segment as in the reference.
+
+sort and gather are index bookkeeping on the device (torch ops).
 """
 
 from __future__ import annotations
 
 import torch
+
+import kernels
+from kernels._hip import dt_code, ld, require_hip, stream
 
 
 def route_topk(logits: torch.Tensor, k: int):
@@ -37,3 +47,45 @@ def sort_by_expert(experts_idx: torch.Tensor, n_experts: int):
 
 def gather_rows(x: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
     return x.index_select(0, idx.to(torch.int64))
+
+
+def combine_rows(expert_out: torch.Tensor, weights: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+    """out[t] = sum_k weights[t, k] * expert_out[pos[t, k]], fp32 accumulation, output in
+    expert_out's dtype (kernels/moe_routing.py:100-113)."""
+    dev = require_hip("combine_rows", expert_out, weights, pos)
+    T, K = pos.shape
+    D = expert_out.shape[1]
+    x = expert_out if expert_out.stride(1) == 1 else expert_out.contiguous()
+    w = weights.contiguous()
+    p = pos.to(torch.int64).contiguous()
+    out = torch.empty(T, D, dtype=x.dtype, device=dev)
+    kernels.check(kernels.lib().mls_moe_combine(
+        x.data_ptr(), dt_code(x.dtype, "combine_rows"), ld(x), x.shape[0], w.data_ptr(), dt_code(w.dtype, "combine_rows weights"),
+        p.data_ptr(), T, K, out.data_ptr(), ld(out), D, stream(dev)), "combine_rows")
+    return out
+
+
+def moe_dispatch_combine(flat: torch.Tensor, weights: torch.Tensor, experts_idx: torch.Tensor,
+                         expert_modules) -> torch.Tensor:
+    """Routed MoE forward (kernels/moe_routing.py:133-153): sort the (token, slot)
+    assignments by expert, gather the rows, run every expert on its contiguous segment,
+    combine weighted by the router. flat [T, D], weights [T, k], experts_idx [T, k]."""
+    from kernels.moe_grouped import int4_expert_mlp, segment_offsets
+    from serve.quantize import stacked_int4_experts
+
+    n_experts = len(expert_modules)
+    token_of_slot, counts, pos = sort_by_expert(experts_idx, n_experts)
+    dispatched = gather_rows(flat, token_of_slot)
+    st = stacked_int4_experts(expert_modules)
+    if st is not None and dispatched.dtype in (torch.bfloat16, torch.float16):
+        expert_out = int4_expert_mlp(dispatched, segment_offsets(counts), st["w_gate"][0], st["w_gate"][1],
+                                     st["w_up"][0], st["w_up"][1], st["w_down"][0], st["w_down"][1],
+                                     st["group_size"])
+    else:
+        expert_out = torch.empty_like(dispatched)
+        start = 0
+        for e, cnt in enumerate(counts.tolist()):
+            if cnt:
+                expert_out[start:start + cnt] = expert_modules[e](dispatched[start:start + cnt])
+            start += cnt
+    return combine_rows(expert_out, weights, pos)

@@ -156,7 +156,76 @@ def quantize_model(model: nn.Module, bits: int = 8, group_size: int = 32,
         for m in mods:
             for name in _MLP_SLOTS:
                 setattr(m, name, QuantLinear(getattr(m, name), bits, group_size, use_kernel))
+        if getattr(blk, "is_moe", False):
+            stacked_int4_experts(mods)
     return model
+
+
+def _expert_slots_ok(experts) -> bool:
+    """True when every expert is a SwiGLU MLP (w_down(silu(w_gate(x)) * w_up(x)),
+    train/model.py:127-135) whose three projections are INT4 QuantLinear running the
+    HIP kernels, with one shape, group size, scale dtype and device across experts, and
+    shapes the grouped MFMA kernels take (K % 64 == 0, group % 32 == 0)."""
+    if len(experts) == 0:
+        return False
+    ref = None
+    for m in experts:
+        lins = [getattr(m, n, None) for n in _MLP_SLOTS]
+        if not all(isinstance(q, QuantLinear) and q.bits == 4 and q.use_kernel for q in lins):
+            return False
+        sig = tuple((tuple(q.w_q.shape), tuple(q.scale.shape), q.scale.dtype, q.group_size, q.w_q.device)
+                    for q in lins)
+        if ref is None:
+            ref = sig
+        elif sig != ref:
+            return False
+    g, u, d = ref
+    D, H, group, dev = g[0][1] * 2, g[0][0], g[3], g[4]
+    return (dev.type == "cuda" and u == g and d[0] == (D, H // 2) and group % 32 == 0
+            and D % 64 == 0 and H % 64 == 0 and g[2] in (torch.float32, torch.float16))
+
+
+def stacked_int4_experts(experts):
+    """Stacked INT4 buffers of a list of SwiGLU experts, for the grouped kernels of
+    kernels.moe_grouped: {"w_gate": (packed [E, H, D/2], scale [E, H, D/group]),
+    "w_up": (...), "w_down": (packed [E, D, H/2], scale [E, D, H/group]),
+    "group_size": g}, or None when the experts do not qualify (_expert_slots_ok).
+
+    The stack is built once: each slot's buffers are copied into one [E, ...] tensor
+    and every expert's QuantLinear buffers are re-pointed at views of it, so the
+    per-expert modules and the stacked tensors share memory. Later calls only check
+    that the buffers are still those views (they are not after .to() or a
+    load_state_dict that replaced them) and rebuild when they are not."""
+    if not _expert_slots_ok(experts):
+        return None
+    first = experts[0]
+    st = first.__dict__.get("_int4_stack")
+    if st is not None and len(st["experts"]) == len(experts) and all(
+            a is b for a, b in zip(st["experts"], experts)):
+        ok = True
+        for name in _MLP_SLOTS:
+            wq, sc = st[name]
+            for e, m in enumerate(experts):
+                q = getattr(m, name)
+                if q.w_q.data_ptr() != wq[e].data_ptr() or q.scale.data_ptr() != sc[e].data_ptr():
+                    ok = False
+                    break
+            if not ok:
+                break
+        if ok:
+            return st
+    st = {"experts": list(experts), "group_size": first.w_gate.group_size}
+    with torch.no_grad():
+        for name in _MLP_SLOTS:
+            lins = [getattr(m, name) for m in experts]
+            wq = torch.stack([q.w_q for q in lins]).contiguous()
+            sc = torch.stack([q.scale for q in lins]).contiguous()
+            for e, q in enumerate(lins):
+                q.w_q = wq[e]
+                q.scale = sc[e]
+            st[name] = (wq, sc)
+    first.__dict__["_int4_stack"] = st
+    return st
 
 
 def model_weight_bytes(model: nn.Module) -> int:

@@ -20,6 +20,17 @@ Each function cites the reference code it restates. Pins (see tests/test_oracle.
   *_matmul         fp64 brute-force triple loop on tiny inputs; golden fixture
                    of config A produced by torch's fp32 matmul.
   route / sort     torch softmax/topk/argsort golden fixture.
+  silu             closed forms: silu(0) = 0, silu(x) - silu(-x) = x, silu(x) -> x
+                   and -> 0 at the tails; torch.nn.functional.silu on the CPU.
+  grouped_*        per-expert loop against int4_matmul on each segment; gate/up
+                   against silu(int4_matmul) * int4_matmul computed per row.
+  combine_rows     the reference test's formula (test_moe_routing.py:21-28), brute
+                   force per element, one-hot weights reduce it to a gather, zero
+                   weights to zero, linearity in the weights.
+  naive_route      equals sort_by_expert + per-segment experts + combine_rows on
+                   random routings (two formulations of the same forward), and the
+                   reference's degenerate cases (all tokens to one expert,
+                   test_moe_routing.py:64-82).
 """
 
 from __future__ import annotations
@@ -185,6 +196,57 @@ def grouped_int4_matmul(a_sorted, packed, scale, offsets, group_size) -> np.ndar
         lo, hi = int(offsets[e]), int(offsets[e + 1])
         if hi > lo:
             out[lo:hi] = a[lo:hi] @ dequantize_int4(packed[e], scale[e], group_size).T
+    return out
+
+
+def silu(x) -> np.ndarray:
+    """x * sigmoid(x) in fp64 (torch.nn.functional.silu, train/model.py:135)."""
+    x = np.asarray(x, dtype=np.float64)
+    return x / (1.0 + np.exp(-x))
+
+
+def grouped_int4_gate_up(a_sorted, wg, sg, wu, su, offsets, group_size) -> np.ndarray:
+    """silu(x Wg_e^T) * (x Wu_e^T) for every row of expert e's segment: the inner
+    product of SwiGLU.forward (train/model.py:134-135) with INT4 gate/up experts, one
+    rounding at the end (fp32 result)."""
+    g = grouped_int4_matmul(a_sorted, wg, sg, offsets, group_size).astype(np.float64)
+    u = grouped_int4_matmul(a_sorted, wu, su, offsets, group_size).astype(np.float64)
+    return (silu(g) * u).astype(np.float32)
+
+
+def grouped_int4_swiglu(a_sorted, wg, sg, wu, su, wd, sd, offsets, group_size) -> np.ndarray:
+    """w_down(silu(w_gate(x)) * w_up(x)) per expert segment (train/model.py:134-135,
+    kernels/moe_routing.py:145-151) with INT4 projections; the hidden activation h
+    stays fp32 (a caller modelling a 16-bit h rounds it itself)."""
+    h = grouped_int4_gate_up(a_sorted, wg, sg, wu, su, offsets, group_size)
+    return grouped_int4_matmul(h, wd, sd, offsets, group_size)
+
+
+def combine_rows(expert_out, weights, pos) -> np.ndarray:
+    """kernels/moe_routing.py:52-76, 100-113: out[t] = sum_k weights[t, k] *
+    expert_out[pos[t, k]], accumulated over k in order (fp64 here)."""
+    x = np.asarray(expert_out, dtype=np.float64)
+    w = np.asarray(weights, dtype=np.float64)
+    pos = np.asarray(pos)
+    T, K = pos.shape
+    out = np.zeros((T, x.shape[1]), dtype=np.float64)
+    for s in range(K):
+        out += w[:, s:s + 1] * x[pos[:, s]]
+    return out
+
+
+def naive_route(flat, weights, experts_idx, expert_fn, n_experts) -> np.ndarray:
+    """train/model.py:178-187 (_naive_route): for each expert, the tokens routed to
+    it, expert_fn(e, rows) scaled by their router weight, index-added into the output.
+    No sort, no inverse permutation: an independent formulation of the routed MoE
+    forward that moe_dispatch_combine (kernels/moe_routing.py:133-153) must equal."""
+    x = np.asarray(flat, dtype=np.float64)
+    w = np.asarray(weights, dtype=np.float64)
+    out = np.zeros_like(x)
+    for e in range(n_experts):
+        tok, slot = np.nonzero(np.asarray(experts_idx) == e)
+        if tok.size:
+            np.add.at(out, tok, np.asarray(expert_fn(e, x[tok]), dtype=np.float64) * w[tok, slot, None])
     return out
 
 

@@ -24,7 +24,7 @@ def declared_symbols() -> list[str]:
 
 def test_header_declares_the_boundary():
     syms = declared_symbols()
-    assert len(syms) == len(set(syms)) == 12
+    assert len(syms) == len(set(syms)) == 14
     assert set(syms) == set(kernels.SIGNATURES)
 
 
@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = kernels.load_library()
-    assert lib.mls_abi_version() == kernels.ABI_VERSION == 1
+    assert lib.mls_abi_version() == kernels.ABI_VERSION == 2
     assert isinstance(lib.mls_last_error(), bytes)
 
 
@@ -105,3 +105,25 @@ def test_grouped_rejects():
     # fp32 activations are outside the grouped kernel
     assert L.mls_int4_grouped_gemm(1, kernels.MLS_F32, 64, 1, 2, 8, 1, 0, 32, 1, 0, 0, 2, 1, 32,
                                    1, kernels.MLS_F32, 16, 16, 64, NULL) == kernels.MLS_ERR_UNSUPPORTED
+
+
+def test_gate_up_and_combine_reject():
+    L = kernels.load_library()
+    bf = kernels.MLS_BF16
+    # null up matrix
+    assert L.mls_int4_grouped_gate_up(1, bf, 64, 1, 2, 8, 1, NULL, 0, 32, 1, 1, 0, 2, 1, 1, 32,
+                                      1, bf, 16, 16, 64, NULL) == kernels.MLS_ERR_ARG
+    # fp32 activations
+    assert L.mls_int4_grouped_gate_up(1, kernels.MLS_F32, 64, 1, 2, 8, 1, 1, 0, 32, 1, 1, 0, 2, 1, 1,
+                                      32, 1, kernels.MLS_F32, 16, 16, 64, NULL) == kernels.MLS_ERR_UNSUPPORTED
+    # output dtype differs from the activations
+    assert L.mls_int4_grouped_gate_up(1, bf, 64, 1, 2, 8, 1, 1, 0, 32, 1, 1, 0, 2, 1, 1, 32,
+                                      1, kernels.MLS_F16, 16, 16, 64, NULL) == kernels.MLS_ERR_ARG
+    # empty problems are no-ops
+    assert L.mls_int4_grouped_gate_up(NULL, bf, 64, NULL, 2, 0, NULL, NULL, 0, 32, NULL, NULL, 0, 2, 1, 1,
+                                      32, NULL, bf, 16, 16, 64, NULL) == 0
+    # combine: k < 1, ldo < D, null pos, empty
+    assert L.mls_moe_combine(1, bf, 8, 4, 1, bf, 1, 2, 0, 1, 8, 8, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_moe_combine(1, bf, 8, 4, 1, bf, 1, 2, 2, 1, 4, 8, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_moe_combine(1, bf, 8, 4, 1, bf, NULL, 2, 2, 1, 8, 8, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_moe_combine(NULL, bf, 8, 0, NULL, bf, NULL, 0, 2, NULL, 8, 8, NULL) == 0

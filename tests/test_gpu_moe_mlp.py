@@ -1,0 +1,247 @@
+"""The quantized MoE expert MLP on the GPU: the fused gate/up launch, the two-launch
+INT4 SwiGLU expert MLP, the atomic-free combine, and the drop-in
+moe_dispatch_combine (kernels/moe_routing.py:133-153) against the oracle and the
+reference's own routing tests (tests/test_moe_routing.py of the reference).
+
+Tolerances: 16-bit outputs |out - ref| <= 1e-2 + 1e-2 |ref| (ref.close_bf16); the
+fused gate/up rounds silu(gate) * up once, where the per-expert module path rounds
+gate, up, silu and the product separately, so the two agree to bf16 precision, not
+bitwise. fp32 combine: rtol = atol = 1e-5 (the reference test's bound)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from oracle import ref
+
+from kernels.moe_grouped import int4_expert_mlp, int4_grouped_gate_up
+from kernels.moe_routing import combine_rows, moe_dispatch_combine, sort_by_expert
+from serve.quantize import QuantLinear, quantize_int4, quantize_model, stacked_int4_experts
+
+pytestmark = pytest.mark.gpu
+
+
+class SwiGLU(nn.Module):
+    """train/model.py:127-135."""
+
+    def __init__(self, d, h):
+        super().__init__()
+        self.w_gate = nn.Linear(d, h, bias=False)
+        self.w_up = nn.Linear(d, h, bias=False)
+        self.w_down = nn.Linear(h, d, bias=False)
+
+    def forward(self, x):
+        return self.w_down(F.silu(self.w_gate(x)) * self.w_up(x))
+
+
+def _int4(dev, E, N, K, gs, seed, sdt):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    P, S = [], []
+    for _ in range(E):
+        p, s = quantize_int4(torch.randn(N, K, generator=g, device=dev) * 0.05, gs)
+        P.append(p)
+        S.append(s.to(sdt))
+    return torch.stack(P), torch.stack(S)
+
+
+def _check16(out, want, what):
+    ok, err = ref.close_bf16(out.float().cpu().numpy(), want)
+    assert ok, f"{what}: max excess over tolerance {err}"
+
+
+@pytest.mark.parametrize("counts,H,K,gs,adt,sdt", [
+    ([5, 0, 130, 1], 192, 256, 128, torch.bfloat16, torch.float16),
+    ([300, 1, 1, 1, 0, 77, 2, 40], 200, 512, 32, torch.float16, torch.float32),
+    ([0, 0, 0, 64], 64, 128, 64, torch.bfloat16, torch.float32),
+    ([17, 250], 384, 1024, 256, torch.bfloat16, torch.float16),
+])
+def test_gate_up_vs_oracle(dev, counts, H, K, gs, adt, sdt):
+    E = len(counts)
+    print(f"gate_up counts={counts} H={H} K={K} gs={gs} {adt} {sdt}", flush=True)
+    WG, SG = _int4(dev, E, H, K, gs, 11 + H, sdt)
+    WU, SU = _int4(dev, E, H, K, gs, 12 + H, sdt)
+    M = sum(counts)
+    a = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).to(adt)
+    h = int4_grouped_gate_up(a.to(dev), WG, SG, WU, SU, torch.tensor(counts, device=dev), gs)
+    assert h.dtype == adt and h.shape == (M, H)
+    off = np.concatenate([[0], np.cumsum(counts)])
+    want = ref.grouped_int4_gate_up(a.float().numpy(), WG.cpu().numpy(), SG.float().cpu().numpy(),
+                                    WU.cpu().numpy(), SU.float().cpu().numpy(), off, gs)
+    _check16(h, want, f"gate/up {counts}")
+
+
+@pytest.mark.parametrize("adt", [torch.bfloat16, torch.float16])
+def test_expert_mlp_vs_oracle(dev, adt):
+    counts = [40, 0, 3, 129, 64, 1, 0, 19]
+    E, D, H, gs = len(counts), 256, 512, 64
+    WG, SG = _int4(dev, E, H, D, gs, 1, torch.float16)
+    WU, SU = _int4(dev, E, H, D, gs, 2, torch.float16)
+    WD, SD = _int4(dev, E, D, H, gs, 3, torch.float16)
+    M = sum(counts)
+    a = torch.randn(M, D, generator=torch.Generator().manual_seed(5)).to(adt)
+    y = int4_expert_mlp(a.to(dev), torch.tensor(counts, device=dev), WG, SG, WU, SU, WD, SD, gs)
+    off = np.concatenate([[0], np.cumsum(counts)])
+    want = ref.grouped_int4_swiglu(a.float().numpy(), WG.cpu().numpy(), SG.float().cpu().numpy(),
+                                   WU.cpu().numpy(), SU.float().cpu().numpy(), WD.cpu().numpy(),
+                                   SD.float().cpu().numpy(), off, gs)
+    _check16(y, want, f"expert MLP {adt}")
+
+
+@pytest.mark.parametrize("D", [24, 64, 1000])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
+def test_combine_rows(dev, D, dt):
+    """test_moe_routing.py:21-28 of the reference, on the GPU, three dtypes, vector and
+    scalar paths."""
+    T, K = 40, 2
+    g = torch.Generator().manual_seed(D)
+    x = torch.randn(T * K, D, generator=g).to(dt)
+    w = torch.rand(T, K, generator=g)
+    pos = torch.randperm(T * K, generator=g).reshape(T, K)
+    for wt in (w, w.to(dt)):
+        out = combine_rows(x.to(dev), wt.to(dev), pos.to(dev))
+        assert out.dtype == dt
+        want = ref.combine_rows(x.float().numpy(), wt.float().numpy(), pos.numpy())
+        if dt == torch.float32:
+            np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-5, atol=1e-5)
+        else:
+            _check16(out, want, f"combine {dt} D={D}")
+
+
+def test_combine_rows_edges(dev):
+    x = torch.randn(8, 32, device=dev)
+    empty = combine_rows(x, torch.zeros(0, 2, device=dev), torch.zeros(0, 2, dtype=torch.int64, device=dev))
+    assert empty.shape == (0, 32)
+    # one-hot weights gather exactly; zero weights give exact zeros
+    pos = torch.tensor([[3, 5], [7, 0]], device=dev)
+    oh = torch.tensor([[0.0, 1.0], [1.0, 0.0]], device=dev)
+    assert torch.equal(combine_rows(x, oh, pos), x[[5, 7]])
+    assert combine_rows(x, torch.zeros(2, 2, device=dev), pos).abs().max().item() == 0.0
+
+
+def _experts(dev, E, D, H, seed):
+    torch.manual_seed(seed)
+    return nn.ModuleList([SwiGLU(D, H) for _ in range(E)]).to(dev)
+
+
+def _route(dev, T, E, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    idx = torch.randint(0, E, (T, k), generator=g)
+    if k == 2:
+        idx[:, 1] = (idx[:, 0] + 1 + torch.randint(0, E - 1, (T,), generator=g)) % E
+    w = torch.rand(T, k, generator=g)
+    return (w / w.sum(-1, keepdim=True)).to(dev), idx.to(dev)
+
+
+def _naive(flat, weights, idx, experts):
+    """train/model.py:178-187."""
+    out = torch.zeros_like(flat)
+    for e in range(len(experts)):
+        tok, slot = torch.where(idx == e)
+        if tok.numel():
+            out.index_add_(0, tok, experts[e](flat[tok]) * weights[tok, slot, None])
+    return out
+
+
+@pytest.mark.parametrize("T,E,k,D", [(64, 4, 2, 32), (37, 8, 1, 16), (128, 8, 2, 64), (16, 2, 2, 24)])
+def test_dispatch_combine_matches_naive(dev, T, E, k, D):
+    """test_moe_routing.py:31-61 of the reference: full-precision experts (per-expert
+    loop), HIP combine."""
+    experts = _experts(dev, E, D, 2 * D, T)
+    flat = torch.randn(T, D, device=dev)
+    w, idx = _route(dev, T, E, k, T + E)
+    with torch.no_grad():
+        out = moe_dispatch_combine(flat, w, idx, experts)
+        want = _naive(flat, w, idx, experts)
+    torch.testing.assert_close(out, want, rtol=1e-4, atol=1e-4)
+
+
+def _quantize_experts(experts, gs):
+    for m in experts:
+        for name in ("w_gate", "w_up", "w_down"):
+            setattr(m, name, QuantLinear(getattr(m, name), bits=4, group_size=gs))
+    return experts
+
+
+@pytest.mark.parametrize("T,E,k,D,H,gs,dt", [
+    (300, 8, 2, 256, 512, 32, torch.bfloat16),
+    (77, 4, 1, 128, 256, 128, torch.float16),
+    (1, 8, 2, 256, 192, 64, torch.bfloat16),
+])
+def test_int4_moe_fused_path(dev, T, E, k, D, H, gs, dt):
+    """INT4 experts: the grouped two-launch path equals the per-expert QuantLinear
+    path (the reference's loop) and the oracle's naive routing."""
+    print(f"fused MoE T={T} E={E} k={k} D={D} H={H} gs={gs} {dt}", flush=True)
+    experts = _quantize_experts(_experts(dev, E, D, H, 7), gs)
+    st = stacked_int4_experts(experts)
+    assert st is not None
+    for e, m in enumerate(experts):     # the modules' buffers are views of the stack
+        assert m.w_gate.w_q.data_ptr() == st["w_gate"][0][e].data_ptr()
+    flat = torch.randn(T, D, device=dev).to(dt)
+    w, idx = _route(dev, T, E, k, 3)
+    with torch.no_grad():
+        out = moe_dispatch_combine(flat, w.to(dt), idx, experts)
+        loop = _naive(flat, w.to(dt), idx, experts)
+    assert out.dtype == dt
+    _check16(out, loop.float().cpu().numpy(), "fused vs per-expert QuantLinear")
+    dq = [[getattr(m, n).dequant().cpu().numpy().astype(np.float64) for n in ("w_gate", "w_up", "w_down")]
+          for m in experts]
+
+    def fn(e, rows):
+        g_, u_, d_ = dq[e]
+        return (ref.silu(rows @ g_.T) * (rows @ u_.T)) @ d_.T
+
+    want = ref.naive_route(flat.float().cpu().numpy(), w.to(dt).float().cpu().numpy(), idx.cpu().numpy(), fn, E)
+    _check16(out, want, "fused vs oracle")
+
+
+def test_int4_moe_degenerate_routing(dev):
+    """test_moe_routing.py:64-82 of the reference on the fused path: every token to
+    expert 0 (the others get empty segments); zero weights give zeros."""
+    E, D, H, T = 4, 128, 256, 20
+    experts = _quantize_experts(_experts(dev, E, D, H, 9), 32)
+    flat = torch.randn(T, D, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        out = moe_dispatch_combine(flat, torch.ones(T, 1, device=dev, dtype=torch.bfloat16),
+                                   torch.zeros(T, 1, dtype=torch.long, device=dev), experts)
+        _check16(out, experts[0](flat).float().cpu().numpy(), "all tokens to expert 0")
+        z = moe_dispatch_combine(flat, torch.zeros(T, 2, device=dev, dtype=torch.bfloat16),
+                                 torch.randint(0, E, (T, 2), device=dev), experts)
+    assert z.abs().max().item() == 0.0
+
+
+def test_int4_moe_restacks_after_move(dev):
+    """Experts quantized on the host, then moved: the first call stacks their buffers
+    on the device; a replaced buffer triggers a rebuild, not stale weights."""
+    E, D, H, T = 4, 128, 256, 50
+    torch.manual_seed(4)
+    experts = _quantize_experts(nn.ModuleList([SwiGLU(D, H) for _ in range(E)]), 32)
+    assert stacked_int4_experts(experts) is None          # host buffers: not the kernel path
+    experts = experts.to(dev)
+    flat = torch.randn(T, D, device=dev).to(torch.bfloat16)
+    w, idx = _route(dev, T, E, 2, 8)
+    w = w.to(torch.bfloat16)
+    with torch.no_grad():
+        a = moe_dispatch_combine(flat, w, idx, experts)
+        _check16(a, _naive(flat, w, idx, experts).float().cpu().numpy(), "after move")
+        old = stacked_int4_experts(experts)["w_down"][0]
+        # a new expert-2 down projection, assigned as a fresh tensor (not in place)
+        q, s = quantize_int4(torch.randn(D, H, device=dev) * 0.05, 32)
+        experts[2].w_down.w_q = q
+        experts[2].w_down.scale = s
+        b = moe_dispatch_combine(flat, w, idx, experts)
+        assert stacked_int4_experts(experts)["w_down"][0].data_ptr() != old.data_ptr()
+        _check16(b, _naive(flat, w, idx, experts).float().cpu().numpy(), "after buffer swap")
+
+
+def test_quantize_model_stacks_moe_experts(dev):
+    from test_host import _Model  # toy model with the reference's slot names
+    m = _Model().to(dev)
+    q = quantize_model(m, bits=4, group_size=32)
+    experts = q.blocks[1].mlp.experts
+    st = experts[0].__dict__.get("_int4_stack")
+    assert st is not None and st["w_up"][0].shape == (2, 128, 32)
+    assert quantize_model(m, bits=8).blocks[1].mlp.experts[0].__dict__.get("_int4_stack") is None

@@ -15,7 +15,8 @@ from oracle import ref
 
 from kernels.dequant_matmul import int4_matmul, int8_dgrad, int8_matmul
 from kernels.fp8_matmul import E4M3_MAX, decode_e4m3, dequantize_e4m3, fp8_matmul, quantize_e4m3
-from kernels.moe_grouped import int4_grouped_matmul
+from kernels.moe_grouped import int4_grouped_gate_up, int4_grouped_matmul
+from kernels.moe_routing import combine_rows, moe_dispatch_combine
 from serve.quantize import (QuantLinear, dequantize_int4, dequantize_int8, model_weight_bytes,
                             quantize_int4, quantize_int8, quantize_model)
 
@@ -37,6 +38,14 @@ def test_kernel_entry_points_refuse_host_tensors():
         fp8_matmul(bits, bits, 0.01, 0.01)
     with pytest.raises(TypeError, match="HIP device"):
         int4_grouped_matmul(a.bfloat16(), w4[None], s4[None], torch.tensor([2]), 32)
+    with pytest.raises(TypeError, match="HIP device"):
+        int4_grouped_gate_up(a.bfloat16(), w4[None], s4[None], w4[None], s4[None], torch.tensor([2]), 32)
+    with pytest.raises(TypeError, match="HIP device"):
+        combine_rows(torch.randn(4, 8), torch.rand(2, 2), torch.arange(4).reshape(2, 2))
+    # the routed MoE forward has no host path either: its combine is the HIP kernel
+    experts = [nn.Linear(64, 64, bias=False) for _ in range(2)]
+    with pytest.raises(TypeError, match="HIP device"):
+        moe_dispatch_combine(a, torch.ones(2, 1), torch.zeros(2, 1, dtype=torch.long), experts)
 
 
 def test_int4_matmul_keeps_reference_assert():
@@ -138,6 +147,16 @@ def test_quantize_model_swaps_every_block_linear():
     assert isinstance(m.blocks[0].attn.wq, nn.Linear)          # original untouched
     fp = model_weight_bytes(m)
     assert model_weight_bytes(q8) < fp * 0.5 and model_weight_bytes(q4) < model_weight_bytes(q8)
+
+
+def test_moe_experts_on_host_are_not_stacked():
+    """The grouped INT4 expert path needs device buffers; host-quantized experts (the
+    reference CLI quantizes before moving to the GPU) are stacked later, on the device."""
+    from serve.quantize import stacked_int4_experts
+    q4 = quantize_model(_Model(), bits=4, use_kernel=True)
+    experts = q4.blocks[1].mlp.experts
+    assert stacked_int4_experts(experts) is None
+    assert experts[0].__dict__.get("_int4_stack") is None
 
 
 def test_fp8_linear_emulation_on_host():

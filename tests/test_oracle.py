@@ -247,6 +247,86 @@ def test_grouped_matches_per_expert_loop():
     assert np.allclose(y[4:9], ref.int4_matmul(a[4:9], p[2], s[2], gs))
 
 
+def test_silu_closed_forms_and_torch():
+    x = np.linspace(-30, 30, 601)
+    y = ref.silu(x)
+    assert ref.silu(0.0) == 0.0
+    assert np.allclose(y - ref.silu(-x), x, rtol=0, atol=1e-12)       # silu(x) - silu(-x) = x
+    assert abs(ref.silu(40.0) - 40.0) < 1e-12 and abs(ref.silu(-40.0)) < 1e-12
+    t = torch.nn.functional.silu(torch.from_numpy(x)).numpy()
+    assert np.allclose(y, t, rtol=1e-12, atol=1e-15)
+
+
+def test_gate_up_matches_per_row_formula():
+    g = np.random.default_rng(7)
+    E, H, K, gs = 3, 32, 64, 32
+    wg = g.integers(0, 256, size=(E, H, K // 2), dtype=np.uint8)
+    wu = g.integers(0, 256, size=(E, H, K // 2), dtype=np.uint8)
+    sg = (g.random((E, H, K // gs)) * 0.05 + 0.01).astype(np.float32)
+    su = (g.random((E, H, K // gs)) * 0.05 + 0.01).astype(np.float32)
+    off = np.array([0, 3, 3, 8])
+    a = g.standard_normal((8, K)).astype(np.float32)
+    h = ref.grouped_int4_gate_up(a, wg, sg, wu, su, off, gs)
+    for r in range(8):
+        e = 0 if r < 3 else 2
+        gate = ref.int4_matmul(a[r:r + 1], wg[e], sg[e], gs)[0].astype(np.float64)
+        up = ref.int4_matmul(a[r:r + 1], wu[e], su[e], gs)[0].astype(np.float64)
+        want = np.array([gv / (1 + np.exp(-gv)) * uv for gv, uv in zip(gate, up)])
+        assert np.allclose(h[r], want, rtol=1e-5, atol=1e-5)
+    # the down projection of the full MLP is the grouped GEMM of h
+    D = 16
+    wd = g.integers(0, 256, size=(E, D, H // 2), dtype=np.uint8)
+    sd = (g.random((E, D, 1)) * 0.05).astype(np.float32)
+    y = ref.grouped_int4_swiglu(a, wg, sg, wu, su, wd, sd, off, gs)
+    assert np.allclose(y[3:], ref.int4_matmul(h[3:], wd[2], sd[2], gs), rtol=1e-5, atol=1e-5)
+
+
+def test_combine_rows_pins():
+    g = np.random.default_rng(8)
+    T, K, D = 40, 2, 24
+    x = g.standard_normal((T * K, D)).astype(np.float32)
+    w = g.random((T, K)).astype(np.float32)
+    pos = g.permutation(T * K).reshape(T, K)
+    out = ref.combine_rows(x, w, pos)
+    # the reference test's formula (test_moe_routing.py:21-28)
+    assert np.allclose(out, (x[pos] * w[..., None]).sum(axis=1), rtol=1e-6, atol=1e-6)
+    # brute force per element
+    for t in (0, 17, 39):
+        for d in (0, 23):
+            assert abs(out[t, d] - sum(float(w[t, s]) * float(x[pos[t, s], d]) for s in range(K))) < 1e-9
+    # one-hot weights: a gather; zero weights: zero; linear in the weights
+    oh = np.zeros_like(w)
+    oh[:, 1] = 1
+    assert np.array_equal(ref.combine_rows(x, oh, pos), x[pos[:, 1]].astype(np.float64))
+    assert not ref.combine_rows(x, np.zeros_like(w), pos).any()
+    assert np.allclose(ref.combine_rows(x, 2 * w + oh, pos), 2 * out + x[pos[:, 1]], atol=1e-9)
+
+
+def test_naive_route_equals_sorted_dispatch():
+    g = np.random.default_rng(9)
+    for T, E, k, D in [(64, 4, 2, 32), (37, 8, 1, 16), (16, 2, 2, 24)]:
+        mats = g.standard_normal((E, D, D))
+        fn = lambda e, rows: np.tanh(rows @ mats[e])  # noqa: E731
+        flat = g.standard_normal((T, D))
+        idx = g.integers(0, E, size=(T, k))
+        if k == 2:
+            idx[:, 1] = (idx[:, 0] + 1 + g.integers(0, E - 1, size=T)) % E
+        w = g.random((T, k))
+        w /= w.sum(-1, keepdims=True)
+        tok, counts, pos = ref.sort_by_expert(idx, E)
+        disp = flat[tok]
+        eo = np.zeros_like(disp)
+        off = np.concatenate([[0], np.cumsum(counts)])
+        for e in range(E):
+            eo[off[e]:off[e + 1]] = fn(e, disp[off[e]:off[e + 1]])
+        assert np.allclose(ref.combine_rows(eo, w, pos), ref.naive_route(flat, w, idx, fn, E), atol=1e-12)
+    # reference degenerate cases: every token to expert 0; zero weights
+    flat = g.standard_normal((20, D))
+    one = ref.naive_route(flat, np.ones((20, 1)), np.zeros((20, 1), np.int64), fn, 2)
+    assert np.allclose(one, fn(0, flat))
+    assert not ref.naive_route(flat, np.zeros((20, 2)), g.integers(0, 2, size=(20, 2)), fn, 2).any()
+
+
 def test_routing_matches_golden():
     d = golden("route_small")
     w, ex = ref.route_topk(d["logits"], 2)
@@ -292,3 +372,17 @@ def test_planted_mistakes_fail_the_pins():
     away = np.where(ref._POS_VALUES[hi] - a_ <= a_ - ref._POS_VALUES[lo], hi, lo)
     finite = np.isfinite(x)
     assert not np.array_equal(away[finite].astype(np.uint8), e["q_boundary"][finite] & 0x7F)
+    # gate and up swapped in the SwiGLU product
+    g = np.random.default_rng(10)
+    wg = g.integers(0, 256, size=(1, 8, 32), dtype=np.uint8)
+    wu = g.integers(0, 256, size=(1, 8, 32), dtype=np.uint8)
+    sc = np.full((1, 8, 2), 0.05, np.float32)
+    a = g.standard_normal((4, 64)).astype(np.float32)
+    off = np.array([0, 4])
+    h = ref.grouped_int4_gate_up(a, wg, sc, wu, sc, off, 32)
+    assert not ref.close_fp32(ref.grouped_int4_gate_up(a, wu, sc, wg, sc, off, 32), h)[0]
+    # combine reading pos transposed ([k, T] order)
+    x = g.standard_normal((12, 4))
+    w = g.random((6, 2))
+    pos = g.permutation(12).reshape(6, 2)
+    assert not np.allclose(ref.combine_rows(x, w, pos.T.reshape(6, 2)), (x[pos] * w[..., None]).sum(1))
