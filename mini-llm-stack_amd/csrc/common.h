@@ -21,6 +21,11 @@ inline bool is_float_dt(int dt) { return dt == MLS_F32 || dt == MLS_F16 || dt ==
 inline int dt_size(int dt) { return dt == MLS_F32 ? 4 : 2; }
 inline bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+// integer value of a tuning environment variable (sweeps), dflt when unset or empty
+inline int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
 
 // ----------------------------------------------------------------- device side
 

@@ -25,6 +25,8 @@
 // extending SDWA convert per byte gives the exact float, and the 1/16 is folded into
 // the group scale (a power of two: exact). Group scales apply to fp32 partial sums at
 // every group boundary, as in the dense INT4 kernels.
+#include <type_traits>
+
 #include "mfma16.h"
 
 namespace mls {
@@ -51,25 +53,42 @@ __device__ __forceinline__ void widen_int4x16(const uint4& q, uint32_t* o) {
 }  // namespace
 
 // STAB: the block's whole [128 x G] fp16 group-scale table is loaded once, coalesced,
-// into LDS (G <= 32, contiguous groups). Otherwise each stage loads the scales of its
-// 128 rows; those loads touch one cache line per row, many more L2 requests than the
-// weights themselves, and their latency then dominates the stage.
+// into LDS (G <= 128, contiguous groups: at most 32 KiB). Otherwise each stage loads the
+// scales of its 128 rows; those loads touch one cache line per row, many more L2
+// requests than the weights themselves. They are issued before the stage's LDS-direct
+// activation loads, so the end-of-stage wait, which must cover the LDS-direct loads,
+// leaves only the weight load in flight behind them.
 // GU (gate/up of a SwiGLU expert MLP): the block's 128 weight rows are 64 rows of the
 // gate matrix (p.b, p.s) and the same 64 rows of the up matrix (p.b2, p.s2); the
 // epilogue writes h = silu(gate) * up for those 64 columns, from the fp32 accumulators.
-template <typename MT, typename OT, int TMX, bool STAB, bool GU>
+template <int R>
+struct Ring {
+  static constexpr int v = R;
+};
+
+// SCL: 32 or 128 = fp16 scale table of up to that many groups (STAB); 0 / 1 = fp32 /
+// fp16 scales loaded per stage (the dtype fixed at compile time, so the loaded values
+// are not consumed, and waited for, until they are stored two stages later).
+template <typename MT, typename OT, int TMX, int SCL, bool GU>
 __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params p) {
+  constexpr bool STAB = SCL >= 32;
+  constexpr int TABG = STAB ? SCL : 0;
   constexpr int BN = 128, BK = 64, NT = 256;
   constexpr int OUTN = GU ? 64 : 128;  // output columns per block
   constexpr int BMX = 32 * TMX, TN = 4;
   constexpr int PW = BMX * 8 / NT;  // activation LDS-direct loads per thread and stage
   static_assert(BMX * 8 % NT == 0, "activation slots");
 
-  extern __shared__ __align__(16) uint8_t smem[];
-  uint4* As = reinterpret_cast<uint4*>(smem);             // [2][BMX][8]
-  uint4* Bs = As + 2 * BMX * 8;                            // [2][BN][8]
-  float* sS = reinterpret_cast<float*>(Bs + 2 * BN * 8);  // [2][2][BN] (per-stage scales)
-  _Float16* sT = reinterpret_cast<_Float16*>(Bs + 2 * BN * 8);  // [G][BN] (STAB)
+  // Double-buffered activation and widened-weight tiles in separate arrays: the
+  // compiler then knows that a pending LDS-direct load into one buffer cannot touch
+  // the other (or the scale table), and inserts no wait for it before their reads.
+  // 72 KiB at TMX = 5; with a scale table of up to 32 groups (8 KiB) two blocks share
+  // a CU.
+  __shared__ __align__(16) uint4 As0[BMX * 8], As1[BMX * 8];
+  __shared__ __align__(16) uint4 Bs0[BN * 8], Bs1[BN * 8];
+  __shared__ __align__(16) uint8_t sTab[STAB ? TABG * BN * 2 : 2 * 2 * BN * 4];
+  _Float16* const sT = reinterpret_cast<_Float16*>(sTab);  // [G][BN] fp16 (STAB)
+  float* const sS = reinterpret_cast<float*>(sTab);        // [2][2][BN] per-stage scales
 
   // ---- which (expert, row chunk, column tile). The grid is sized by a bound on the
   // row chunks; the blocks past the real item count exit, and the real items are
@@ -93,7 +112,7 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   const int m0 = __builtin_amdgcn_readfirstlane(lo + (chunk - cum) * BMX);
   const int rows = __builtin_amdgcn_readfirstlane(min(BMX, hi - m0));
   const int nsub = (rows + 15) >> 4;  // active 16-row subtiles
-  const int ssz = p.s_dt == MLS_F16 ? 2 : 4;
+  constexpr int ssz = SCL == 0 ? 4 : 2;
   const uint8_t* bmat = p.b + (int64_t)e * p.b_estride;
   const uint8_t* smat = (const uint8_t*)p.s + (int64_t)e * p.s_estride * ssz;
   const int n0 = nt * OUTN, N = p.N;
@@ -128,33 +147,63 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   const uint8_t* s_mat = (GU && s_r >= 64) ? smat_hi : smat;
   const int64_t s_row = (int64_t)min(n0 + (GU ? (s_r & 63) : s_r), N - 1) * p.ld_sn;
 
-  // weights of the stage to store next (rb, rs0, rs1) and of the one after (nb, ns0, ns1)
-  uint4 rb, nb;
-  float rs0 = 0.f, rs1 = 0.f, ns0 = 0.f, ns1 = 0.f;
-  auto dma_a = [&](int buf, int k0) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < PW; ++i) lds_load16(rsa, As + buf * BMX * 8 + (wave * PW + i) * 64, a_off[i], k0 * 2);
+  auto abuf = [&](auto r) __attribute__((always_inline)) -> uint4* {
+    if constexpr (decltype(r)::v == 0) return As0;
+    else return As1;
   };
-  // the weight chunk first, then (per-stage scales) the scale loads; threads past BN
-  // re-read a scale they never store
-  auto load_b = [&](int k0, uint4& w, float& s0, float& s1) __attribute__((always_inline)) {
-    w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsb, b_off, k0 / 2, 0));
+  auto bbuf = [&](auto r) __attribute__((always_inline)) -> uint4* {
+    if constexpr (decltype(r)::v == 0) return Bs0;
+    else return Bs1;
+  };
+
+  // weight chunks (and per-stage scales) in a register ring of three: slot kt % 3 holds
+  // stage kt's chunk until it is stored (stage kt - 1), then receives stage kt + 3's.
+  // The slots are named variables selected at compile time, so no register copies
+  // (each of which would wait for its load) sit between a load and its use.
+  uint4 w0, w1, w2;
+  float s00 = 0.f, s01 = 0.f, s10 = 0.f, s11 = 0.f, s20 = 0.f, s21 = 0.f;
+  auto wreg = [&](auto q) __attribute__((always_inline)) -> uint4& {
+    if constexpr (decltype(q)::v == 0) return w0;
+    else if constexpr (decltype(q)::v == 1) return w1;
+    else return w2;
+  };
+  auto sreg0 = [&](auto q) __attribute__((always_inline)) -> float& {
+    if constexpr (decltype(q)::v == 0) return s00;
+    else if constexpr (decltype(q)::v == 1) return s10;
+    else return s20;
+  };
+  auto sreg1 = [&](auto q) __attribute__((always_inline)) -> float& {
+    if constexpr (decltype(q)::v == 0) return s01;
+    else if constexpr (decltype(q)::v == 1) return s11;
+    else return s21;
+  };
+  auto dma_a = [&](uint4* dst, int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < PW; ++i) lds_load16(rsa, dst + (wave * PW + i) * 64, a_off[i], k0 * 2);
+  };
+  // per-stage scales (!STAB); threads past BN re-read a scale they never store
+  auto load_s = [&](int k0, float& s0, float& s1) __attribute__((always_inline)) {
     if constexpr (!STAB) {
       const int kc = min(k0, p.K - BK);  // a stage past the end reuses the last scales
-      s0 = scale_at(s_mat, p.s_dt, s_row + (int64_t)(kc / p.group) * p.ld_sg) * 0.0625f;
-      s1 = scale_at(s_mat, p.s_dt, s_row + (int64_t)((kc + 32) / p.group) * p.ld_sg) * 0.0625f;
+      using ST = std::conditional_t<SCL == 1, _Float16, float>;
+      const ST* sp = reinterpret_cast<const ST*>(s_mat) + s_row;
+      s0 = (float)sp[(int64_t)(kc / p.group) * p.ld_sg] * 0.0625f;
+      s1 = (float)sp[(int64_t)((kc + 32) / p.group) * p.ld_sg] * 0.0625f;
     }
   };
-  auto store_b = [&](int buf) __attribute__((always_inline)) {
-    uint4* bs = Bs + buf * BN * 8;
+  auto load_w = [&](int k0, uint4& w) __attribute__((always_inline)) {
+    w = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsb, b_off, k0 / 2, 0));
+  };
+  auto store_b = [&](auto r, const uint4& w, float t0, float t1) __attribute__((always_inline)) {
+    uint4* bs = bbuf(r);
     uint32_t o[16];
-    widen_int4x16<MT>(rb, o);
+    widen_int4x16<MT>(w, o);
 #pragma unroll
     for (int h = 0; h < 4; ++h)
       bs[b_row * 8 + ((4 * b_cc + h) ^ swz(b_row))] = make_uint4(o[4 * h + 0], o[4 * h + 1], o[4 * h + 2], o[4 * h + 3]);
     if (!STAB && tid < BN) {
-      sS[(buf * 2 + 0) * BN + tid] = rs0;
-      sS[(buf * 2 + 1) * BN + tid] = rs1;
+      sS[(decltype(r)::v * 2 + 0) * BN + tid] = t0;
+      sS[(decltype(r)::v * 2 + 1) * BN + tid] = t1;
     }
   };
 
@@ -182,25 +231,28 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
       for (int t = 0; t < 8; ++t) sT[(part * 8 + t) * BN + r] = h[t];
     }
   }
-  // prologue: stage 0 into buffer 0; stages 1 and 2 in registers
-  dma_a(0, 0);
-  load_b(0, rb, rs0, rs1);
-  __builtin_amdgcn_s_waitcnt(0);
-  store_b(0);
-  load_b(BK, rb, rs0, rs1);
-  load_b(2 * BK, nb, ns0, ns1);
-  __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  __builtin_amdgcn_sched_barrier(0);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
+
+  // Stage kt on LDS buffer r = kt % 2 and register slot q = kt % 3. At its start (the
+  // buffers r ^ 1 were last read in stage kt - 1, before the barrier that ended it):
+  // stage kt + 3's scales into slot q, stage kt + 1's activations into A buffer r ^ 1,
+  // stage kt + 3's weight chunk into slot q; then stage kt + 1's widened weights (slot
+  // q + 1, loaded in stage kt - 2) into B buffer r ^ 1; multiply buffer r; wait for
+  // stage kt + 1's activations: exactly one load (the weight chunk) was issued after
+  // them and vector loads complete in order, so vmcnt(1) covers them while the weight
+  // chunk stays in flight.
+  auto stage = [&](auto rc, auto qc, int kt) __attribute__((always_inline)) {
+    constexpr int r = decltype(rc)::v, q = decltype(qc)::v;
     const int k0 = kt * BK;
-    store_b(buf ^ 1);  // stage kt + 1 (past the end: harmless)
-    const uint4* as = As + buf * BMX * 8;
-    const uint4* bs = Bs + buf * BN * 8;
-    // one 32-k half at a time (operand registers for one half only); the next stage's
-    // LDS-direct loads go out after the last operand read of this stage, so the wait
-    // the compiler keeps before LDS reads behind them falls on the barrier
+    __builtin_amdgcn_sched_barrier(0);
+    load_s(k0 + 3 * BK, sreg0(qc), sreg1(qc));
+    __builtin_amdgcn_sched_barrier(0);
+    dma_a(abuf(Ring<r ^ 1>{}), k0 + BK);  // past the end: zeros / unused
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(k0 + 3 * BK, wreg(qc));
+    __builtin_amdgcn_sched_barrier(0);
+    store_b(Ring<r ^ 1>{}, wreg(Ring<(q + 1) % 3>{}), sreg0(Ring<(q + 1) % 3>{}), sreg1(Ring<(q + 1) % 3>{}));
+    const uint4* as = abuf(rc);
+    const uint4* bs = bbuf(rc);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       uint4 aop[TMX], bop[TN];
@@ -223,30 +275,17 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
           const uint2 h2 = *reinterpret_cast<const uint2*>(sT + g * BN + wn * 64 + i * 16 + 4 * lk);
           const _Float16* h = reinterpret_cast<const _Float16*>(&h2);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sc[i][r] = (float)h[r] * 0.0625f;
+          for (int q = 0; q < 4; ++q) sc[i][q] = (float)h[q] * 0.0625f;
         }
       } else {
 #pragma unroll
         for (int i = 0; i < TN; ++i) {
-          const float4 s4 = *reinterpret_cast<const float4*>(sS + (buf * 2 + ks) * BN + wn * 64 + i * 16 + 4 * lk);
+          const float4 s4 = *reinterpret_cast<const float4*>(sS + (r * 2 + ks) * BN + wn * 64 + i * 16 + 4 * lk);
           sc[i][0] = s4.x;
           sc[i][1] = s4.y;
           sc[i][2] = s4.z;
           sc[i][3] = s4.w;
         }
-      }
-      if (ks == 1) {
-        __builtin_amdgcn_sched_barrier(0);
-        dma_a(buf ^ 1, k0 + BK);  // stage kt + 1 (past the end: zeros / harmless)
-        // the weight loads must issue after the LDS-direct loads: the vmcnt(1) before
-        // the barrier counts on the LDS-direct loads being the older ones
-        __builtin_amdgcn_sched_barrier(0);
-        // stage kt + 2's weights move up (loaded during stage kt - 1), stage kt + 3's go out
-        rb = nb;
-        rs0 = ns0;
-        rs1 = ns1;
-        load_b(k0 + 3 * BK, nb, ns0, ns1);
-        __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int j = 0; j < TMX; ++j) {
@@ -260,33 +299,67 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
 #pragma unroll
           for (int j = 0; j < TMX; ++j) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[i][j][r] = fmaf(sc[i][r], accg[i][j][r], acc[i][j][r]);
+            for (int q = 0; q < 4; ++q) acc[i][j][q] = fmaf(sc[i][q], accg[i][j][q], acc[i][j][q]);
             accg[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
           }
       }
     }
-    // every wavefront's LDS-direct loads of stage kt + 1 and LDS stores land before the
-    // barrier. At least one load (the weight chunk) is issued after the LDS-direct loads
-    // and loads complete in order, so vmcnt(1) covers them whatever number of scale
-    // loads follows; the last weight load stays in flight
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // prologue: stage 0 into buffers 0; stages 1 and 2's weights into slots 1 and 2
+  dma_a(As0, 0);
+  load_w(0, w0);
+  load_s(0, s00, s01);
+  __builtin_amdgcn_s_waitcnt(0);
+  store_b(Ring<0>{}, w0, s00, s01);
+  load_w(BK, w1);
+  load_s(BK, s10, s11);
+  load_w(2 * BK, w2);
+  load_s(2 * BK, s20, s21);
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  // six stages per trip (LDS buffer kt % 2, register slot kt % 3), leaving after any
+  if (nk > 0) {
+    for (int kt = 0;; kt += 6) {
+      stage(Ring<0>{}, Ring<0>{}, kt);
+      if (kt + 1 >= nk) break;
+      stage(Ring<1>{}, Ring<1>{}, kt + 1);
+      if (kt + 2 >= nk) break;
+      stage(Ring<0>{}, Ring<2>{}, kt + 2);
+      if (kt + 3 >= nk) break;
+      stage(Ring<1>{}, Ring<0>{}, kt + 3);
+      if (kt + 4 >= nk) break;
+      stage(Ring<0>{}, Ring<1>{}, kt + 4);
+      if (kt + 5 >= nk) break;
+      stage(Ring<1>{}, Ring<2>{}, kt + 5);
+      if (kt + 6 >= nk) break;
+    }
   }
+  // loads past the end may still be in flight: drain them before the LDS is reused
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue: acc[i][j][r] = C[m = m0 + (2 j + wm) 16 + lr][n = n0 + 64 wn + 16 i + 4 lk + r]
   OT* c = static_cast<OT*>(p.c);
   if constexpr (GU) {
     // wavefronts wn = 1 hold the up products: they pass them through LDS (the
-    // activation buffers, free after the loop's last barrier) to the wavefronts wn = 0,
-    // which hold the gate products of the same (m, n) and write silu(gate) * up
-    float* U = reinterpret_cast<float*>(smem);  // [BMX][64]
+    // activation buffers, free now) to the wavefronts wn = 0, which hold the gate
+    // products of the same (m, n) and write silu(gate) * up. Subtile q = 2 j + wm
+    // (16 rows x 64 columns fp32, 4 KiB) goes to buffer q % 2 at 4 KiB (q / 2): the
+    // TMX subtiles of one parity fill one TMX x 4 KiB buffer exactly.
+    auto ubuf = [&](int q) __attribute__((always_inline)) -> float* {
+      uint4* b = (q & 1) ? As1 : As0;
+      return reinterpret_cast<float*>(b) + (q >> 1) * 1024;
+    };
     if (wn == 1) {
 #pragma unroll
       for (int i = 0; i < TN; ++i)
 #pragma unroll
         for (int j = 0; j < TMX; ++j)
-          *reinterpret_cast<f32x4*>(U + ((2 * j + wm) * 16 + lr) * 64 + i * 16 + 4 * lk) = acc[i][j];
+          *reinterpret_cast<f32x4*>(ubuf(2 * j + wm) + lr * 64 + i * 16 + 4 * lk) = acc[i][j];
     }
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -299,7 +372,7 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
       for (int j = 0; j < TMX; ++j) {
         const int ml = (2 * j + wm) * 16 + lr;
         if (ml >= rows) continue;
-        const f32x4 u = *reinterpret_cast<const f32x4*>(U + ml * 64 + i * 16 + 4 * lk);
+        const f32x4 u = *reinterpret_cast<const f32x4*>(ubuf(2 * j + wm) + lr * 64 + i * 16 + 4 * lk);
         float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -337,35 +410,29 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   }
 }
 
-template <typename MT, int TMX, bool STAB, bool GU>
+template <typename MT, int TMX, int SCL, bool GU>
 static int launch_grouped(Mfma16Params p, hipStream_t st) {
-  constexpr int BMX = 32 * TMX, BN = 128, OUTN = GU ? 64 : 128;
+  constexpr int BMX = 32 * TMX, OUTN = GU ? 64 : 128;
   p.n_tiles = (int)cdiv(p.N, OUTN);
   // upper bound on sum_e ceil(rows_e / BMX) without reading the device offsets
   p.m_tiles = (int)(cdiv(p.M, BMX) + p.E);
-  const size_t tab = STAB ? (size_t)BN * 32 * 2 : (size_t)2 * 2 * BN * 4;
-  const size_t lds = (size_t)2 * (BMX + BN) * 8 * 16 + tab;
-  auto kern = grouped_int4_kernel<MT, MT, TMX, STAB, GU>;
-  static bool attr_set = false;
-  if (!attr_set) {
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)lds) != hipSuccess)
-      return fail(MLS_ERR_HIP, "grouped INT4 GEMM: cannot reserve %zu bytes of LDS", lds);
-    attr_set = true;
-  }
+  auto kern = grouped_int4_kernel<MT, MT, TMX, SCL, GU>;
   const int64_t blocks = (int64_t)p.n_tiles * p.m_tiles;
   if (blocks > 0x7FFFFFFF) return MLS_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, st, p);
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, st, p);
   return check_launch(GU ? "grouped INT4 gate/up GEMM" : "grouped INT4 GEMM");
 }
 
-template <bool STAB, bool GU>
+template <int SCL, bool GU>
 static int launch_grouped_tmx(const Mfma16Params& p, hipStream_t st, bool bf16, int tmx) {
   switch (tmx) {
-    case 5: return bf16 ? launch_grouped<__bf16, 5, STAB, GU>(p, st) : launch_grouped<_Float16, 5, STAB, GU>(p, st);
-    case 4: return bf16 ? launch_grouped<__bf16, 4, STAB, GU>(p, st) : launch_grouped<_Float16, 4, STAB, GU>(p, st);
-    case 3: return bf16 ? launch_grouped<__bf16, 3, STAB, GU>(p, st) : launch_grouped<_Float16, 3, STAB, GU>(p, st);
-    default: return bf16 ? launch_grouped<__bf16, 2, STAB, GU>(p, st) : launch_grouped<_Float16, 2, STAB, GU>(p, st);
+    case 5:
+      if constexpr (SCL >= 32)
+        return bf16 ? launch_grouped<__bf16, 5, SCL, GU>(p, st) : launch_grouped<_Float16, 5, SCL, GU>(p, st);
+      [[fallthrough]];  // per-stage scales: 160-row chunks are not built (they would spill)
+    case 4: return bf16 ? launch_grouped<__bf16, 4, SCL, GU>(p, st) : launch_grouped<_Float16, 4, SCL, GU>(p, st);
+    case 3: return bf16 ? launch_grouped<__bf16, 3, SCL, GU>(p, st) : launch_grouped<_Float16, 3, SCL, GU>(p, st);
+    default: return bf16 ? launch_grouped<__bf16, 2, SCL, GU>(p, st) : launch_grouped<_Float16, 2, SCL, GU>(p, st);
   }
 }
 
@@ -374,15 +441,21 @@ static int launch_grouped_tmx(const Mfma16Params& p, hipStream_t st, bool bf16, 
 // rows fit in one chunk and its weights are streamed and widened once.
 int launch_grouped_seg(const Mfma16Params& p, hipStream_t st, bool bf16, bool gate_up) {
   const int64_t want = cdiv(p.M * 5, p.E * 4);
-  const int tmx = want > 128 ? 5 : want > 96 ? 4 : want > 64 ? 3 : 2;
-  // scale table in LDS: fp16 scales, contiguous groups, G a multiple of 8 up to 32,
-  // 16-byte aligned rows
+  // MLS_GROUPED_TMX (2..5) overrides the chunk height (32 TMX rows) for sweeps
+  static const int tmx_env = env_int("MLS_GROUPED_TMX", 0);
+  int tmx = tmx_env >= 2 && tmx_env <= 5 ? tmx_env : want > 128 ? 5 : want > 96 ? 4 : want > 64 ? 3 : 2;
+  // scale table in LDS: fp16 scales, contiguous groups, G a multiple of 8 up to 128,
+  // 16-byte aligned rows; a table of up to 32 groups keeps two blocks per CU
   const int64_t G = p.K / p.group;
-  const bool stab = p.s_dt == MLS_F16 && p.ld_sg == 1 && G % 8 == 0 && G <= 32 && (p.ld_sn % 8) == 0 &&
+  const bool stab = p.s_dt == MLS_F16 && p.ld_sg == 1 && G % 8 == 0 && G <= 128 && (p.ld_sn % 8) == 0 &&
                     (p.s_estride % 8) == 0 && aligned(p.s, 16) && (!gate_up || aligned(p.s2, 16));
-  if (gate_up)
-    return stab ? launch_grouped_tmx<true, true>(p, st, bf16, tmx) : launch_grouped_tmx<false, true>(p, st, bf16, tmx);
-  return stab ? launch_grouped_tmx<true, false>(p, st, bf16, tmx) : launch_grouped_tmx<false, false>(p, st, bf16, tmx);
+  if (!stab && p.s_dt == MLS_F16)
+    return gate_up ? launch_grouped_tmx<1, true>(p, st, bf16, tmx) : launch_grouped_tmx<1, false>(p, st, bf16, tmx);
+  if (!stab)
+    return gate_up ? launch_grouped_tmx<0, true>(p, st, bf16, tmx) : launch_grouped_tmx<0, false>(p, st, bf16, tmx);
+  if (G <= 32)
+    return gate_up ? launch_grouped_tmx<32, true>(p, st, bf16, tmx) : launch_grouped_tmx<32, false>(p, st, bf16, tmx);
+  return gate_up ? launch_grouped_tmx<128, true>(p, st, bf16, tmx) : launch_grouped_tmx<128, false>(p, st, bf16, tmx);
 }
 
 }  // namespace mls

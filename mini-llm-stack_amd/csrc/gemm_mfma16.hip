@@ -618,10 +618,6 @@ static int pick_bm(int64_t M, int64_t N, int max_bm) {
 // forced row-tile height (16 .. 256), MLS_MFMA_ADMA = 0 stages 16-bit activations
 // through registers instead of loading them straight into LDS, MLS_MFMA_BN = 256 or 192
 // forces the column-tile width of the 256-row weight-only kernel.
-static int env_int(const char* name, int dflt) {
-  const char* v = getenv(name);
-  return v && *v ? atoi(v) : dflt;
-}
 
 template <int AKIND, int BKIND, typename MT, typename OT>
 static int dense16(Mfma16Params p, hipStream_t st) {
