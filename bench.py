@@ -12,8 +12,8 @@ HIP events; value = algorithmic bytes x K / elapsed.
 
 The other BASELINE configs (INT4 M = 4 / 16, the INT8 GEMV target, INT8 prefill,
 FP8 e4m3 GEMM, INT4 MoE grouped GEMM) and the whole INT4 SwiGLU expert MLP of a
-routed MoE layer (gate/up, down, combine) are reported under "extra" with the same
-protocol, followed by a 256 MiB streaming copy (the bandwidth a plain elementwise
+routed MoE layer (gate/up, down, combine) and the load-time INT4 quantizer are reported
+under "extra" with the same protocol, followed by a 256 MiB streaming copy (the bandwidth a plain elementwise
 kernel reaches on this GPU). cpu_baseline times the reference's CPU algorithm (the numpy
 restatement in oracle/: dequantize, then fp32 matmul) on the host for a bounded
 sample of the headline workload.
@@ -225,6 +225,21 @@ def moe_mlp_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=1
     return dict(ms=ms, bytes=nbytes, flops=6 * rows * H * D, copies=copies, counts=counts.tolist())
 
 
+def quantize_int4_load(dev, steps: int, warmup: int, N=14336, K=4096, gs=128):
+    """Load-time INT4 quantization of one fp32 weight matrix on the GPU
+    (serve/quantize.py:28-36 semantics, bit-exact): reads N*K fp32, writes the packed
+    nibbles and fp32 group scales."""
+    import torch
+    from serve.quantize import quantize_int4
+    g = torch.Generator(device=dev).manual_seed(6)
+    copies = 2
+    ws = [torch.randn(N, K, generator=g, device=dev) * 0.02 for _ in range(copies)]
+    fns = [lambda w=w: quantize_int4(w, gs) for w in ws]
+    ms = time_steps(fns, warmup, steps)
+    nbytes = N * K * 4 + N * K // 2 + N * (K // gs) * 4
+    return dict(ms=ms, bytes=nbytes, flops=0, copies=copies)
+
+
 def copy_calibration(dev, steps: int, warmup: int, nbytes: int = 256 << 20):
     """A plain streaming kernel of known traffic (torch's elementwise bitwise_not over
     int32: reads nbytes, writes nbytes). Its rocprofv3 FETCH_SIZE / WRITE_SIZE
@@ -318,7 +333,7 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--only", default=None,
                     help="run one workload: int4_gemv, int4_m4, int4_m16, int8_gemv, int8_prefill, "
-                         "fp8_gemm, fp8_native, moe_int4, moe_mlp_int4, copy (counter calibration)")
+                         "fp8_gemm, fp8_native, moe_int4, moe_mlp_int4, quantize_int4, copy (counter calibration)")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
@@ -361,6 +376,7 @@ def main(argv=None) -> int:
                                                       "launches": "gate/up + down + combine",
                                                       "segments": r["counts"]}))(
             moe_mlp_int4(dev, small, 4)),
+        "quantize_int4": lambda: _hbm_row("quantize_int4_14336x4096_g128", quantize_int4_load(dev, small, 4)),
         "copy": lambda: _hbm_row("copy_256MiB", copy_calibration(dev, small, 4)),
     }
     if args.only:
@@ -376,7 +392,7 @@ def main(argv=None) -> int:
     extra = []
     if not args.no_extra:
         for k in ("int4_m4", "int4_m16", "int8_gemv", "int8_prefill", "fp8_gemm", "fp8_native",
-                  "moe_int4", "moe_mlp_int4", "copy"):
+                  "moe_int4", "moe_mlp_int4", "quantize_int4", "copy"):
             log(f"{k} ...")
             row = runners[k]()
             log(json.dumps(row))

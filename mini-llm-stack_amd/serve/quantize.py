@@ -113,6 +113,24 @@ class QuantLinear(nn.Module):
         self.register_buffer("w_q", w_q)
         self.register_buffer("scale", scale)
 
+    @classmethod
+    def from_quantized(cls, w_q: torch.Tensor, scale: torch.Tensor, bits: int, group_size: int,
+                       in_features: int, use_kernel: bool = True) -> "QuantLinear":
+        """A QuantLinear around buffers that are already quantized (a quantized
+        checkpoint): no fp weight, no quantization pass."""
+        assert bits in (4, 8)
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self.bits, self.group_size, self.use_kernel = bits, group_size, use_kernel
+        self.out_features, self.in_features = w_q.shape[0], in_features
+        want = in_features if bits == 8 else in_features // 2
+        if w_q.dim() != 2 or w_q.shape[1] != want:
+            raise ValueError(f"QuantLinear.from_quantized: w_q {tuple(w_q.shape)} does not hold "
+                             f"{in_features} int{bits} columns")
+        self.register_buffer("w_q", w_q)
+        self.register_buffer("scale", scale)
+        return self
+
     def dequant(self) -> torch.Tensor:
         if self.bits == 8:
             return dequantize_int8(self.w_q, self.scale)
@@ -241,3 +259,94 @@ def model_weight_bytes(model: nn.Module) -> int:
         seen.add(id(p))
         total += p.numel() * p.element_size()
     return total
+
+
+# ------------------------------------------------------------------ quantized checkpoints
+#
+# The reference saves the fp state dict and quantizes again at every load
+# (serve/api.py:47, 79-81). A quantized checkpoint stores the QuantLinear buffers
+# themselves (w_q, scale: serve/quantize.py:68-73) next to the model's fp parameters,
+# in a safetensors file (plain tensors + a string header; loading executes nothing),
+# so a load is a copy to the device and quantization runs once, on the GPU.
+#
+# Header ("__metadata__"): format = "mls-quantized", version = "1", and per quantized
+# module "q:<module name>" = "<bits>,<group_size>,<in_features>". Tensors: the model's
+# state dict (the QuantLinear buffers under their state-dict names, every other
+# parameter and buffer as stored), each saved as its own contiguous copy.
+
+QCKPT_FORMAT, QCKPT_VERSION = "mls-quantized", "1"
+
+
+def save_quantized(model: nn.Module, path, extra_metadata: dict | None = None) -> None:
+    """Write a model whose linears are QuantLinear (quantize_model's output) to a
+    quantized safetensors checkpoint at `path`."""
+    from safetensors.torch import save_file
+    meta = {"format": QCKPT_FORMAT, "version": QCKPT_VERSION}
+    for name, m in model.named_modules():
+        if isinstance(m, QuantLinear):
+            meta[f"q:{name}"] = f"{m.bits},{m.group_size},{m.in_features}"
+    if len(meta) == 2:
+        raise ValueError("save_quantized: the model holds no QuantLinear (run quantize_model first)")
+    for k, v in (extra_metadata or {}).items():
+        if k in meta or k.startswith("q:"):
+            raise ValueError(f"save_quantized: metadata key {k!r} is reserved")
+        meta[k] = str(v)
+    tensors = {k: v.detach().contiguous().clone() for k, v in model.state_dict().items()}
+    save_file(tensors, str(path), metadata=meta)
+
+
+def read_quantized_metadata(path) -> dict:
+    """The string header of a quantized checkpoint (format, version, modules, extras)."""
+    from safetensors import safe_open
+    with safe_open(str(path), framework="pt") as f:
+        meta = dict(f.metadata() or {})
+    if meta.get("format") != QCKPT_FORMAT:
+        raise ValueError(f"{path}: not a quantized checkpoint (format {meta.get('format')!r})")
+    if meta.get("version") != QCKPT_VERSION:
+        raise ValueError(f"{path}: quantized checkpoint version {meta.get('version')!r}, "
+                         f"this build reads {QCKPT_VERSION!r}")
+    return meta
+
+
+def _set_submodule(model: nn.Module, name: str, mod: nn.Module) -> None:
+    parent, _, leaf = name.rpartition(".")
+    setattr(model.get_submodule(parent) if parent else model, leaf, mod)
+
+
+def load_quantized(model: nn.Module, path, device=None, use_kernel: bool = True) -> nn.Module:
+    """Load a quantized checkpoint into `model` (the fp architecture, e.g. a freshly
+    built Transformer; it is modified in place and returned): every module the header
+    lists becomes a QuantLinear holding the stored buffers, then the remaining
+    parameters load as a state dict (strict: missing or unexpected keys raise). With
+    `device`, tensors are read straight onto it. MoE experts are stacked for the
+    grouped kernels as quantize_model does."""
+    from safetensors.torch import load_file
+    meta = read_quantized_metadata(path)
+    dev = torch.device(device) if device is not None else None
+    tensors = load_file(str(path), device=str(dev) if dev is not None else "cpu")
+    for key, spec in meta.items():
+        if not key.startswith("q:"):
+            continue
+        name = key[2:]
+        bits, group, in_features = (int(x) for x in spec.split(","))
+        old = model.get_submodule(name)
+        if not isinstance(old, (nn.Linear, QuantLinear)):
+            raise ValueError(f"load_quantized: {name} is a {type(old).__name__}, not a linear layer")
+        w_q, scale = tensors.pop(f"{name}.w_q"), tensors.pop(f"{name}.scale")
+        out_features = old.out_features
+        if w_q.shape[0] != out_features or in_features != old.in_features:
+            raise ValueError(f"load_quantized: {name} stores {w_q.shape[0]}x{in_features}, "
+                             f"the model has {out_features}x{old.in_features}")
+        _set_submodule(model, name, QuantLinear.from_quantized(w_q, scale, bits, group, in_features, use_kernel))
+    if dev is not None:
+        model.to(dev)
+    missing, unexpected = model.load_state_dict(tensors, strict=False)
+    quant_keys = {k for k in model.state_dict() if k.endswith((".w_q", ".scale"))
+                  and isinstance(model.get_submodule(k.rsplit(".", 1)[0]), QuantLinear)}
+    missing = [k for k in missing if k not in quant_keys]
+    if missing or unexpected:
+        raise ValueError(f"load_quantized: missing {missing[:5]}, unexpected {unexpected[:5]}")
+    for blk in getattr(model, "blocks", []):
+        if getattr(blk, "is_moe", False):
+            stacked_int4_experts(blk.mlp.experts)
+    return model

@@ -106,3 +106,37 @@ def test_quantize_int4_large(dev):
     p, s = quantize_int4(w.to(dev), 128)
     rp, rs = ref.quantize_int4(w.numpy(), 128)
     assert np.array_equal(p.cpu().numpy(), rp) and np.array_equal(_bits(s.cpu().numpy()), _bits(rs))
+
+
+@pytest.mark.parametrize("N,K,gs,stride", [
+    (64, 768, 256, 0),      # vector path, last 512-k span partial
+    (33, 1024, 512, 0),     # one group per span
+    (17, 96, 8, 0),         # one lane per group
+    (40, 960, 96, 0),       # group not a power of two: generic path
+    (12, 60, 6, 0),         # tiny odd-ish group: generic path
+    (50, 512, 32, 3),       # rows not 16-byte aligned: generic path
+])
+def test_quantize_int4_paths(dev, N, K, gs, stride):
+    """Both INT4 quantizer paths (one wavefront per 512-k span with shuffle-reduced
+    group maxima; one thread per group) against the oracle, bit-exact, including
+    all-zero groups and exact .5 ties."""
+    g = torch.Generator().manual_seed(N * K + gs)
+    full = torch.randn(N, K + stride, generator=g) * 0.05
+    full[3, :gs] = 0.0                                       # an all-zero group
+    full[5, :gs] = torch.arange(gs, dtype=torch.float32) * 0.5 - gs / 4   # ties at .5
+    w = full[:, :K]
+    p, s = quantize_int4(w.to(dev) if stride == 0 else full.to(dev)[:, :K], gs)
+    rp, rs = ref.quantize_int4(w.contiguous().numpy(), gs)
+    assert np.array_equal(p.cpu().numpy(), rp)
+    assert np.array_equal(_bits(s.cpu().numpy()), _bits(rs))
+
+
+@pytest.mark.parametrize("N,K,stride", [(70, 4100, 0), (9, 4098, 0), (31, 1000, 2)])
+def test_quantize_int8_paths(dev, N, K, stride):
+    g = torch.Generator().manual_seed(N + K)
+    full = torch.randn(N, K + stride, generator=g) * 0.05
+    full[2] = 0.0
+    w = full[:, :K]
+    q, s = quantize_int8(w.to(dev) if stride == 0 else full.to(dev)[:, :K])
+    rq, rs = ref.quantize_int8(w.contiguous().numpy())
+    assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(_bits(s.cpu().numpy()), _bits(rs))

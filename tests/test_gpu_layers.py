@@ -103,3 +103,29 @@ def test_greedy_decode_tokens_identical(dev):
                 a, b = run(True, toks), run(False, toks)
                 assert torch.equal(a, b), f"bits={bits} M={M}"
                 toks = a
+
+
+def test_quantized_checkpoint_on_device(dev, tmp_path):
+    """Quantize on the GPU, save, load straight onto the GPU: identical buffers and
+    identical kernel outputs; a host-quantized checkpoint loads to the same bytes (the
+    GPU quantizers are bit-exact); MoE experts come back stacked for the grouped path."""
+    from serve.quantize import load_quantized, save_quantized, stacked_int4_experts
+    from test_host import _Model
+    torch.manual_seed(5)
+    m = _Model()
+    qd = quantize_model(m.to(dev), bits=4, group_size=32, use_kernel=True)
+    path = tmp_path / "q4.safetensors"
+    save_quantized(qd, path)
+    loaded = load_quantized(_Model(), path, device=dev)
+    for k, v in qd.state_dict().items():
+        w = loaded.state_dict()[k]
+        assert w.device.type == "cuda" and torch.equal(v, w), k
+    x = torch.randn(5, 64, device=dev).to(torch.bfloat16)
+    assert torch.equal(loaded.blocks[0].attn.wo(x), qd.blocks[0].attn.wo(x))
+    assert stacked_int4_experts(loaded.blocks[1].mlp.experts) is not None
+    # a checkpoint written from a host-quantized model holds the same bytes
+    hpath = tmp_path / "q4_host.safetensors"
+    save_quantized(quantize_model(m.cpu(), bits=4, group_size=32, use_kernel=False), hpath)
+    hl = load_quantized(_Model(), hpath, device=dev)
+    for k, v in loaded.state_dict().items():
+        assert torch.equal(v, hl.state_dict()[k]), k

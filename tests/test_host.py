@@ -174,3 +174,59 @@ def test_fp8_linear_emulation_on_host():
     want = ref.dequantize_e4m3(xb, sx) @ ref.dequantize_e4m3(wb, sw).T
     assert np.allclose(y.detach().numpy(), want, rtol=1e-5, atol=1e-6)
     assert E4M3_MAX == 448.0
+
+
+# ------------------------------------------------------------------ quantized checkpoints
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_quantized_checkpoint_roundtrip_host(tmp_path, bits):
+    """save_quantized / load_quantized: the loaded model holds bit-identical QuantLinear
+    buffers and fp parameters, without running the quantizer again."""
+    from serve.quantize import load_quantized, read_quantized_metadata, save_quantized
+    torch.manual_seed(1)
+    m = _Model()
+    q = quantize_model(m, bits=bits, group_size=32, use_kernel=False)
+    path = tmp_path / "q.safetensors"
+    save_quantized(q, path, extra_metadata={"vocab": "abc"})
+    meta = read_quantized_metadata(path)
+    assert meta["vocab"] == "abc" and sum(k.startswith("q:") for k in meta) == 4 + 3 + 4 + 3 * 2
+    assert meta["q:blocks.0.attn.wq"] == f"{bits},32,64"
+    torch.manual_seed(2)                     # a different random init: everything must load
+    loaded = load_quantized(_Model(), path, use_kernel=False)
+    sq, sl = q.state_dict(), loaded.state_dict()
+    assert sq.keys() == sl.keys()
+    for k in sq:
+        assert sq[k].dtype == sl[k].dtype and torch.equal(sq[k], sl[k]), k
+    for a, b in zip(q.modules(), loaded.modules()):
+        assert type(a) is type(b)
+        if isinstance(a, QuantLinear):
+            assert (a.bits, a.group_size, a.in_features, a.out_features) == \
+                (b.bits, b.group_size, b.in_features, b.out_features)
+    assert model_weight_bytes(loaded) == model_weight_bytes(q)
+    x = torch.randn(3, 64)
+    assert torch.equal(loaded.blocks[0].attn.wq(x), q.blocks[0].attn.wq(x))
+    # the file holds the quantized weights, not fp copies
+    fp_bytes = sum(v.numel() * v.element_size() for v in m.state_dict().values())
+    assert path.stat().st_size < fp_bytes * (0.5 if bits == 8 else 0.3)
+
+
+def test_quantized_checkpoint_rejects(tmp_path):
+    from safetensors.torch import save_file
+    from serve.quantize import load_quantized, save_quantized
+    with pytest.raises(ValueError, match="no QuantLinear"):
+        save_quantized(_Model(), tmp_path / "fp.safetensors")
+    q = quantize_model(_Model(), bits=4, use_kernel=False)
+    path = tmp_path / "q.safetensors"
+    save_quantized(q, path)
+    with pytest.raises(ValueError, match="stores"):
+        load_quantized(_Model(d=64, h=192), path, use_kernel=False)     # hidden size differs
+    with pytest.raises(ValueError, match="reserved"):
+        save_quantized(q, path, extra_metadata={"format": "x"})
+    other = tmp_path / "other.safetensors"
+    save_file({"a": torch.zeros(2)}, str(other), metadata={"format": "mls-quantized", "version": "0"})
+    with pytest.raises(ValueError, match="version"):
+        load_quantized(_Model(), other)
+    save_file({"a": torch.zeros(2)}, str(other), metadata={"format": "something-else"})
+    with pytest.raises(ValueError, match="not a quantized checkpoint"):
+        load_quantized(_Model(), other)
