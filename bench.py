@@ -12,8 +12,9 @@ HIP events; value = algorithmic bytes x K / elapsed.
 
 The other BASELINE configs (INT4 M = 4 / 16, the INT8 GEMV target, INT8 prefill,
 FP8 e4m3 GEMM, INT4 MoE grouped GEMM) and the whole INT4 SwiGLU expert MLP of a
-routed MoE layer (gate/up, down, combine) and the load-time INT4 quantizer are reported
-under "extra" with the same protocol, followed by a 256 MiB streaming copy (the bandwidth a plain elementwise
+routed MoE layer (gate/up, down, combine), FP8Linear's backward at config D's shape
+(e5m2 gradients) and the load-time INT4 quantizer are reported under "extra" with the
+same protocol, followed by a 256 MiB streaming copy (the bandwidth a plain elementwise
 kernel reaches on this GPU). cpu_baseline times the reference's CPU algorithm (the numpy
 restatement in oracle/: dequantize, then fp32 matmul) on the host for a bounded
 sample of the headline workload.
@@ -162,6 +163,37 @@ def fp8_gemm(dev, steps: int, warmup: int, M=4096, N=8192, K=8192, native=False)
     ms = time_steps(fns, warmup, steps)
     nbytes = M * K + N * K + 4 * (M + N) + M * N * 2
     return dict(ms=ms, bytes=nbytes, flops=2 * M * N * K, copies=copies)
+
+
+def fp8_backward(dev, steps: int, warmup: int, M=4096, N=8192, K=8192, native=False):
+    """FP8Linear's backward at config D's shape (train/fp8.py:80-95): dy [M,N] to e5m2,
+    dx = dy W (dy times W^T [K,N]), dw = dy^T x (dy^T [N,M] times x^T [K,M]), with the
+    byte transposes; two 2*M*N*K GEMMs. The scale of dy is taken as given (the
+    reference reads it on the host before this work starts)."""
+    import torch
+    from kernels.fp8_matmul import E4M3_MAX, E5M2_MAX, fp8_matmul, quantize_e4m3, quantize_e5m2, transpose_u8
+    g = torch.Generator(device=dev).manual_seed(7)
+    copies = 2
+    sets = []
+    for _ in range(copies):
+        x = torch.randn(M, K, generator=g, device=dev)
+        w = torch.randn(N, K, generator=g, device=dev) * 0.02
+        dy = torch.randn(M, N, generator=g, device=dev) * 1e-3
+        sx, sw = float(x.abs().amax()) / E4M3_MAX, float(w.abs().amax()) / E4M3_MAX
+        sdy = float(dy.abs().amax()) / E5M2_MAX
+        sets.append((quantize_e4m3(x, sx), quantize_e4m3(w, sw), dy, sx, sw, sdy))
+
+    def step(xb, wb, dy, sx, sw, sdy):
+        dyb = quantize_e5m2(dy, sdy)
+        dx = fp8_matmul(dyb, transpose_u8(wb), sdy, sw, torch.float32, native=native, a_format="e5m2")
+        dw = fp8_matmul(transpose_u8(dyb), transpose_u8(xb), sdy, sx, torch.float32, native=native,
+                        a_format="e5m2")
+        return dx, dw
+
+    fns = [lambda st=st: step(*st) for st in sets]
+    ms = time_steps(fns, warmup, steps)
+    nbytes = M * N * 4 + 2 * (M * N + N * K + M * K) + (M * K + N * K) * 4
+    return dict(ms=ms, bytes=nbytes, flops=2 * 2 * M * N * K, copies=copies)
 
 
 def moe_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=128):
@@ -333,7 +365,8 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--only", default=None,
                     help="run one workload: int4_gemv, int4_m4, int4_m16, int8_gemv, int8_prefill, "
-                         "fp8_gemm, fp8_native, moe_int4, moe_mlp_int4, quantize_int4, copy (counter calibration)")
+                         "fp8_gemm, fp8_native, fp8_bwd, fp8_bwd_native, moe_int4, moe_mlp_int4, quantize_int4, "
+                         "copy (counter calibration)")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
@@ -363,6 +396,13 @@ def main(argv=None) -> int:
         "fp8_native": lambda: _mfma_row("fp8_e4m3_4096x8192x8192_native",
                                         fp8_gemm(dev, small, 4, native=True), FP8_PEAK_TFLOPS,
                                         {"datapath": "fp8 MFMA (8-product groups, 13-bit alignment)"}),
+        "fp8_bwd": lambda: _mfma_row("fp8_linear_backward_4096x8192x8192_exact", fp8_backward(dev, small, 4),
+                                     FP8_PEAK_TFLOPS, {"datapath": "e5m2/e4m3 widened to bf16, bf16 MFMA",
+                                                       "gemms": "dx = dy W, dw = dy^T x, + e5m2 encode, 3 transposes",
+                                                       "bf16_roofline_frac": None}),
+        "fp8_bwd_native": lambda: _mfma_row("fp8_linear_backward_4096x8192x8192_native",
+                                            fp8_backward(dev, small, 4, native=True), FP8_PEAK_TFLOPS,
+                                            {"datapath": "fp8 MFMA, bf8 x fp8 operands"}),
         "moe_int4": lambda: (lambda r: _mfma_row("moe_int4_grouped_1024x14336x4096", r,
                                                  BF16_PEAK_TFLOPS,
                                                  {"hbm_roofline_frac": round(
@@ -392,7 +432,7 @@ def main(argv=None) -> int:
     extra = []
     if not args.no_extra:
         for k in ("int4_m4", "int4_m16", "int8_gemv", "int8_prefill", "fp8_gemm", "fp8_native",
-                  "moe_int4", "moe_mlp_int4", "quantize_int4", "copy"):
+                  "fp8_bwd", "fp8_bwd_native", "moe_int4", "moe_mlp_int4", "quantize_int4", "copy"):
             log(f"{k} ...")
             row = runners[k]()
             log(json.dumps(row))

@@ -1,7 +1,10 @@
-// OCP FP8 E4M3 ("fn") codec kernels: decode (reference semantics: NaN -> 0),
+// FP8 codec kernels. OCP E4M3 ("fn"): decode (reference semantics: NaN -> 0),
 // dequantize (NaN stays NaN, times a scale) and the saturating encoder used by
 // quantize_e4m3. Written from the OCP OFP8 definition: 1 sign, 4 exponent bits
 // (bias 7), 3 mantissa bits, no infinities, S.1111.111 = NaN, max finite 448.
+// E5M2: the encoder of FP8 training's gradients (train/fp8.py:50-52), from the OCP
+// definition: 1 sign, 5 exponent bits (bias 15), 2 mantissa bits, infinities and NaNs
+// at exponent 31, max finite 57344.
 #include "common.h"
 
 namespace mls {
@@ -36,6 +39,28 @@ __device__ __forceinline__ uint32_t e4m3_encode(float q) {
   const uint32_t sign = (__float_as_uint(q) >> 24) & 0x80u;
   if (__builtin_isnan(q)) return 0x7Fu | sign;
   return e4m3_code_of_mag(fminf(fabsf(q), 448.0f)) | sign;
+}
+
+// e5m2 code of a finite magnitude 0 <= a <= 57344, round to nearest, ties to even.
+// e5m2: 1 sign, 5 exponent bits (bias 15), 2 mantissa bits; subnormals m/4 * 2^-14.
+__device__ __forceinline__ uint32_t e5m2_code_of_mag(float a) {
+  const uint32_t u = __float_as_uint(a);
+  if (u < 0x38800000u)  // a < 2^-14: the subnormal grid has step 2^-16; code 4 is 2^-14
+    return (uint32_t)__builtin_rintf(a * 65536.0f);
+  // a >= 2^-14: fp32 exponent field E >= 113. Keep the 2 top mantissa bits and rebias
+  // the exponent (127 -> 15); a carry out of the mantissa bumps the exponent.
+  uint32_t code = (u >> 21) - (112u << 2);
+  const uint32_t rem = u & 0x1FFFFFu;
+  if (rem > 0x100000u || (rem == 0x100000u && (code & 1u))) code += 1u;
+  return code;
+}
+
+// The reference's e5m2 quantization of q (already divided by the scale): clamp to
+// +-57344 (the largest finite e5m2), round; NaN -> 0x7F | sign.
+__device__ __forceinline__ uint32_t e5m2_encode(float q) {
+  const uint32_t sign = (__float_as_uint(q) >> 24) & 0x80u;
+  if (__builtin_isnan(q)) return 0x7Fu | sign;
+  return e5m2_code_of_mag(fminf(fabsf(q), 57344.0f)) | sign;
 }
 
 // vec: bits/out are 16-byte aligned, so the bulk is read 16 bytes per thread.
@@ -73,16 +98,17 @@ __global__ void e4m3_dequant_kernel(const uint8_t* __restrict__ bits, int64_t ro
   }
 }
 
-template <typename T>
-__global__ void e4m3_encode_kernel(const T* __restrict__ x, int64_t rows, int64_t cols, int64_t ldx,
-                                   float scale, const float* __restrict__ sp, int64_t sstride,
-                                   uint8_t* __restrict__ out, int64_t ldo) {
+template <typename T, bool E5M2>
+__global__ void fp8_encode_kernel(const T* __restrict__ x, int64_t rows, int64_t cols, int64_t ldx,
+                                  float scale, const float* __restrict__ sp, int64_t sstride,
+                                  uint8_t* __restrict__ out, int64_t ldo) {
   const int64_t total = rows * cols;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
     const int64_t r = i / cols, c = i - r * cols;
     const float s = sp ? sp[r * sstride] : scale;
-    out[r * ldo + c] = (uint8_t)e4m3_encode(to_f32(x[r * ldx + c]) / s);
+    const float q = to_f32(x[r * ldx + c]) / s;
+    out[r * ldo + c] = (uint8_t)(E5M2 ? e5m2_encode(q) : e4m3_encode(q));
   }
 }
 
@@ -123,26 +149,41 @@ extern "C" int mls_e4m3_dequantize(const uint8_t* bits, int64_t rows, int64_t co
   return check_launch("mls_e4m3_dequantize");
 }
 
-extern "C" int mls_e4m3_encode(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
-                               float scale, const float* scale_ptr, int64_t scale_stride,
-                               uint8_t* out, int64_t ldo, mls_stream_t stream) {
-  if (rows < 0 || cols < 0) return fail(MLS_ERR_ARG, "mls_e4m3_encode: negative size");
+template <bool E5M2>
+static int fp8_encode(const char* fn, const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
+                      float scale, const float* scale_ptr, int64_t scale_stride, uint8_t* out, int64_t ldo,
+                      mls_stream_t stream) {
+  if (rows < 0 || cols < 0) return fail(MLS_ERR_ARG, "%s: negative size", fn);
   if (rows == 0 || cols == 0) return MLS_OK;
-  if (!x || !out) return fail(MLS_ERR_ARG, "mls_e4m3_encode: null pointer");
-  if (!is_float_dt(x_dt)) return fail(MLS_ERR_ARG, "mls_e4m3_encode: bad x dtype %d", x_dt);
+  if (!x || !out) return fail(MLS_ERR_ARG, "%s: null pointer", fn);
+  if (!is_float_dt(x_dt)) return fail(MLS_ERR_ARG, "%s: bad x dtype %d", fn, x_dt);
   if (ldx < cols || ldo < cols || scale_stride < 0)
-    return fail(MLS_ERR_ARG, "mls_e4m3_encode: bad leading dimension or scale stride");
+    return fail(MLS_ERR_ARG, "%s: bad leading dimension or scale stride", fn);
   const int block = 256;
   const dim3 grid(grid_for(rows * cols, block));
   hipStream_t st = (hipStream_t)stream;
   if (x_dt == MLS_F32)
-    hipLaunchKernelGGL(e4m3_encode_kernel<float>, grid, dim3(block), 0, st, (const float*)x, rows,
+    hipLaunchKernelGGL((fp8_encode_kernel<float, E5M2>), grid, dim3(block), 0, st, (const float*)x, rows,
                        cols, ldx, scale, scale_ptr, scale_stride, out, ldo);
   else if (x_dt == MLS_F16)
-    hipLaunchKernelGGL(e4m3_encode_kernel<_Float16>, grid, dim3(block), 0, st, (const _Float16*)x,
+    hipLaunchKernelGGL((fp8_encode_kernel<_Float16, E5M2>), grid, dim3(block), 0, st, (const _Float16*)x,
                        rows, cols, ldx, scale, scale_ptr, scale_stride, out, ldo);
   else
-    hipLaunchKernelGGL(e4m3_encode_kernel<__bf16>, grid, dim3(block), 0, st, (const __bf16*)x, rows,
+    hipLaunchKernelGGL((fp8_encode_kernel<__bf16, E5M2>), grid, dim3(block), 0, st, (const __bf16*)x, rows,
                        cols, ldx, scale, scale_ptr, scale_stride, out, ldo);
-  return check_launch("mls_e4m3_encode");
+  return check_launch(fn);
+}
+
+extern "C" int mls_e4m3_encode(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
+                               float scale, const float* scale_ptr, int64_t scale_stride,
+                               uint8_t* out, int64_t ldo, mls_stream_t stream) {
+  return fp8_encode<false>("mls_e4m3_encode", x, x_dt, rows, cols, ldx, scale, scale_ptr, scale_stride, out,
+                           ldo, stream);
+}
+
+extern "C" int mls_e5m2_encode(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
+                               float scale, const float* scale_ptr, int64_t scale_stride,
+                               uint8_t* out, int64_t ldo, mls_stream_t stream) {
+  return fp8_encode<true>("mls_e5m2_encode", x, x_dt, rows, cols, ldx, scale, scale_ptr, scale_stride, out,
+                          ldo, stream);
 }

@@ -37,7 +37,18 @@ __device__ __forceinline__ float e4m3_ref_value(uint32_t b) {
   return (b & 0x80u) ? -mag : mag;
 }
 
-template <typename CT>
+// Exact value of an e5m2 byte (1 sign, 5 exponent bits with bias 15, 2 mantissa bits;
+// exponent 31 is inf (m = 0) or NaN), as torch's float8_e5m2 view reads it.
+__device__ __forceinline__ float e5m2_value(uint32_t b) {
+  const uint32_t e = (b >> 2) & 31u, m = b & 3u;
+  float mag;
+  if (e == 0) mag = (float)m * 0x1p-16f;                          // m/4 * 2^-14
+  else if (e == 31u) mag = m ? __uint_as_float(0x7FC00000u) : __uint_as_float(0x7F800000u);
+  else mag = __uint_as_float(((e + 112u) << 23) | (m << 21));     // (1 + m/4) * 2^(e-15)
+  return (b & 0x80u) ? -mag : mag;
+}
+
+template <typename CT, int FA>
 __global__ void fp8_gemm_generic_kernel(const uint8_t* __restrict__ a, int64_t lda,
                                         const uint8_t* __restrict__ b, int64_t ldb, float sa,
                                         const float* __restrict__ sap, int64_t sas, float sb,
@@ -50,17 +61,20 @@ __global__ void fp8_gemm_generic_kernel(const uint8_t* __restrict__ a, int64_t l
   const uint8_t* ar = a + m * lda;
   const uint8_t* br = b + n * ldb;
   float acc = 0.0f;
-  for (int64_t k = 0; k < K; ++k) acc = fmaf(e4m3_ref_value(ar[k]), e4m3_ref_value(br[k]), acc);
+  for (int64_t k = 0; k < K; ++k)
+    acc = fmaf(FA ? e5m2_value(ar[k]) : e4m3_ref_value(ar[k]), e4m3_ref_value(br[k]), acc);
   const float s = (sap ? sap[m * sas] : sa) * (sbp ? sbp[n * sbs] : sb);
   c[m * ldc + n] = from_f32<CT>(acc * s);
 }
 
-__device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, const f32x4& c) {
-  // format 0 / 0 = e4m3 for both operands; zero scales select the unscaled instruction
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+// bop: the B tile (e4m3, format 0) as the instruction's first operand; aop: the A tile,
+// format FA (0 = e4m3, 1 = e5m2); zero scales select the unscaled instruction
+template <int FA>
+__device__ __forceinline__ f32x4 mfma_fp8(const i32x8& bop, const i32x8& aop, const f32x4& c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bop, aop, c, 0, FA, 0, 0, 0, 0);
 }
 
-template <typename CT, int WM, int WN>
+template <typename CT, int WM, int WN, int FA>
 __global__ __launch_bounds__(64 * WM * WN) void fp8_gemm_mfma_kernel(
     const uint8_t* __restrict__ a, int64_t lda, const uint8_t* __restrict__ b, int64_t ldb,
     float sa, const float* __restrict__ sap, int64_t sas, float sb,
@@ -149,7 +163,7 @@ __global__ __launch_bounds__(64 * WM * WN) void fp8_gemm_mfma_kernel(
     for (int j = j_lo; j < j_hi; ++j) {
       const i32x8 aop = operand(as, wm0 + j * 16 + lr);
 #pragma unroll
-      for (int i = 0; i < TN; ++i) acc[i][j] = mfma_fp8(bop[i], aop, acc[i][j]);
+      for (int i = 0; i < TN; ++i) acc[i][j] = mfma_fp8<FA>(bop[i], aop, acc[i][j]);
     }
   };
 
@@ -209,7 +223,7 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds,
                                            soff, 0, 0);
 }
 
-template <typename CT, int WM, int WN>
+template <typename CT, int WM, int WN, int FA>
 __global__ __launch_bounds__(64 * WM * WN) void fp8_gemm_dma_kernel(
     const uint8_t* __restrict__ a, int64_t lda, const uint8_t* __restrict__ b, int64_t ldb,
     float sa, const float* __restrict__ sap, int64_t sas, float sb,
@@ -293,7 +307,7 @@ __global__ __launch_bounds__(64 * WM * WN) void fp8_gemm_dma_kernel(
 #pragma unroll
     for (int j = 0; j < TM; ++j)
 #pragma unroll
-      for (int i = 0; i < TN; ++i) acc[i][j] = mfma_fp8(bop[i], aop[j], acc[i][j]);
+      for (int i = 0; i < TN; ++i) acc[i][j] = mfma_fp8<FA>(bop[i], aop[j], acc[i][j]);
     __builtin_amdgcn_sched_barrier(0);  // the MFMAs stay ahead of the barrier's wait
     __syncthreads();
   }
@@ -324,19 +338,19 @@ __global__ __launch_bounds__(64 * WM * WN) void fp8_gemm_dma_kernel(
   }
 }
 
-template <typename CT>
+template <typename CT, int FA>
 static int launch_generic(const Fp8Args& f) {
-  hipLaunchKernelGGL(fp8_gemm_generic_kernel<CT>, dim3((unsigned)cdiv(f.M * f.N, 256)), dim3(256), 0,
+  hipLaunchKernelGGL((fp8_gemm_generic_kernel<CT, FA>), dim3((unsigned)cdiv(f.M * f.N, 256)), dim3(256), 0,
                      f.stream, f.a, f.lda, f.b, f.ldb, f.sa, f.sap, f.sas, f.sb, f.sbp, f.sbs,
                      (CT*)f.c, f.ldc, f.M, f.N, f.K);
   return check_launch("mls_fp8_gemm(generic)");
 }
 
-template <typename CT, int WM, int WN>
+template <typename CT, int WM, int WN, int FA>
 static int launch_native_w(const Fp8Args& f) {
   const int mt = (int)cdiv(f.M, 256), nt = (int)cdiv(f.N, 256);
   const size_t lds = 2 * 2 * 256 * 128;
-  auto kern = fp8_gemm_mfma_kernel<CT, WM, WN>;
+  auto kern = fp8_gemm_mfma_kernel<CT, WM, WN, FA>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -350,10 +364,10 @@ static int launch_native_w(const Fp8Args& f) {
   return check_launch("mls_fp8_gemm(native)");
 }
 
-template <typename CT, int WM, int WN>
+template <typename CT, int WM, int WN, int FA>
 static int launch_native_dma(const Fp8Args& f) {
   const int mt = (int)cdiv(f.M, 256), nt = (int)cdiv(f.N, 256);
-  hipLaunchKernelGGL((fp8_gemm_dma_kernel<CT, WM, WN>), dim3((unsigned)(mt * nt)), dim3(64 * WM * WN), 0,
+  hipLaunchKernelGGL((fp8_gemm_dma_kernel<CT, WM, WN, FA>), dim3((unsigned)(mt * nt)), dim3(64 * WM * WN), 0,
                      f.stream, f.a, f.lda, f.b, f.ldb, f.sa, f.sap, f.sas, f.sb, f.sbp, f.sbs, (CT*)f.c,
                      f.ldc, (int)f.M, (int)f.N, (int)f.K, mt, nt);
   return check_launch("mls_fp8_gemm(native)");
@@ -377,8 +391,9 @@ static int launch_native(const Fp8Args& f) {
     const char* e = getenv("MLS_FP8_DMA");
     return !(e && e[0] == '0');
   }();
-  if (dma) return w8 ? launch_native_dma<CT, 2, 4>(f) : launch_native_dma<CT, 2, 2>(f);
-  return w8 ? launch_native_w<CT, 2, 4>(f) : launch_native_w<CT, 2, 2>(f);
+  if (f.a_e5m2) return launch_native_dma<CT, 2, 4, 1>(f);  // the tuning variants are e4m3-only
+  if (dma) return w8 ? launch_native_dma<CT, 2, 4, 0>(f) : launch_native_dma<CT, 2, 2, 0>(f);
+  return w8 ? launch_native_w<CT, 2, 4, 0>(f) : launch_native_w<CT, 2, 2, 0>(f);
 }
 
 }  // namespace mls
@@ -393,13 +408,15 @@ extern "C" int mls_fp8_gemm(const uint8_t* a, int64_t lda, const uint8_t* b, int
     return fail(MLS_ERR_ARG, "mls_fp8_gemm: negative size M=%lld N=%lld K=%lld", (long long)M,
                 (long long)N, (long long)K);
   if (!is_float_dt(c_dt)) return fail(MLS_ERR_ARG, "mls_fp8_gemm: bad output dtype %d", c_dt);
-  if (flags & ~MLS_FP8_NATIVE) return fail(MLS_ERR_ARG, "mls_fp8_gemm: unknown flags 0x%x", flags);
+  if (flags & ~(MLS_FP8_NATIVE | MLS_FP8_A_E5M2))
+    return fail(MLS_ERR_ARG, "mls_fp8_gemm: unknown flags 0x%x", flags);
   if (M == 0 || N == 0) return MLS_OK;
   if (!a || !b || !c) return fail(MLS_ERR_ARG, "mls_fp8_gemm: null pointer");
   if (lda < K || ldb < K || ldc < N || sa_stride < 0 || sb_stride < 0)
     return fail(MLS_ERR_ARG, "mls_fp8_gemm: bad leading dimension or scale stride");
+  const bool a5 = (flags & MLS_FP8_A_E5M2) != 0;
   const Fp8Args f{a, lda, b, ldb, sa, sa_ptr, sa_stride, sb, sb_ptr, sb_stride, c, c_dt, ldc, M, N, K,
-                  (hipStream_t)stream};
+                  (hipStream_t)stream, a5};
   int rc = MLS_ERR_UNSUPPORTED;
   if (flags & MLS_FP8_NATIVE) {
     if (c_dt == MLS_F32) rc = launch_native<float>(f);
@@ -409,7 +426,12 @@ extern "C" int mls_fp8_gemm(const uint8_t* a, int64_t lda, const uint8_t* b, int
     rc = launch_fp8_exact(f);
   }
   if (rc != MLS_ERR_UNSUPPORTED) return rc;
-  if (c_dt == MLS_F32) return launch_generic<float>(f);
-  if (c_dt == MLS_F16) return launch_generic<_Float16>(f);
-  return launch_generic<__bf16>(f);
+  if (a5) {
+    if (c_dt == MLS_F32) return launch_generic<float, 1>(f);
+    if (c_dt == MLS_F16) return launch_generic<_Float16, 1>(f);
+    return launch_generic<__bf16, 1>(f);
+  }
+  if (c_dt == MLS_F32) return launch_generic<float, 0>(f);
+  if (c_dt == MLS_F16) return launch_generic<_Float16, 0>(f);
+  return launch_generic<__bf16, 0>(f);
 }

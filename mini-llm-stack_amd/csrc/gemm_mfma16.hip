@@ -136,7 +136,8 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_gemm_kernel(const Mfma16P
         as[row * 8 + (a_cc ^ swz(row))] = ra[i];
       } else {
         uint32_t o[8];
-        widen_e4m3(ra[i], o);
+        if constexpr (AKIND == A_E5M2) widen_e5m2(ra[i], o);
+        else widen_e4m3(ra[i], o);
         as[row * 8 + ((2 * a_cc + 0) ^ swz(row))] = make_uint4(o[0], o[1], o[2], o[3]);
         as[row * 8 + ((2 * a_cc + 1) ^ swz(row))] = make_uint4(o[4], o[5], o[6], o[7]);
       }
@@ -746,6 +747,11 @@ int launch_fp8_exact(const Fp8Args& f) {
   p.a = f.a; p.lda = f.lda; p.b = f.b; p.ldb = f.ldb;
   p.sa = f.sa; p.sap = f.sap; p.sas = f.sas; p.sb = f.sb; p.sbp = f.sbp; p.sbs = f.sbs;
   p.c = f.c; p.ldc = f.ldc; p.M = (int)f.M; p.N = (int)f.N; p.K = (int)f.K;
+  if (f.a_e5m2) {
+    if (f.c_dt == MLS_F32) return dense16<A_E5M2, B_E4M3, __bf16, float>(p, f.stream);
+    if (f.c_dt == MLS_F16) return dense16<A_E5M2, B_E4M3, __bf16, _Float16>(p, f.stream);
+    return dense16<A_E5M2, B_E4M3, __bf16, __bf16>(p, f.stream);
+  }
   if (f.c_dt == MLS_F32) return dense16<A_E4M3, B_E4M3, __bf16, float>(p, f.stream);
   if (f.c_dt == MLS_F16) return dense16<A_E4M3, B_E4M3, __bf16, _Float16>(p, f.stream);
   return dense16<A_E4M3, B_E4M3, __bf16, __bf16>(p, f.stream);

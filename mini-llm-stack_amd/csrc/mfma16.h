@@ -7,7 +7,7 @@
 
 namespace mls {
 
-enum { A_RAW16 = 0, A_E4M3 = 1 };
+enum { A_RAW16 = 0, A_E4M3 = 1, A_E5M2 = 2 };
 enum { B_INT8 = 0, B_INT4 = 1, B_E4M3 = 2 };
 
 struct Mfma16Params {
@@ -125,6 +125,17 @@ __device__ __forceinline__ void widen_e4m3(const uint4& q, uint32_t* o) {
   for (int t = 0; t < 4; ++t) {
     o[2 * t + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[t], 1.0f, false));
     o[2 * t + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(d[t], 1.0f, true));
+  }
+}
+
+// 16 e5m2 bytes -> 16 bf16; exact: e5m2 (5 exponent bits, 2 mantissa bits, subnormals
+// down to 2^-16, infinities) is a subset of bf16.
+__device__ __forceinline__ void widen_e5m2(const uint4& q, uint32_t* o) {
+  const uint32_t d[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    o[2 * t + 0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d[t], 1.0f, false));
+    o[2 * t + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(d[t], 1.0f, true));
   }
 }
 

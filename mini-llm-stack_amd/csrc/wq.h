@@ -67,9 +67,11 @@ struct Fp8Args {
   int64_t ldc;
   int64_t M, N, K;
   hipStream_t stream;
+  bool a_e5m2;  // A holds e5m2 bytes (B is always e4m3 here)
 };
 
-// Exact e4m3 GEMM: operands widened to bf16 on the way into LDS, bf16 MFMA.
+// Exact fp8 GEMM (A e4m3 or e5m2, B e4m3): operands widened to bf16 on the way into
+// LDS, bf16 MFMA.
 int launch_fp8_exact(const Fp8Args& f);
 
 }  // namespace mls

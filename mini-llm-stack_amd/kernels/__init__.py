@@ -18,13 +18,14 @@ from pathlib import Path
 # This implementation only ever runs compiled gfx950 code.
 INTERPRETER = False
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LIB_PATH = Path(os.environ.get("MLS_LIB") or
                 Path(__file__).resolve().parent.parent / "libmls_hip.so")
 
 MLS_F32, MLS_F16, MLS_BF16 = 0, 1, 2
 MLS_OK, MLS_ERR_ARG, MLS_ERR_UNSUPPORTED, MLS_ERR_HIP = 0, -1, -2, -3
 MLS_FP8_NATIVE = 1
+MLS_FP8_A_E5M2 = 2
 
 _LIB = None
 
@@ -37,6 +38,8 @@ SIGNATURES = {
     "mls_e4m3_decode": ([_P, _P, _I64, _P], _I),
     "mls_e4m3_dequantize": ([_P, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _P], _I),
     "mls_e4m3_encode": ([_P, _I, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _P], _I),
+    "mls_e5m2_encode": ([_P, _I, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _P], _I),
+    "mls_transpose_u8": ([_P, _I64, _I64, _I64, _P, _I64, _P], _I),
     "mls_quantize_int8": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P], _I),
     "mls_quantize_int4": ([_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P], _I),
     "mls_int8_gemm": ([_P, _I, _I64, _P, _I64, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P], _I),

@@ -16,6 +16,10 @@ product per group. Scales are applied in the epilogue and may be Python floats
 (per tensor, the reference's form), 0-d tensors, or fp32 tensors of shape [M] /
 [N] (per row).
 
+fp8_matmul(..., a_format="e5m2") takes an e5m2 A operand (FP8 training's gradients;
+e5m2 widens to bf16 exactly, and the native path selects the MFMA's bf8 format);
+quantize_e5m2 and transpose_u8 are the other pieces of that backward.
+
 quantize_e4m3 / dequantize_e4m3 run the gfx950 codec kernels on HIP tensors. On
 host tensors (the load-time and CPU-training callers) they run the reference's
 own host op sequence, which is the definition the HIP codec is bit-exact to.
@@ -31,6 +35,8 @@ import kernels
 from kernels._hip import dt_code, ld, require_hip, rows, stream
 
 E4M3_MAX = 448.0
+E5M2_MAX = 57344.0
+_FORMATS = {"e4m3": 0, "e5m2": kernels.MLS_FP8_A_E5M2}
 
 
 def decode_e4m3(bits: torch.Tensor) -> torch.Tensor:
@@ -94,6 +100,41 @@ def quantize_e4m3(x: torch.Tensor, scale) -> torch.Tensor:
     return out.reshape(shape)
 
 
+def quantize_e5m2(x: torch.Tensor, scale) -> torch.Tensor:
+    """e5m2 bits of x / scale, clamped to ±57344, round to nearest even: the
+    gradient quantizer of FP8 training (train/fp8.py:50-52). Returns uint8. scale: a
+    float, a 1-element tensor or [M, 1] per row of a 2-D x."""
+    if x.device.type != "cuda":
+        q = (x.float() / scale).clamp(-E5M2_MAX, E5M2_MAX)
+        return q.to(torch.float8_e5m2).view(torch.uint8)
+    dev = x.device
+    shape = x.shape
+    x2 = rows(x.reshape(1, 1) if x.dim() == 0 else x.reshape(-1, shape[-1]))
+    sa = _row_scale(scale, x2.shape[0], dev, "quantize_e5m2", False) \
+        if x.dim() <= 2 or not isinstance(scale, torch.Tensor) or scale.numel() == 1 else None
+    if sa is None:
+        raise ValueError("quantize_e5m2: scale must be a float, a 1-element tensor or [M, 1]")
+    out = torch.empty(x2.shape, dtype=torch.uint8, device=dev)
+    kernels.check(kernels.lib().mls_e5m2_encode(
+        x2.data_ptr(), dt_code(x.dtype, "quantize_e5m2"), x2.shape[0], x2.shape[1], ld(x2), sa[0], sa[1], sa[2],
+        out.data_ptr(), ld(out), stream(dev)), "quantize_e5m2")
+    return out.reshape(shape)
+
+
+def transpose_u8(t: torch.Tensor) -> torch.Tensor:
+    """A contiguous [cols, rows] copy of a 2-D byte tensor (fp8 bits): the .t() of
+    an fp8 operand, materialised for the K-contiguous GEMM."""
+    dev = require_hip("transpose_u8", t)
+    if t.dim() != 2 or t.element_size() != 1:
+        raise ValueError(f"transpose_u8: expected a 2-D byte tensor, got {t.dtype} {tuple(t.shape)}")
+    src = rows(t.view(torch.uint8))
+    R, C = src.shape
+    out = torch.empty(C, R, dtype=torch.uint8, device=dev)
+    kernels.check(kernels.lib().mls_transpose_u8(src.data_ptr(), R, C, ld(src), out.data_ptr(), ld(out),
+                                                 stream(dev)), "transpose_u8")
+    return out
+
+
 def dequantize_e4m3(bits: torch.Tensor, scale) -> torch.Tensor:
     """value(bits) * scale in fp32; the NaN patterns stay NaN, as in torch's float8
     view (kernels/fp8_matmul.py:109-110)."""
@@ -116,11 +157,14 @@ def dequantize_e4m3(bits: torch.Tensor, scale) -> torch.Tensor:
 
 def fp8_matmul(a_bits: torch.Tensor, b_bits: torch.Tensor,
                sa, sb, out_dtype: torch.dtype = torch.float32, *,
-               native: bool | None = None) -> torch.Tensor:
+               native: bool | None = None, a_format: str = "e4m3") -> torch.Tensor:
     """a_bits [M,K], b_bits [N,K] uint8 e4m3 -> sa*sb*(Â @ B̂ᵀ) [M,N]
     (kernels/fp8_matmul.py:113-128). sa / sb: float, 0-d tensor, or fp32 [M] / [N].
     native: use the fp8 matrix cores (see the module docstring); default from
-    MLS_FP8_NATIVE, else the exact bf16 datapath."""
+    MLS_FP8_NATIVE, else the exact bf16 datapath. a_format="e5m2": a_bits holds
+    e5m2 bytes (the gradient operand of FP8 training's backward, train/fp8.py:80-95)."""
+    if a_format not in _FORMATS:
+        raise ValueError(f"fp8_matmul: a_format {a_format!r} (e4m3 or e5m2)")
     if native is None:
         native = os.environ.get("MLS_FP8_NATIVE", "0") not in ("", "0")
     dev = require_hip("fp8_matmul", a_bits, b_bits)
@@ -138,6 +182,7 @@ def fp8_matmul(a_bits: torch.Tensor, b_bits: torch.Tensor,
     kernels.check(kernels.lib().mls_fp8_gemm(
         a2.data_ptr(), ld(a2), b2.data_ptr(), ld(b2),
         sa_args[0], sa_args[1], sa_args[2], sb_args[0], sb_args[1], sb_args[2],
-        c.data_ptr(), cdt, ld(c), M, N, K, kernels.MLS_FP8_NATIVE if native else 0, stream(dev)),
+        c.data_ptr(), cdt, ld(c), M, N, K, (kernels.MLS_FP8_NATIVE if native else 0) | _FORMATS[a_format],
+        stream(dev)),
         "fp8_matmul")
     return c

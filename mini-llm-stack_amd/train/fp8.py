@@ -2,10 +2,15 @@
 
 Same classes and behaviour as the reference's train/fp8.py (:33-131): the
 forward quantizes x and W to e4m3 with delayed per-tensor scales and, when
-use_kernel is set, multiplies them with kernels.fp8_matmul (native fp8 MFMA);
-otherwise it multiplies the decoded operands in fp32. The backward re-quantizes
-dy to e5m2 (just-in-time scale) and computes both gradients against the same
-fp8 operands the forward used, in fp32.
+use_kernel is set, multiplies them with kernels.fp8_matmul; otherwise it
+multiplies the decoded operands in fp32. The backward re-quantizes dy to e5m2
+(just-in-time scale) and computes both gradients against the same fp8 operands
+the forward used. The reference always emulates the backward in fp32
+(train/fp8.py:80-95); with use_kernel on a HIP device it runs here as two fp8
+GEMMs with an e5m2 operand (dx = dy W: dy [M,N] e5m2 times W^T [K,N] e4m3;
+dw = dy^T x: dy^T [N,M] times x^T [K,M]), the transposes materialised by a byte
+transpose kernel; the exact datapath reproduces the emulation's fp32 result up
+to summation order.
 """
 
 from __future__ import annotations
@@ -15,9 +20,8 @@ from collections import deque
 import torch
 import torch.nn as nn
 
-from kernels.fp8_matmul import E4M3_MAX, dequantize_e4m3, fp8_matmul, quantize_e4m3
-
-E5M2_MAX = 57344.0
+from kernels.fp8_matmul import (E4M3_MAX, E5M2_MAX, dequantize_e4m3, fp8_matmul, quantize_e4m3,
+                                quantize_e5m2, transpose_u8)
 
 
 class DynamicScaler:
@@ -40,8 +44,8 @@ class DynamicScaler:
 
 
 def _quant_e5m2(x: torch.Tensor, scale: float) -> torch.Tensor:
-    q = (x.float() / scale).clamp(-E5M2_MAX, E5M2_MAX)
-    return q.to(torch.float8_e5m2).view(torch.uint8)
+    """train/fp8.py:50-52 (the HIP encoder on device tensors, bit-exact)."""
+    return quantize_e5m2(x, scale)
 
 
 def _dequant_e5m2(bits: torch.Tensor, scale: float) -> torch.Tensor:
@@ -56,6 +60,7 @@ class _FP8LinearFn(torch.autograd.Function):
         ctx.save_for_backward(xb, wb)
         ctx.scales = (sx, sw)
         ctx.scale_grads = scale_grads
+        ctx.use_kernel = use_kernel
         if use_kernel:
             return fp8_matmul(xb, wb, sx, sw)
         return dequantize_e4m3(xb, sx) @ dequantize_e4m3(wb, sw).t()
@@ -68,7 +73,12 @@ class _FP8LinearFn(torch.autograd.Function):
             sdy = max(float(dy.detach().abs().amax()) / E5M2_MAX, 1e-12)
         else:
             sdy = 1.0
-        dyh = _dequant_e5m2(_quant_e5m2(dy, sdy), sdy)
+        dyb = _quant_e5m2(dy, sdy)
+        if ctx.use_kernel and dy.device.type == "cuda":
+            dx = fp8_matmul(dyb, transpose_u8(wb), sdy, sw, torch.float32, a_format="e5m2")
+            dw = fp8_matmul(transpose_u8(dyb), transpose_u8(xb), sdy, sx, torch.float32, a_format="e5m2")
+            return dx, dw, None, None, None, None
+        dyh = _dequant_e5m2(dyb, sdy)
         xh = dequantize_e4m3(xb, sx)
         wh = dequantize_e4m3(wb, sw)
         return dyh @ wh, dyh.t() @ xh, None, None, None, None

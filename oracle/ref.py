@@ -27,6 +27,11 @@ Each function cites the reference code it restates. Pins (see tests/test_oracle.
   combine_rows     the reference test's formula (test_moe_routing.py:21-28), brute
                    force per element, one-hot weights reduce it to a gather, zero
                    weights to zero, linearity in the weights.
+  e5m2_decode      torch's float8_e5m2 view of all 256 patterns (live) and closed-form
+                   points (max 57344, min normal 2^-14, min subnormal 2^-16, inf, NaN).
+  quantize_e5m2    torch's float8_e5m2 cast after the reference's clamp on every rounding
+                   boundary and random samples (live torch).
+  fp8_linear_backward  the reference's emulation sequence in torch fp64 on tiny inputs.
   naive_route      equals sort_by_expert + per-segment experts + combine_rows on
                    random routings (two formulations of the same forward), and the
                    reference's degenerate cases (all tokens to one expert,
@@ -106,6 +111,65 @@ def dequantize_e4m3(bits: np.ndarray, scale) -> np.ndarray:
     """kernels/fp8_matmul.py:109-110: exact value times the scale, one fp32 rounding."""
     return (e4m3_decode(bits, nan_to_zero=False) * np.asarray(scale, dtype=np.float32)).astype(
         np.float32)
+
+
+# ------------------------------------------------------------------ e5m2 (FP8 training gradients)
+
+E5M2_MAX = 57344.0
+
+
+def _e5m2_table() -> np.ndarray:
+    """Value of every byte: 1 sign, 5 exponent bits (bias 15), 2 mantissa bits;
+    exponent 0 is subnormal (m/4 * 2^-14); exponent 31 is inf (m = 0) or NaN
+    (OCP E5M2, torch.float8_e5m2; train/fp8.py:50-56)."""
+    vals = np.empty(256, dtype=np.float64)
+    for b in range(256):
+        s = -1.0 if b & 0x80 else 1.0
+        e = (b >> 2) & 0x1F
+        m = b & 0x3
+        if e == 31:
+            vals[b] = s * np.inf if m == 0 else np.nan
+        elif e == 0:
+            vals[b] = s * (m / 4.0) * 2.0 ** -14
+        else:
+            vals[b] = s * (1.0 + m / 4.0) * 2.0 ** (e - 15)
+    return vals
+
+
+E5M2_TABLE = _e5m2_table()
+_POS5_CODES = np.arange(0, 0x7C)               # 0x00 .. 0x7B: finite non-negative values
+_POS5_VALUES = E5M2_TABLE[_POS5_CODES]
+
+
+def e5m2_decode(bits: np.ndarray) -> np.ndarray:
+    """fp32 values of e5m2 bytes (torch's float8_e5m2 view, train/fp8.py:55-56)."""
+    return E5M2_TABLE[np.asarray(bits, dtype=np.uint8)].astype(np.float32)
+
+
+def quantize_e5m2(x: np.ndarray, scale) -> np.ndarray:
+    """train/fp8.py:50-52: q = float32(x) / float32(scale) (IEEE), clamp to
+    ±57344, then the nearest e5m2 value, ties to the even code (torch's cast);
+    NaN -> 0x7F with q's sign. Nearest-value search, like e4m3_encode."""
+    q = (np.asarray(x, dtype=np.float32) / np.asarray(scale, dtype=np.float32)).astype(np.float32)
+    sign = (q.view(np.uint32) >> 31).astype(np.uint8) << 7
+    a = np.minimum(np.abs(q.astype(np.float64)), E5M2_MAX)
+    hi = np.minimum(np.searchsorted(_POS5_VALUES, a, side="left"), len(_POS5_VALUES) - 1)
+    lo = np.maximum(hi - 1, 0)
+    d_lo, d_hi = a - _POS5_VALUES[lo], _POS5_VALUES[hi] - a
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & (_POS5_CODES[hi] % 2 == 0))
+    code = np.where(pick_hi, _POS5_CODES[hi], _POS5_CODES[lo]).astype(np.uint8)
+    code = np.where(np.isnan(q), np.uint8(0x7F), code)
+    return (code | sign).astype(np.uint8)
+
+
+def fp8_linear_backward(dy, xb, wb, sx, sw, sdy):
+    """_FP8LinearFn.backward (train/fp8.py:80-95) in fp64: dy re-quantized to e5m2
+    with scale sdy, then dx = dyh @ wh and dw = dyh^T @ xh against the forward's e4m3
+    operands xb [M,K] and wb [N,K] (scales sx, sw). Returns (dx [M,K], dw [N,K])."""
+    dyh = e5m2_decode(quantize_e5m2(dy, sdy)).astype(np.float64) * np.float32(sdy)
+    xh = E4M3_TABLE[np.asarray(xb, dtype=np.uint8)] * np.float32(sx)
+    wh = E4M3_TABLE[np.asarray(wb, dtype=np.uint8)] * np.float32(sw)
+    return dyh @ wh, dyh.T @ xh
 
 
 # ------------------------------------------------------------------ INT8 / INT4 weights

@@ -24,7 +24,7 @@ def declared_symbols() -> list[str]:
 
 def test_header_declares_the_boundary():
     syms = declared_symbols()
-    assert len(syms) == len(set(syms)) == 14
+    assert len(syms) == len(set(syms)) == 16
     assert set(syms) == set(kernels.SIGNATURES)
 
 
@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = kernels.load_library()
-    assert lib.mls_abi_version() == kernels.ABI_VERSION == 2
+    assert lib.mls_abi_version() == kernels.ABI_VERSION == 3
     assert isinstance(lib.mls_last_error(), bytes)
 
 
@@ -127,3 +127,15 @@ def test_gate_up_and_combine_reject():
     assert L.mls_moe_combine(1, bf, 8, 4, 1, bf, 1, 2, 2, 1, 4, 8, NULL) == kernels.MLS_ERR_ARG
     assert L.mls_moe_combine(1, bf, 8, 4, 1, bf, NULL, 2, 2, 1, 8, 8, NULL) == kernels.MLS_ERR_ARG
     assert L.mls_moe_combine(NULL, bf, 8, 0, NULL, bf, NULL, 0, 2, NULL, 8, 8, NULL) == 0
+
+
+def test_fp8_train_entry_points_reject():
+    L = kernels.load_library()
+    # unknown flag bit
+    assert L.mls_fp8_gemm(1, 64, 1, 64, 1.0, NULL, 0, 1.0, NULL, 0, 1, 0, 8, 4, 8, 64, 8, NULL) == \
+        kernels.MLS_ERR_ARG
+    assert L.mls_e5m2_encode(1, 5, 2, 2, 2, 1.0, NULL, 0, 1, 2, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_e5m2_encode(1, 0, 2, 4, 2, 1.0, NULL, 0, 1, 4, NULL) == kernels.MLS_ERR_ARG   # ldx < cols
+    assert L.mls_transpose_u8(1, 4, 8, 4, 1, 4, NULL) == kernels.MLS_ERR_ARG                  # lds < cols
+    assert L.mls_transpose_u8(1, 4, 8, 8, 1, 3, NULL) == kernels.MLS_ERR_ARG                  # ldd < rows
+    assert L.mls_transpose_u8(NULL, 0, 8, 8, NULL, 0, NULL) == 0

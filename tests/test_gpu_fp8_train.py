@@ -1,0 +1,139 @@
+"""FP8 training's backward on the GPU (train/fp8.py:80-95): the e5m2 encoder
+(bit-exact), the byte transpose (exact), the fp8 GEMM with an e5m2 A operand, and
+FP8Linear's kernel backward against the reference's fp32 emulation.
+
+Tolerances: fp32 outputs |Δ| <= 2^-9 max(|ref|, rms(ref)) (ref.close_fp32), 16-bit
+outputs rtol = atol = 1e-2 (ref.close_bf16), against the decode-then-fp64 oracle. The
+exact datapath widens e5m2 and e4m3 to bf16 without rounding, so it differs from the
+oracle by summation order only."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+from oracle import ref
+
+from kernels.fp8_matmul import E4M3_MAX, E5M2_MAX, fp8_matmul, quantize_e5m2, transpose_u8
+from train.fp8 import FP8Linear
+
+pytestmark = pytest.mark.gpu
+
+torch.backends.cuda.matmul.allow_tf32 = False
+
+
+def _boundaries():
+    v = ref._POS5_VALUES.astype(np.float64)
+    mids = (v[:-1] + v[1:]) / 2
+    pts = np.concatenate([v, mids, np.nextafter(mids.astype(np.float32), np.float32(0)),
+                          np.nextafter(mids.astype(np.float32), np.float32(np.inf)),
+                          [60000.0, 61440.0, 1e9, 2.0 ** -17, 3 * 2.0 ** -17]]).astype(np.float32)
+    return np.concatenate([pts, -pts, np.array([np.nan, -np.nan, np.inf, -np.inf], np.float32)])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("scale", [1.0, 0.37, 2.5e-6])
+def test_quantize_e5m2_bit_exact(dev, dtype, scale):
+    g = np.random.default_rng(int(scale * 1e6) + 3)
+    x = np.concatenate([_boundaries() * np.float32(scale),
+                        (g.standard_normal(100003) * 1e3 * scale).astype(np.float32)])
+    xt = torch.from_numpy(x).to(dtype)
+    got = quantize_e5m2(xt.to(dev), scale).cpu().numpy()
+    want = ref.quantize_e5m2(xt.float().numpy(), scale)
+    assert np.array_equal(got, want)
+
+
+def test_quantize_e5m2_strided_rows(dev):
+    g = torch.Generator().manual_seed(4)
+    full = torch.randn(37, 130, generator=g) * 100
+    x = full[:, 3:101]
+    got = quantize_e5m2(full.to(dev)[:, 3:101], 0.01).cpu().numpy()
+    assert np.array_equal(got, ref.quantize_e5m2(x.contiguous().numpy(), 0.01))
+
+
+@pytest.mark.parametrize("R,C,off", [(1, 1, 0), (64, 64, 0), (63, 65, 0), (1000, 37, 0),
+                                     (4096, 512, 0), (130, 300, 5)])
+def test_transpose_u8(dev, R, C, off):
+    g = torch.Generator().manual_seed(R * C)
+    full = torch.randint(0, 256, (R, C + off), generator=g, dtype=torch.uint8)
+    t = full[:, off:] if off else full
+    got = transpose_u8(full.to(dev)[:, off:] if off else full.to(dev))
+    assert got.shape == (C, R) and got.is_contiguous()
+    assert torch.equal(got.cpu(), t.t().contiguous())
+
+
+def test_every_e5m2_byte_widens(dev):
+    """Every finite e5m2 byte through the exact datapath's e5m2 -> bf16 widening:
+    A = the 248 finite bytes, B = identity (e4m3 1.0), C = their values."""
+    codes = np.array([b for b in range(256) if (b & 0x7F) < 0x7C], dtype=np.uint8)
+    K = 256
+    a = np.zeros((64, K), np.uint8)
+    a[0, :len(codes)] = codes
+    b = np.zeros((K, K), np.uint8)
+    b[np.arange(K), np.arange(K)] = 0x38
+    out = fp8_matmul(torch.from_numpy(a).to(dev), torch.from_numpy(b).to(dev), 1.0, 1.0, a_format="e5m2")
+    assert np.array_equal(out[0, :len(codes)].cpu().numpy(), ref.e5m2_decode(codes))
+
+
+def _operands(M, N, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn(M, K, generator=g) * 1e-3          # gradient-like magnitudes
+    b = torch.randn(N, K, generator=g)
+    sa = float(a.abs().amax()) / E5M2_MAX
+    sb = float(b.abs().amax()) / E4M3_MAX
+    ab = ref.quantize_e5m2(a.numpy(), sa)
+    bb = ref.quantize_e4m3(b.numpy(), sb)
+    want = (ref.e5m2_decode(ab).astype(np.float64) * np.float32(sa)) @ \
+        (ref.e4m3_decode(bb, nan_to_zero=False).astype(np.float64) * np.float32(sb)).T
+    return torch.from_numpy(ab), torch.from_numpy(bb), sa, sb, want
+
+
+@pytest.mark.parametrize("native", [False, True])
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (300, 200, 384), (1024, 512, 2048), (17, 33, 40)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_e5m2_gemm_paths(dev, M, N, K, native, out_dtype):
+    ab, bb, sa, sb, want = _operands(M, N, K, M + 7 * N + K)
+    out = fp8_matmul(ab.to(dev), bb.to(dev), sa, sb, out_dtype, native=native, a_format="e5m2")
+    o = out.float().cpu().numpy()
+    ok, worst = ref.close_fp32(o, want) if out_dtype == torch.float32 else ref.close_bf16(o, want)
+    assert ok, f"e5m2 x e4m3 {M}x{N}x{K} native={native}: worst {worst:.3g}"
+
+
+def test_e5m2_gemm_rejects_bad_format(dev):
+    ab, bb, sa, sb, _ = _operands(16, 16, 64, 1)
+    with pytest.raises(ValueError, match="a_format"):
+        fp8_matmul(ab.to(dev), bb.to(dev), sa, sb, a_format="e3m4")
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 128, 256), (300, 512, 192), (7, 24, 40)])
+def test_fp8_linear_backward_kernel_vs_emulation(dev, M, N, K):
+    """FP8Linear(use_kernel=True) backward (two e5m2 x e4m3 GEMMs + transposes) against
+    the reference's emulation (use_kernel=False) on the same weights, inputs and
+    upstream gradient; both against the oracle at the smallest shape."""
+    torch.manual_seed(M + N + K)
+    lin = nn.Linear(K, N, bias=False)
+    mk, me = FP8Linear(lin, use_kernel=True).to(dev), FP8Linear(lin, use_kernel=False).to(dev)
+    x = torch.randn(M, K, device=dev)
+    dy = torch.randn(M, N, device=dev) * 1e-2
+    grads = []
+    for m in (mk, me):
+        xi = x.clone().requires_grad_(True)
+        m(xi).backward(dy)
+        grads.append((xi.grad.float().cpu().numpy(), m.weight.grad.float().cpu().numpy()))
+    (dxk, dwk), (dxe, dwe) = grads
+    for got, want, what in ((dxk, dxe, "dx"), (dwk, dwe, "dw")):
+        ok, worst = ref.close_fp32(got, want)
+        assert ok, f"{what} {M}x{N}x{K}: worst {worst:.3g}"
+    if M * N * K < 10000:
+        # first call of the delayed scalers: just-in-time amax / fp8 max
+        sx = max(float(x.abs().amax()), 1e-12) / E4M3_MAX
+        sw = max(float(lin.weight.detach().abs().amax()), 1e-12) / E4M3_MAX
+        sdy = max(float(dy.abs().amax()) / E5M2_MAX, 1e-12)
+        xb = ref.quantize_e4m3(x.cpu().numpy(), sx)
+        wb = ref.quantize_e4m3(lin.weight.detach().numpy(), sw)
+        dx, dw = ref.fp8_linear_backward(dy.cpu().numpy(), xb, wb, sx, sw, sdy)
+        for got, want, what in ((dxk, dx, "dx"), (dwk, dw, "dw")):
+            ok, worst = ref.close_fp32(got, want)
+            assert ok, f"{what} vs oracle: worst {worst:.3g}"

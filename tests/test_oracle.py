@@ -327,6 +327,61 @@ def test_naive_route_equals_sorted_dispatch():
     assert not ref.naive_route(flat, np.zeros((20, 2)), g.integers(0, 2, size=(20, 2)), fn, 2).any()
 
 
+def _e5m2_boundaries():
+    """Every midpoint between adjacent finite e5m2 values, one fp32 ulp either side,
+    the values themselves, the clamp edge and the specials (both signs)."""
+    v = ref._POS5_VALUES.astype(np.float64)
+    mids = (v[:-1] + v[1:]) / 2
+    pts = np.concatenate([v, mids, np.nextafter(mids.astype(np.float32), np.float32(0)),
+                          np.nextafter(mids.astype(np.float32), np.float32(np.inf)),
+                          [57344.0, 60000.0, 61439.0, 61440.0, 1e9, 2.0 ** -17, 3 * 2.0 ** -17, 2.0 ** -30]])
+    pts = pts.astype(np.float32)
+    return np.concatenate([pts, -pts, np.array([np.nan, -np.nan, np.inf, -np.inf], np.float32)])
+
+
+def test_e5m2_decode_table_and_closed_forms():
+    b = np.arange(256, dtype=np.uint8)
+    t = torch.from_numpy(b).view(torch.float8_e5m2).float().numpy()
+    assert np.array_equal(ref.e5m2_decode(b), t, equal_nan=True)
+    d = ref.e5m2_decode(np.array([0x7B, 0x04, 0x01, 0x7C, 0xFC, 0x7D, 0x80], np.uint8))
+    assert d[0] == 57344.0 and d[1] == 2.0 ** -14 and d[2] == 2.0 ** -16
+    assert d[3] == np.inf and d[4] == -np.inf and np.isnan(d[5]) and d[6] == 0 and np.signbit(d[6])
+
+
+@pytest.mark.parametrize("scale", [1.0, 0.37, 3e-6])
+def test_quantize_e5m2_matches_torch_cast(scale):
+    """train/fp8.py:50-52 run by torch on the CPU, on every rounding boundary (scaled
+    back by the scale) and random samples."""
+    g = np.random.default_rng(11)
+    x = np.concatenate([_e5m2_boundaries() * np.float32(scale),
+                        (g.standard_normal(20000) * 1e3 * scale).astype(np.float32)]).astype(np.float32)
+    q = (torch.from_numpy(x).float() / scale).clamp(-57344.0, 57344.0)
+    want = q.to(torch.float8_e5m2).view(torch.uint8).numpy()
+    assert np.array_equal(ref.quantize_e5m2(x, scale), want)
+
+
+def test_fp8_linear_backward_matches_torch_emulation():
+    """The reference's backward op sequence (train/fp8.py:80-95) in torch fp64."""
+    g = np.random.default_rng(12)
+    M, N, K = 6, 5, 7
+    dy = (g.standard_normal((M, N)) * 1e-3).astype(np.float32)
+    xb = g.integers(0, 256, size=(M, K), dtype=np.uint8)
+    wb = g.integers(0, 256, size=(N, K), dtype=np.uint8)
+    xb[xb & 0x7F == 0x7F] = 0
+    wb[wb & 0x7F == 0x7F] = 0
+    sx, sw = 0.01, 0.002
+    sdy = float(np.abs(dy).max()) / 57344.0
+    dx, dw = ref.fp8_linear_backward(dy, xb, wb, sx, sw, sdy)
+    q = (torch.from_numpy(dy) / sdy).clamp(-57344.0, 57344.0).to(torch.float8_e5m2)
+    dyh = q.double() * torch.tensor(sdy, dtype=torch.float32).double()
+    xh = torch.from_numpy(xb).view(torch.float8_e4m3fn).double() * np.float32(sx)
+    wh = torch.from_numpy(wb).view(torch.float8_e4m3fn).double() * np.float32(sw)
+    assert np.allclose(dx, (dyh @ wh).numpy(), rtol=1e-12, atol=0)
+    assert np.allclose(dw, (dyh.t() @ xh).numpy(), rtol=1e-12, atol=0)
+    # brute force for one element of each
+    assert abs(dx[2, 3] - sum(float(dyh[2, n]) * float(wh[n, 3]) for n in range(N))) < 1e-15
+
+
 def test_routing_matches_golden():
     d = golden("route_small")
     w, ex = ref.route_topk(d["logits"], 2)
@@ -381,6 +436,11 @@ def test_planted_mistakes_fail_the_pins():
     off = np.array([0, 4])
     h = ref.grouped_int4_gate_up(a, wg, sc, wu, sc, off, 32)
     assert not ref.close_fp32(ref.grouped_int4_gate_up(a, wu, sc, wg, sc, off, 32), h)[0]
+    # e5m2 ties rounded away from zero instead of to even
+    v = ref._POS5_VALUES
+    mids = ((v[:-1] + v[1:]) / 2).astype(np.float32)
+    away = np.arange(1, len(v)).astype(np.uint8)              # always the upper neighbour
+    assert not np.array_equal(away, ref.quantize_e5m2(mids, 1.0))
     # combine reading pos transposed ([k, T] order)
     x = g.standard_normal((12, 4))
     w = g.random((6, 2))
