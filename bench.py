@@ -13,8 +13,8 @@ HIP events; value = algorithmic bytes x K / elapsed.
 The other BASELINE configs (INT4 M = 4 / 16, the INT8 GEMV target, INT8 prefill,
 FP8 e4m3 GEMM, INT4 MoE grouped GEMM) and the whole INT4 SwiGLU expert MLP of a
 routed MoE layer (gate/up, down, combine), FP8Linear's backward at config D's shape
-(e5m2 gradients) and the load-time INT4 quantizer are reported under "extra" with the
-same protocol, followed by a 256 MiB streaming copy (the bandwidth a plain elementwise
+(e5m2 gradients), paged-attention decode over a bf16 KV cache and the load-time INT4
+quantizer are reported under "extra" with the same protocol, followed by a 256 MiB streaming copy (the bandwidth a plain elementwise
 kernel reaches on this GPU). cpu_baseline times the reference's CPU algorithm (the numpy
 restatement in oracle/: dequantize, then fp32 matmul) on the host for a bounded
 sample of the headline workload.
@@ -196,6 +196,26 @@ def fp8_backward(dev, steps: int, warmup: int, M=4096, N=8192, K=8192, native=Fa
     return dict(ms=ms, bytes=nbytes, flops=2 * 2 * M * N * K, copies=copies)
 
 
+def paged_attn(dev, steps: int, warmup: int, S=64, H=32, D=128, ctx=2048, bs=16):
+    """Paged-attention decode (kernels/paged_attention.py): S sequences of `ctx` cached
+    tokens each, H heads of D, bf16 pools in blocks of `bs` tokens handed out in a
+    shuffled order (as a long-running pool fragments). HBM-bound on the K/V reads."""
+    import torch
+    from kernels.paged_attention import paged_attention_decode
+    g = torch.Generator(device=dev).manual_seed(8)
+    nb = S * ctx // bs
+    kp = torch.randn(nb, H, bs, D, generator=g, device=dev).to(torch.bfloat16)
+    vp = torch.randn(nb, H, bs, D, generator=g, device=dev).to(torch.bfloat16)
+    perm = torch.randperm(nb, generator=g, device=dev).to(torch.int32)
+    tables = perm.reshape(S, ctx // bs).contiguous()
+    lens = torch.full((S,), ctx, dtype=torch.int32, device=dev)
+    q = torch.randn(S, H, D, generator=g, device=dev).to(torch.bfloat16)
+    fns = [lambda: paged_attention_decode(q, kp, vp, tables, lens)]
+    ms = time_steps(fns, warmup, steps)
+    nbytes = 2 * S * ctx * H * D * 2 + 2 * S * H * D * 2 + S * (ctx // bs) * 4 + S * 4
+    return dict(ms=ms, bytes=nbytes, flops=4 * S * H * ctx * D, copies=1)
+
+
 def moe_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=128):
     import torch
     from kernels.moe_grouped import int4_grouped_matmul
@@ -365,7 +385,8 @@ def main(argv=None) -> int:
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--only", default=None,
                     help="run one workload: int4_gemv, int4_m4, int4_m16, int8_gemv, int8_prefill, "
-                         "fp8_gemm, fp8_native, fp8_bwd, fp8_bwd_native, moe_int4, moe_mlp_int4, quantize_int4, "
+                         "fp8_gemm, fp8_native, fp8_bwd, fp8_bwd_native, moe_int4, moe_mlp_int4, paged_attn, "
+                         "quantize_int4, "
                          "copy (counter calibration)")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -416,6 +437,8 @@ def main(argv=None) -> int:
                                                       "launches": "gate/up + down + combine",
                                                       "segments": r["counts"]}))(
             moe_mlp_int4(dev, small, 4)),
+        "paged_attn": lambda: _hbm_row("paged_attention_decode_64seq_32h_d128_ctx2048_bf16",
+                                       paged_attn(dev, small, 4)),
         "quantize_int4": lambda: _hbm_row("quantize_int4_14336x4096_g128", quantize_int4_load(dev, small, 4)),
         "copy": lambda: _hbm_row("copy_256MiB", copy_calibration(dev, small, 4)),
     }
@@ -432,7 +455,8 @@ def main(argv=None) -> int:
     extra = []
     if not args.no_extra:
         for k in ("int4_m4", "int4_m16", "int8_gemv", "int8_prefill", "fp8_gemm", "fp8_native",
-                  "fp8_bwd", "fp8_bwd_native", "moe_int4", "moe_mlp_int4", "quantize_int4", "copy"):
+                  "fp8_bwd", "fp8_bwd_native", "moe_int4", "moe_mlp_int4", "paged_attn", "quantize_int4",
+                  "copy"):
             log(f"{k} ...")
             row = runners[k]()
             log(json.dumps(row))

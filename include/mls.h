@@ -39,7 +39,7 @@ enum {
   MLS_ERR_HIP = -3          /* a HIP runtime call failed */
 };
 
-#define MLS_ABI_VERSION 3
+#define MLS_ABI_VERSION 4
 
 /* No reference counterpart: version of this ABI (MLS_ABI_VERSION). */
 int mls_abi_version(void);
@@ -192,6 +192,24 @@ int mls_int4_grouped_gate_up(const void* a, int a_dt, int64_t lda,
 int mls_moe_combine(const void* x, int x_dt, int64_t ldx, int64_t x_rows, const void* w, int w_dt,
                     const int64_t* pos, int64_t T, int k, void* out, int64_t ldo,
                     int64_t D, mls_stream_t stream);
+
+/* Replaces _paged_attn_kernel + paged_attention_decode (kernels/paged_attention.py:33-118):
+ * out[s][h][:] = softmax_j(scale * q[s][h] . K_j) V_j over the context_lens[s] tokens of
+ * sequence s, token j at row j % block_size of block block_tables[s][j / block_size].
+ * q, out: [n_seqs][H][D] (strides q_ss/q_sh, o_ss/o_sh; unit stride in D), q_dt (out too);
+ * pools: [num_blocks][H][block_size][D] of kv_dt, strides kv_sb/kv_sh/kv_st shared by K and
+ * V, unit stride in D. Tokens at or past the context length weigh 0; a block id outside
+ * [0, num_blocks) is skipped; a zero context gives zeros. The workspace (fp32) must hold
+ * mls_paged_attention_workspace(n_seqs, H, D, max_blocks) floats (0: none needed). */
+int64_t mls_paged_attention_workspace(int64_t n_seqs, int64_t H, int64_t D, int64_t max_blocks);
+int mls_paged_attention_decode(const void* q, int q_dt, int64_t q_ss, int64_t q_sh,
+                               const void* k_pool, const void* v_pool, int kv_dt,
+                               int64_t kv_sb, int64_t kv_sh, int64_t kv_st, int64_t num_blocks,
+                               const int32_t* block_tables, int64_t bt_ss, int64_t max_blocks,
+                               const int32_t* context_lens,
+                               void* out, int64_t o_ss, int64_t o_sh,
+                               int64_t n_seqs, int64_t H, int64_t D, int64_t block_size, float scale,
+                               float* workspace, int64_t workspace_floats, mls_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -32,6 +32,12 @@ Each function cites the reference code it restates. Pins (see tests/test_oracle.
   quantize_e5m2    torch's float8_e5m2 cast after the reference's clamp on every rounding
                    boundary and random samples (live torch).
   fp8_linear_backward  the reference's emulation sequence in torch fp64 on tiny inputs.
+  attention        torch's scaled_dot_product_attention on the CPU; closed forms (one key
+                   -> its value; equal keys -> the mean of the values).
+  paged_attention_decode  equals attention() on the contiguous K/V it was scattered from
+                   (the reference's test, test_serving.py:62-84); poisoned slots past the
+                   context are ignored (:87-106); invariant under a permutation of the
+                   pool's blocks with the tables permuted alike.
   naive_route      equals sort_by_expert + per-segment experts + combine_rows on
                    random routings (two formulations of the same forward), and the
                    reference's degenerate cases (all tokens to one expert,
@@ -311,6 +317,39 @@ def naive_route(flat, weights, experts_idx, expert_fn, n_experts) -> np.ndarray:
         tok, slot = np.nonzero(np.asarray(experts_idx) == e)
         if tok.size:
             np.add.at(out, tok, np.asarray(expert_fn(e, x[tok]), dtype=np.float64) * w[tok, slot, None])
+    return out
+
+
+# ------------------------------------------------------------------ paged-attention decode
+
+
+def attention(q, k, v, scale) -> np.ndarray:
+    """softmax(scale * q k^T) v in fp64 for one query row (train/model.py:55-70 with
+    causal=False: the decode case, every cached key visible). q [D], k, v [L, D]."""
+    q, k, v = (np.asarray(t, dtype=np.float64) for t in (q, k, v))
+    if k.shape[0] == 0:
+        return np.zeros(q.shape[-1])
+    s = (k @ q) * scale
+    p = np.exp(s - s.max())
+    return (p / p.sum()) @ v
+
+
+def paged_attention_decode(q, k_pool, v_pool, block_tables, context_lens, scale=None) -> np.ndarray:
+    """kernels/paged_attention.py:33-118: for each (sequence, head), the keys and values
+    of the sequence's first context_lens[s] tokens, token j at row j % block_size of
+    block block_tables[s][j // block_size], attended by q[s, h]. fp64 result."""
+    q = np.asarray(q)
+    n, H, D = q.shape
+    bs = k_pool.shape[2]
+    scale = D ** -0.5 if scale is None else scale
+    out = np.zeros((n, H, D))
+    for s in range(n):
+        L = int(context_lens[s])
+        rows = [(int(block_tables[s][j // bs]), j % bs) for j in range(L)]
+        for h in range(H):
+            k = np.array([k_pool[b, h, r] for b, r in rows], dtype=np.float64).reshape(L, D)
+            v = np.array([v_pool[b, h, r] for b, r in rows], dtype=np.float64).reshape(L, D)
+            out[s, h] = attention(q[s, h], k, v, scale)
     return out
 
 

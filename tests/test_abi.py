@@ -19,12 +19,12 @@ NULL = None
 
 def declared_symbols() -> list[str]:
     text = HEADER.read_text()
-    return re.findall(r"^\s*(?:int|const char\*)\s+(mls_\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(mls_\w+)\s*\(", text, flags=re.M)
 
 
 def test_header_declares_the_boundary():
     syms = declared_symbols()
-    assert len(syms) == len(set(syms)) == 16
+    assert len(syms) == len(set(syms)) == 18
     assert set(syms) == set(kernels.SIGNATURES)
 
 
@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = kernels.load_library()
-    assert lib.mls_abi_version() == kernels.ABI_VERSION == 3
+    assert lib.mls_abi_version() == kernels.ABI_VERSION == 4
     assert isinstance(lib.mls_last_error(), bytes)
 
 
@@ -139,3 +139,28 @@ def test_fp8_train_entry_points_reject():
     assert L.mls_transpose_u8(1, 4, 8, 4, 1, 4, NULL) == kernels.MLS_ERR_ARG                  # lds < cols
     assert L.mls_transpose_u8(1, 4, 8, 8, 1, 3, NULL) == kernels.MLS_ERR_ARG                  # ldd < rows
     assert L.mls_transpose_u8(NULL, 0, 8, 8, NULL, 0, NULL) == 0
+
+
+def test_paged_attention_rejects_and_sizes_workspace():
+    L = kernels.load_library()
+    f32 = kernels.MLS_F32
+    # no workspace needed for many (sequence, head) pairs; a split needs n*H*s*(D+2)
+    assert L.mls_paged_attention_workspace(128, 32, 128, 128) == 0
+    w = L.mls_paged_attention_workspace(1, 2, 64, 313)
+    assert w > 0 and w % (2 * 66) == 0
+    args = dict(q=1, qdt=f32, qss=64, qsh=32, k=1, v=1, kvdt=f32, sb=512, sh=256, st=32, nb=4, bt=1, btss=2,
+                mb=2, ctx=1, out=1, oss=64, osh=32, n=1, H=2, D=32, bs=8, scale=1.0, ws=NULL, wsn=0)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return L.mls_paged_attention_decode(a["q"], a["qdt"], a["qss"], a["qsh"], a["k"], a["v"], a["kvdt"],
+                                            a["sb"], a["sh"], a["st"], a["nb"], a["bt"], a["btss"], a["mb"],
+                                            a["ctx"], a["out"], a["oss"], a["osh"], a["n"], a["H"], a["D"],
+                                            a["bs"], a["scale"], a["ws"], a["wsn"], NULL)
+
+    assert call(bs=0) == kernels.MLS_ERR_ARG
+    assert call(qdt=9) == kernels.MLS_ERR_ARG
+    assert call(ctx=NULL) == kernels.MLS_ERR_ARG
+    assert call(st=16) == kernels.MLS_ERR_ARG                 # row stride below D
+    assert call(btss=1) == kernels.MLS_ERR_ARG                # table rows overlap
+    assert call(n=0) == 0

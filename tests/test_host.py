@@ -42,6 +42,10 @@ def test_kernel_entry_points_refuse_host_tensors():
         int4_grouped_gate_up(a.bfloat16(), w4[None], s4[None], w4[None], s4[None], torch.tensor([2]), 32)
     with pytest.raises(TypeError, match="HIP device"):
         combine_rows(torch.randn(4, 8), torch.rand(2, 2), torch.arange(4).reshape(2, 2))
+    from kernels.paged_attention import paged_attention_decode
+    with pytest.raises(TypeError, match="HIP device"):
+        paged_attention_decode(torch.randn(1, 2, 16), torch.randn(4, 2, 8, 16), torch.randn(4, 2, 8, 16),
+                               torch.zeros(1, 1, dtype=torch.int32), torch.ones(1, dtype=torch.int32))
     # the routed MoE forward has no host path either: its combine is the HIP kernel
     experts = [nn.Linear(64, 64, bias=False) for _ in range(2)]
     with pytest.raises(TypeError, match="HIP device"):

@@ -382,6 +382,71 @@ def test_fp8_linear_backward_matches_torch_emulation():
     assert abs(dx[2, 3] - sum(float(dyh[2, n]) * float(wh[n, 3]) for n in range(N))) < 1e-15
 
 
+def _scatter(ks, vs, H, D, bs, num_blocks, rng):
+    """Write per-sequence contiguous K/V [H, L, D] into random free blocks of a pool;
+    returns pools, padded tables and lengths."""
+    kp = rng.standard_normal((num_blocks, H, bs, D))
+    vp = rng.standard_normal((num_blocks, H, bs, D))
+    free = list(rng.permutation(num_blocks))
+    tables = []
+    for k, v in zip(ks, vs):
+        L = k.shape[1]
+        blocks = [int(free.pop()) for _ in range((L + bs - 1) // bs)]
+        for j in range(L):
+            kp[blocks[j // bs], :, j % bs] = k[:, j]
+            vp[blocks[j // bs], :, j % bs] = v[:, j]
+        tables.append(blocks)
+    mb = max(len(t) for t in tables)
+    tab = np.array([t + [0] * (mb - len(t)) for t in tables], dtype=np.int32)
+    return kp, vp, tab, np.array([k.shape[1] for k in ks], dtype=np.int32)
+
+
+def test_attention_matches_torch_sdpa_and_closed_forms():
+    g = np.random.default_rng(13)
+    q, k, v = g.standard_normal(16), g.standard_normal((9, 16)), g.standard_normal((9, 16))
+    want = torch.nn.functional.scaled_dot_product_attention(
+        torch.from_numpy(q)[None, None], torch.from_numpy(k)[None], torch.from_numpy(v)[None])[0, 0]
+    assert np.allclose(ref.attention(q, k, v, 16 ** -0.5), want.numpy(), rtol=1e-12, atol=1e-12)
+    assert np.allclose(ref.attention(q, k[:1], v[:1], 0.3), v[0])
+    assert np.allclose(ref.attention(q, np.repeat(k[:1], 5, 0), v[:5], 0.3), v[:5].mean(0))
+
+
+@pytest.mark.parametrize("lens", [[7], [16], [5, 23, 12], [1, 1, 40]])
+def test_paged_oracle_matches_contiguous(lens):
+    """test_serving.py:62-84 of the reference, on the oracle: paged == contiguous."""
+    g = np.random.default_rng(sum(lens))
+    H, D, bs = 4, 32, 8
+    ks = [g.standard_normal((H, L, D)) for L in lens]
+    vs = [g.standard_normal((H, L, D)) for L in lens]
+    kp, vp, tab, ctx = _scatter(ks, vs, H, D, bs, 32, g)
+    q = g.standard_normal((len(lens), H, D))
+    out = ref.paged_attention_decode(q, kp, vp, tab, ctx)
+    for i in range(len(lens)):
+        for h in range(H):
+            assert np.allclose(out[i, h], ref.attention(q[i, h], ks[i][h], vs[i][h], D ** -0.5), atol=1e-12)
+    # a permutation of the pool's blocks, with the tables renamed alike, changes nothing
+    perm = g.permutation(32)
+    inv = np.argsort(perm)
+    out2 = ref.paged_attention_decode(q, kp[perm], vp[perm], inv[tab].astype(np.int32), ctx)
+    assert np.allclose(out, out2, atol=1e-12)
+
+
+def test_paged_oracle_ignores_slots_past_context():
+    """test_serving.py:87-106: poisoned slots of a partially filled block do not leak."""
+    g = np.random.default_rng(14)
+    H, D, bs = 2, 16, 8
+    k, v = g.standard_normal((1, H, 5, D)), g.standard_normal((1, H, 5, D))
+    kp, vp, tab, ctx = _scatter([k[0]], [v[0]], H, D, bs, 4, g)
+    kp[tab[0, 0], :, 5:] = 1e6
+    vp[tab[0, 0], :, 5:] = 1e6
+    q = g.standard_normal((1, H, D))
+    out = ref.paged_attention_decode(q, kp, vp, tab, ctx)
+    assert np.allclose(out[0, 1], ref.attention(q[0, 1], k[0, 1], v[0, 1], D ** -0.5), atol=1e-12)
+    # planted: counting one token too many picks up the poison
+    bad = ref.paged_attention_decode(q, kp, vp, tab, ctx + 1)
+    assert not np.allclose(bad, out, atol=1e-3)
+
+
 def test_routing_matches_golden():
     d = golden("route_small")
     w, ex = ref.route_topk(d["logits"], 2)
