@@ -137,3 +137,22 @@ def test_fp8_linear_backward_kernel_vs_emulation(dev, M, N, K):
         for got, want, what in ((dxk, dx, "dx"), (dwk, dw, "dw")):
             ok, worst = ref.close_fp32(got, want)
             assert ok, f"{what} vs oracle: worst {worst:.3g}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("fmt", ["e4m3", "e5m2"])
+def test_encoders_vector_path(dev, dtype, fmt):
+    """Rows of a multiple of 4 elements take the 4-per-thread encoder: bit-exact too,
+    including boundaries, NaN and per-row scales."""
+    from kernels.fp8_matmul import quantize_e4m3
+    g = np.random.default_rng(5)
+    pts = _boundaries() if fmt == "e5m2" else np.concatenate(
+        [ref._POS_VALUES, (ref._POS_VALUES[:-1] + ref._POS_VALUES[1:]) / 2]).astype(np.float32)
+    x = np.concatenate([pts, -pts, (g.standard_normal(4096 * 4) * 50).astype(np.float32)])
+    x = x[: (x.size // 256) * 256].reshape(-1, 256)
+    xt = torch.from_numpy(x).to(dtype)
+    enc = quantize_e5m2 if fmt == "e5m2" else quantize_e4m3
+    want_fn = ref.quantize_e5m2 if fmt == "e5m2" else ref.quantize_e4m3
+    assert np.array_equal(enc(xt.to(dev), 0.5).cpu().numpy(), want_fn(xt.float().numpy(), 0.5))
+    rs = torch.rand(x.shape[0], 1, generator=torch.Generator().manual_seed(2)) + 0.1
+    assert np.array_equal(enc(xt.to(dev), rs.to(dev)).cpu().numpy(), want_fn(xt.float().numpy(), rs.numpy()))
