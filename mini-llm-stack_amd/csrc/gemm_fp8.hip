@@ -30,6 +30,11 @@
 
 namespace mls {
 
+template <int R>
+struct Ring {
+  static constexpr int v = R;
+};
+
 __device__ __forceinline__ float e4m3_ref_value(uint32_t b) {
   const uint32_t e = (b >> 3) & 15u, m = b & 7u;
   float mag = e == 0 ? (float)m * 0x1p-9f : __uint_as_float(((e + 120u) << 23) | (m << 20));
@@ -237,7 +242,10 @@ __global__ __launch_bounds__(64 * WM * WN) void fp8_gemm_dma_kernel(
   constexpr int PW = SLOTS / (64 * NW);  // loads per wavefront and operand
   constexpr int GM = 4;
   static_assert(PW >= 1 && SLOTS % (64 * NW) == 0, "slots");
-  __shared__ __align__(16) uint4 lds[4 * SLOTS];  // A0 | B0 | A1 | B1
+  // double buffers in separate arrays: the compiler then knows that the LDS-direct
+  // loads of the next stage (into one pair) cannot touch the pair being read, and
+  // keeps no wait for them before those reads
+  __shared__ __align__(16) uint4 A0[SLOTS], B0[SLOTS], A1[SLOTS], B1[SLOTS];
 
   const int L = xcd_remap(blockIdx.x, gridDim.x);
   const int per_group = GM * n_tiles;
@@ -285,32 +293,41 @@ __global__ __launch_bounds__(64 * WM * WN) void fp8_gemm_dma_kernel(
     const uint4 hi = base[row * 8 + ((lk + 4) ^ sw)];
     return i32x8{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
   };
-  // Stage s lives in buffer s & 1. Each stage first reads all of its operands into
-  // registers, then issues the loads of stage s + 1 into the other buffer, then runs
-  // its MFMAs: the loads complete under the MFMAs, and the wait the compiler places
-  // for them before the next LDS read falls after this stage's closing barrier anyway.
+  // Stage kt lives in buffer pair kt & 1. At its start the LDS-direct loads of stage
+  // kt + 1 go out into the other pair (last read in stage kt - 1, before the barrier
+  // that ended it), so they have the whole stage to land. The B operands are read
+  // first; each A operand is read one MFMA group ahead of its use, so LDS reads
+  // overlap the MFMAs. The closing wait covers stage kt + 1's loads for the barrier.
   const int nk = K / BK;
-  dma(lds, lds + SLOTS, 0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const uint4* const as = lds + (kt & 1) * 2 * SLOTS;
-    const uint4* const bs = as + SLOTS;
-    uint4* const an = lds + ((kt & 1) ^ 1) * 2 * SLOTS;
-    i32x8 bop[TN], aop[TM];
+  auto stage = [&](auto pc, int kt) __attribute__((always_inline)) {
+    constexpr int P = decltype(pc)::v;
+    const uint4* const as = P ? A1 : A0;
+    const uint4* const bs = P ? B1 : B0;
+    __builtin_amdgcn_sched_barrier(0);
+    dma(P ? A0 : A1, P ? B0 : B1, (kt + 1) * BK);  // past the end: harmless reads
+    __builtin_amdgcn_sched_barrier(0);
+    i32x8 bop[TN], aop[2];
 #pragma unroll
     for (int i = 0; i < TN; ++i) bop[i] = operand(bs, wn0 + i * 16 + lr);
+    aop[0] = operand(as, wm0 + lr);
 #pragma unroll
-    for (int j = 0; j < TM; ++j) aop[j] = operand(as, wm0 + j * 16 + lr);
+    for (int j = 0; j < TM; ++j) {
+      if (j + 1 < TM) aop[(j + 1) & 1] = operand(as, wm0 + (j + 1) * 16 + lr);
+#pragma unroll
+      for (int i = 0; i < TN; ++i) acc[i][j] = mfma_fp8<FA>(bop[i], aop[j & 1], acc[i][j]);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    dma(an, an + SLOTS, (kt + 1) * BK);  // past the end: harmless reads
-    __builtin_amdgcn_sched_barrier(0);   // issued before the MFMAs, not after them
-#pragma unroll
-    for (int j = 0; j < TM; ++j)
-#pragma unroll
-      for (int i = 0; i < TN; ++i) acc[i][j] = mfma_fp8<FA>(bop[i], aop[j], acc[i][j]);
-    __builtin_amdgcn_sched_barrier(0);  // the MFMAs stay ahead of the barrier's wait
-    __syncthreads();
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  dma(A0, B0, 0);
+  __syncthreads();
+  int kt = 0;
+  for (; kt + 2 <= nk; kt += 2) {
+    stage(Ring<0>{}, kt);
+    stage(Ring<1>{}, kt + 1);
   }
+  if (kt < nk) stage(Ring<0>{}, kt);
 
 #pragma unroll
   for (int i = 0; i < TN; ++i) {
