@@ -229,7 +229,7 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds,
 }
 
 template <typename CT, int WM, int WN, int FA>
-__global__ __launch_bounds__(64 * WM * WN) void fp8_gemm_dma_kernel(
+__global__ __launch_bounds__(64 * WM * WN, 1) void fp8_gemm_dma_kernel(
     const uint8_t* __restrict__ a, int64_t lda, const uint8_t* __restrict__ b, int64_t ldb,
     float sa, const float* __restrict__ sap, int64_t sas, float sb,
     const float* __restrict__ sbp, int64_t sbs, CT* __restrict__ c, int64_t ldc, int M, int N,
