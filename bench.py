@@ -248,8 +248,8 @@ def moe_mlp_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=1
     gate/up launch (silu(x Wg^T) * x Wu^T), the down launch, and the weighted combine
     back to token order (kernels/moe_routing.py:145-153 with INT4 experts)."""
     import torch
-    from kernels.moe_grouped import int4_expert_mlp, segment_offsets
-    from kernels.moe_routing import combine_rows, gather_rows, route_topk, sort_by_expert
+    from kernels.moe_grouped import int4_expert_mlp_combine, segment_offsets
+    from kernels.moe_routing import gather_rows, route_topk, sort_by_expert
     from serve.quantize import quantize_int4
     g = torch.Generator(device=dev).manual_seed(5)
     x = torch.randn(T, D, generator=g, device=dev).to(torch.bfloat16)
@@ -270,7 +270,7 @@ def moe_mlp_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=1
                 S.append(s.to(torch.float16))
             mats += [torch.stack(P), torch.stack(S)]
         sets.append(mats)
-    fns = [lambda m=m: combine_rows(int4_expert_mlp(a, off, *m, gs), w, pos) for m in sets]
+    fns = [lambda m=m: int4_expert_mlp_combine(a, off, *m, gs, w, pos) for m in sets]
     ms = time_steps(fns, warmup, steps)
     rows = T * 2
     nbytes = 3 * (E * H * D // 2 + E * H * (D // gs) * 2) + rows * D * 2 * 2 + rows * H * 2 * 2 + T * D * 2

@@ -39,7 +39,7 @@ enum {
   MLS_ERR_HIP = -3          /* a HIP runtime call failed */
 };
 
-#define MLS_ABI_VERSION 4
+#define MLS_ABI_VERSION 5
 
 /* No reference counterpart: version of this ABI (MLS_ABI_VERSION). */
 int mls_abi_version(void);
@@ -186,12 +186,29 @@ int mls_int4_grouped_gate_up(const void* a, int a_dt, int64_t lda,
                              int64_t H, int64_t K, mls_stream_t stream);
 
 /* Replaces _combine_rows_kernel + combine_rows (kernels/moe_routing.py:52-76, 100-113):
- * out[t][d] = sum_{s<k} w[t][s] * x[pos[t][s]][d], fp32 accumulation, one rounding;
- * one block per output row, no atomics. x: x_dt [x_rows][ldx]; out: x_dt; w: w_dt ([T][k]);
- * pos: int64 [T][k]; a position outside [0, x_rows) contributes nothing. */
-int mls_moe_combine(const void* x, int x_dt, int64_t ldx, int64_t x_rows, const void* w, int w_dt,
-                    const int64_t* pos, int64_t T, int k, void* out, int64_t ldo,
-                    int64_t D, mls_stream_t stream);
+ * out[t][d] = sum_{s<k} w[t][s] * X(pos[t][s], d), fp32 accumulation, one rounding; one block
+ * per output row, no atomics. x: x_dt [x_rows][ldx]; X(r, d) = x[r][d], or with splits > 1
+ * the sum of the `splits` partial products x[p * split_stride + r * ldx + d] of a K-split
+ * GEMM (mls_int4_grouped_gemm_partial). out: out_dt [T][ldo]; w: w_dt [T][k]; pos: int64
+ * [T][k]; a position outside [0, x_rows) contributes nothing. */
+int mls_moe_combine(const void* x, int x_dt, int64_t ldx, int64_t x_rows, int splits, int64_t split_stride,
+                    const void* w, int w_dt, const int64_t* pos, int64_t T, int k,
+                    void* out, int out_dt, int64_t ldo, int64_t D, mls_stream_t stream);
+
+/* No single reference counterpart: the down projection of the INT4 expert MLP
+ * (train/model.py:135 per expert, kernels/moe_routing.py:145-151) as `splits` fp32
+ * partial products over equal K ranges, partial[p][r][n] at partial + p * split_stride +
+ * r * ldp + n, for mls_moe_combine to sum: a narrow output (few column tiles) then still
+ * spreads over two blocks per CU. Arguments otherwise as mls_int4_grouped_gemm; needs
+ * K / splits a multiple of 64 and of the group (MLS_ERR_UNSUPPORTED otherwise).
+ * mls_int4_grouped_splits returns the split count this build uses for a shape (1: no
+ * split). */
+int mls_int4_grouped_splits(int64_t M_total, int E, int64_t N, int64_t K, int group);
+int mls_int4_grouped_gemm_partial(const void* a, int a_dt, int64_t lda, const int32_t* seg_off,
+                                  int E, int64_t M_total, const uint8_t* w, int64_t w_estride, int64_t ldw,
+                                  const void* s, int s_dt, int64_t s_estride, int64_t ld_sn, int64_t ld_sg,
+                                  int group, int splits, float* partial, int64_t ldp, int64_t split_stride,
+                                  int64_t N, int64_t K, mls_stream_t stream);
 
 /* Replaces _paged_attn_kernel + paged_attention_decode (kernels/paged_attention.py:33-118):
  * out[s][h][:] = softmax_j(scale * q[s][h] . K_j) V_j over the context_lens[s] tokens of

@@ -53,7 +53,8 @@ __device__ __forceinline__ void widen_int4x16(const uint4& q, uint32_t* o) {
 }  // namespace
 
 // STAB: the block's whole [128 x G] fp16 group-scale table is loaded once, coalesced,
-// into LDS (G <= 128, contiguous groups: at most 32 KiB). Otherwise each stage loads the
+// into LDS (G <= 128 and a multiple of 4, contiguous groups: at most 32 KiB).
+// Otherwise each stage loads the
 // scales of its 128 rows; those loads touch one cache line per row, many more L2
 // requests than the weights themselves. They are issued before the stage's LDS-direct
 // activation loads, so the end-of-stage wait, which must cover the LDS-direct loads,
@@ -95,12 +96,17 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   // spread over the XCDs by their own count (remapping over the whole grid would park
   // every surplus block on the last XCDs and leave them idle). Consecutive logical ids
   // share the row chunk and sit on one XCD.
+  // With a K split, item = (chunk, split, column tile): the splits of one chunk sit on
+  // one XCD next to its column tiles, sharing the chunk's activation rows in L2.
+  const int ksn = p.ksplit > 1 ? p.ksplit : 1;
   int chunks = 0;
   for (int e = 0; e < p.E; ++e) chunks += (p.seg_off[e + 1] - p.seg_off[e] + BMX - 1) / BMX;
-  const int items = chunks * p.n_tiles;
+  const int items = chunks * p.n_tiles * ksn;
   if ((int)blockIdx.x >= items) return;
   const int L = xcd_remap(blockIdx.x, items);
-  const int chunk = L / p.n_tiles, nt = L % p.n_tiles;
+  const int chunk = L / (p.n_tiles * ksn), rem = L % (p.n_tiles * ksn);
+  const int split = rem / p.n_tiles, nt = rem % p.n_tiles;
+  const int Kp = p.K / ksn, kbase = split * Kp;  // this block's K range
   int e = 0, cum = 0, lo = 0, hi = 0;
   for (; e < p.E; ++e) {
     lo = p.seg_off[e];
@@ -113,8 +119,8 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   const int rows = __builtin_amdgcn_readfirstlane(min(BMX, hi - m0));
   const int nsub = (rows + 15) >> 4;  // active 16-row subtiles
   constexpr int ssz = SCL == 0 ? 4 : 2;
-  const uint8_t* bmat = p.b + (int64_t)e * p.b_estride;
-  const uint8_t* smat = (const uint8_t*)p.s + (int64_t)e * p.s_estride * ssz;
+  const uint8_t* bmat = p.b + (int64_t)e * p.b_estride + kbase / 2;
+  const uint8_t* smat = (const uint8_t*)p.s + ((int64_t)e * p.s_estride + (int64_t)(kbase / p.group) * p.ld_sg) * ssz;
   const int n0 = nt * OUTN, N = p.N;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -123,15 +129,17 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   const int lr = lane & 15, lk = lane >> 4;
   if constexpr (GU) {
     // waves 2 and 3 stage B rows 64 .. 127: the up matrix
-    if (wave >= 2) bmat = p.b2 + (int64_t)e * p.b_estride;
+    if (wave >= 2) bmat = p.b2 + (int64_t)e * p.b_estride + kbase / 2;
   }
-  const uint8_t* smat_hi = GU ? (const uint8_t*)p.s2 + (int64_t)e * p.s_estride * ssz : smat;
+  const uint8_t* smat_hi =
+      GU ? (const uint8_t*)p.s2 + ((int64_t)e * p.s_estride + (int64_t)(kbase / p.group) * p.ld_sg) * ssz : smat;
 
   const int rows_b = __builtin_amdgcn_readfirstlane(min(OUTN, N - n0));
   const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const uint8_t*)p.a + (int64_t)m0 * p.lda * 2), (short)0, (int)(rows * p.lda * 2), 0x00020000);
+      (void*)((const uint8_t*)p.a + ((int64_t)m0 * p.lda + kbase) * 2), (short)0,
+      (int)(rows * p.lda * 2 - kbase * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(bmat + (int64_t)n0 * p.ldb), (short)0, (int)(rows_b * p.ldb), 0x00020000);
+      (void*)(bmat + (int64_t)n0 * p.ldb), (short)0, (int)(rows_b * p.ldb - kbase / 2), 0x00020000);
   // activation slot t = (wave * PW + i) * 64 + lane: row t / 8, logical chunk (t % 8) ^ (row & 7)
   int a_off[PW];
 #pragma unroll
@@ -184,7 +192,7 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   // per-stage scales (!STAB); threads past BN re-read a scale they never store
   auto load_s = [&](int k0, float& s0, float& s1) __attribute__((always_inline)) {
     if constexpr (!STAB) {
-      const int kc = min(k0, p.K - BK);  // a stage past the end reuses the last scales
+      const int kc = min(k0, Kp - BK);  // a stage past the end reuses the last scales
       using ST = std::conditional_t<SCL == 1, _Float16, float>;
       const ST* sp = reinterpret_cast<const ST*>(s_mat) + s_row;
       s0 = (float)sp[(int64_t)(kc / p.group) * p.ld_sg] * 0.0625f;
@@ -216,19 +224,19 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
       accg[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-  const int nk = p.K / BK;
+  const int nk = Kp / BK;
   if constexpr (STAB) {
     // scale table: row n0 + r holds G fp16 scales; 16-byte piece c = tid + 256 i is
     // row c / (G / 8), groups 8 (c % (G / 8)) .. + 7, written transposed to sT[g][r]
-    const int G = p.K / p.group, ppr = G / 8;
+    const int G = Kp / p.group, ppr = G / 4;
     for (int c = tid; c < BN * ppr; c += 256) {
       const int r = c / ppr, part = c % ppr;
       const int64_t n = min(n0 + (GU ? (r & 63) : r), N - 1);
       const uint8_t* sm = (GU && r >= 64) ? smat_hi : smat;
-      const uint4 v = *reinterpret_cast<const uint4*>((const _Float16*)sm + n * p.ld_sn + part * 8);
+      const uint2 v = *reinterpret_cast<const uint2*>((const _Float16*)sm + n * p.ld_sn + part * 4);
       const _Float16* h = reinterpret_cast<const _Float16*>(&v);
 #pragma unroll
-      for (int t = 0; t < 8; ++t) sT[(part * 8 + t) * BN + r] = h[t];
+      for (int t = 0; t < 4; ++t) sT[(part * 4 + t) * BN + r] = h[t];
     }
   }
 
@@ -343,7 +351,7 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue: acc[i][j][r] = C[m = m0 + (2 j + wm) 16 + lr][n = n0 + 64 wn + 16 i + 4 lk + r]
-  OT* c = static_cast<OT*>(p.c);
+  OT* c = static_cast<OT*>(p.c) + (int64_t)split * p.c_sstride;
   if constexpr (GU) {
     // wavefronts wn = 1 hold the up products: they pass them through LDS (the
     // activation buffers, free now) to the wavefronts wn = 0, which hold the gate
@@ -410,14 +418,14 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   }
 }
 
-template <typename MT, int TMX, int SCL, bool GU>
+template <typename MT, int TMX, int SCL, bool GU, typename OT = MT>
 static int launch_grouped(Mfma16Params p, hipStream_t st) {
   constexpr int BMX = 32 * TMX, OUTN = GU ? 64 : 128;
   p.n_tiles = (int)cdiv(p.N, OUTN);
   // upper bound on sum_e ceil(rows_e / BMX) without reading the device offsets
   p.m_tiles = (int)(cdiv(p.M, BMX) + p.E);
-  auto kern = grouped_int4_kernel<MT, MT, TMX, SCL, GU>;
-  const int64_t blocks = (int64_t)p.n_tiles * p.m_tiles;
+  auto kern = grouped_int4_kernel<MT, OT, TMX, SCL, GU>;
+  const int64_t blocks = (int64_t)p.n_tiles * p.m_tiles * (p.ksplit > 1 ? p.ksplit : 1);
   if (blocks > 0x7FFFFFFF) return MLS_ERR_UNSUPPORTED;
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, st, p);
   return check_launch(GU ? "grouped INT4 gate/up GEMM" : "grouped INT4 GEMM");
@@ -439,16 +447,69 @@ static int launch_grouped_tmx(const Mfma16Params& p, hipStream_t st, bool bf16, 
 // Row-chunk height: the smallest of 64 / 96 / 128 / 160 rows that holds 1.25x the
 // average segment (routed segments scatter around the average), so a typical expert's
 // rows fit in one chunk and its weights are streamed and widened once.
-int launch_grouped_seg(const Mfma16Params& p, hipStream_t st, bool bf16, bool gate_up) {
-  const int64_t want = cdiv(p.M * 5, p.E * 4);
-  // MLS_GROUPED_TMX (2..5) overrides the chunk height (32 TMX rows) for sweeps
+// MLS_GROUPED_TMX (2..5) overrides the chunk height (32 TMX rows) for sweeps.
+static int chunk_tmx(int64_t M, int E) {
+  const int64_t want = cdiv(M * 5, (int64_t)E * 4);
   static const int tmx_env = env_int("MLS_GROUPED_TMX", 0);
-  int tmx = tmx_env >= 2 && tmx_env <= 5 ? tmx_env : want > 128 ? 5 : want > 96 ? 4 : want > 64 ? 3 : 2;
-  // scale table in LDS: fp16 scales, contiguous groups, G a multiple of 8 up to 128,
-  // 16-byte aligned rows; a table of up to 32 groups keeps two blocks per CU
+  return tmx_env >= 2 && tmx_env <= 5 ? tmx_env : want > 128 ? 5 : want > 96 ? 4 : want > 64 ? 3 : 2;
+}
+
+int grouped_splits(int64_t M, int E, int64_t N, int64_t K, int group) {
+  // MLS_GROUPED_SPLITS (1, 2, 4, 8) forces the split count for sweeps
+  static const int env = env_int("MLS_GROUPED_SPLITS", 0);
+  if (M <= 0 || E <= 0 || N <= 0 || K <= 0 || group <= 0) return 1;
+  const int64_t tiles = cdiv(N, 128) * (cdiv(M, 32 * chunk_tmx(M, E)) + E / 2);
+  int best = 1;
+  for (int s = 1; s <= 8; s *= 2) {
+    const int64_t kp = K / s;
+    // each range: a multiple of 64 and of the group, its scales in the 32-group table
+    const bool ok = K % s == 0 && kp % 64 == 0 && kp % group == 0 && kp / group <= 32 && (kp / group) % 4 == 0;
+    if (env > 0) {
+      if (s == env) return ok ? s : 1;
+      continue;
+    }
+    if (ok) {
+      best = s;
+      if (tiles * s >= 512) break;  // two blocks per CU reached
+    }
+  }
+  return env > 0 ? 1 : best;
+}
+
+template <int SCL>
+static int launch_partial_tmx(const Mfma16Params& p, hipStream_t st, bool bf16, int tmx) {
+  switch (tmx) {
+    case 5:
+      if constexpr (SCL >= 32)
+        return bf16 ? launch_grouped<__bf16, 5, SCL, false, float>(p, st)
+                    : launch_grouped<_Float16, 5, SCL, false, float>(p, st);
+      [[fallthrough]];  // per-stage scales: 160-row chunks are not built (they would spill)
+    case 4: return bf16 ? launch_grouped<__bf16, 4, SCL, false, float>(p, st) : launch_grouped<_Float16, 4, SCL, false, float>(p, st);
+    case 3: return bf16 ? launch_grouped<__bf16, 3, SCL, false, float>(p, st) : launch_grouped<_Float16, 3, SCL, false, float>(p, st);
+    default: return bf16 ? launch_grouped<__bf16, 2, SCL, false, float>(p, st) : launch_grouped<_Float16, 2, SCL, false, float>(p, st);
+  }
+}
+
+int launch_grouped_partial(const Mfma16Params& p, hipStream_t st, bool bf16) {
+  const int s = p.ksplit;
+  if (s < 1 || p.K % s != 0) return MLS_ERR_UNSUPPORTED;
+  const int64_t kp = p.K / s, G = kp / p.group;
+  if (kp % 64 != 0 || kp % p.group != 0) return MLS_ERR_UNSUPPORTED;
+  const int tmx = chunk_tmx(p.M, p.E);
+  const bool stab = p.s_dt == MLS_F16 && p.ld_sg == 1 && G % 4 == 0 && G <= 32 && (p.ld_sn % 4) == 0 &&
+                    (p.s_estride % 4) == 0 && aligned(p.s, 8);
+  if (stab) return launch_partial_tmx<32>(p, st, bf16, tmx);
+  if (p.s_dt == MLS_F16) return launch_partial_tmx<1>(p, st, bf16, tmx);
+  return launch_partial_tmx<0>(p, st, bf16, tmx);
+}
+
+int launch_grouped_seg(const Mfma16Params& p, hipStream_t st, bool bf16, bool gate_up) {
+  const int tmx = chunk_tmx(p.M, p.E);
+  // scale table in LDS: fp16 scales, contiguous groups, G a multiple of 4 up to 128,
+  // 8-byte aligned rows; a table of up to 32 groups keeps two blocks per CU
   const int64_t G = p.K / p.group;
-  const bool stab = p.s_dt == MLS_F16 && p.ld_sg == 1 && G % 8 == 0 && G <= 128 && (p.ld_sn % 8) == 0 &&
-                    (p.s_estride % 8) == 0 && aligned(p.s, 16) && (!gate_up || aligned(p.s2, 16));
+  const bool stab = p.s_dt == MLS_F16 && p.ld_sg == 1 && G % 4 == 0 && G <= 128 && (p.ld_sn % 4) == 0 &&
+                    (p.s_estride % 4) == 0 && aligned(p.s, 8) && (!gate_up || aligned(p.s2, 8));
   if (!stab && p.s_dt == MLS_F16)
     return gate_up ? launch_grouped_tmx<1, true>(p, st, bf16, tmx) : launch_grouped_tmx<1, false>(p, st, bf16, tmx);
   if (!stab)

@@ -737,6 +737,21 @@ int launch_grouped_gate_up(const GroupedArgs& g, const uint8_t* wu, const void* 
   return launch_grouped_seg(p, w.stream, w.a_dt == MLS_BF16, true);
 }
 
+int launch_grouped_int4_partial(const GroupedArgs& g, int splits, float* partial, int64_t ldp, int64_t sstride) {
+  const WqArgs& w = g.base;
+  if (w.a_dt != MLS_F16 && w.a_dt != MLS_BF16) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(w.a, 16) || w.lda % 8 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(w.w, 16) || w.ldw % 16 != 0 || g.w_estride % 16 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(partial, 16) || !tile_fits(w.lda * 2, w.ldw)) return MLS_ERR_UNSUPPORTED;
+  Mfma16Params p{};
+  p.a = w.a; p.lda = w.lda; p.b = w.w; p.ldb = w.ldw;
+  p.s = w.s; p.s_dt = w.s_dt; p.ld_sn = w.ld_sn; p.ld_sg = w.ld_sg; p.group = w.group;
+  p.c = partial; p.ldc = ldp; p.M = (int)w.M; p.N = (int)w.N; p.K = (int)w.K;
+  p.seg_off = g.seg_off; p.E = g.E; p.b_estride = g.w_estride; p.s_estride = g.s_estride;
+  p.ksplit = splits; p.c_sstride = sstride;
+  return launch_grouped_partial(p, w.stream, w.a_dt == MLS_BF16);
+}
+
 int launch_fp8_exact(const Fp8Args& f) {
   if (f.K % 64 != 0 || f.M < 16 || f.N < 16) return MLS_ERR_UNSUPPORTED;
   if (!aligned(f.a, 16) || !aligned(f.b, 16) || f.lda % 16 != 0 || f.ldb % 16 != 0)

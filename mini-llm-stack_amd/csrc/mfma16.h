@@ -32,6 +32,8 @@ struct Mfma16Params {
   int64_t b_estride, s_estride;  // grouped: bytes / scale elements between experts
   const uint8_t* b2;              // grouped gate/up: the up matrix (b is the gate)
   const void* s2;
+  int ksplit;                     // grouped: K split into this many partial products (0, 1: none)
+  int64_t c_sstride;              // grouped split: elements between the partial outputs
 };
 
 template <typename T> struct Mfma16;
@@ -151,5 +153,12 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds,
 // gate_up: the gate/up pair of a SwiGLU expert MLP (p.b/p.s gate, p.b2/p.s2 up), output
 // silu(gate) * up.
 int launch_grouped_seg(const Mfma16Params& p, hipStream_t st, bool bf16, bool gate_up);
+// The same GEMM as ksplit fp32 partial products over equal K ranges (p.c is fp32,
+// partial s at p.c + s * p.c_sstride). MLS_ERR_UNSUPPORTED unless each range is a
+// multiple of 64 and of the group and its scales fit the 32-group LDS table.
+int launch_grouped_partial(const Mfma16Params& p, hipStream_t st, bool bf16);
+// K splits that give the down projection of an expert MLP (few column tiles) two
+// blocks per CU; 1 when no split is needed or possible.
+int grouped_splits(int64_t M, int E, int64_t N, int64_t K, int group);
 
 }  // namespace mls

@@ -49,6 +49,11 @@ int launch_grouped_int4(const GroupedArgs& p);
 // are the gate matrices, wu / su the up matrices (same strides); base.c receives
 // silu(a Wg^T) * (a Wu^T).
 int launch_grouped_gate_up(const GroupedArgs& p, const uint8_t* wu, const void* su);
+// `splits` fp32 partial products over equal K ranges: partial + s * sstride holds
+// a[rows] . dequant(w)[:, K range s]^T, [M_total][ldp].
+int launch_grouped_int4_partial(const GroupedArgs& p, int splits, float* partial, int64_t ldp, int64_t sstride);
+// K splits that give a grouped GEMM with few column tiles two blocks per CU (1: none).
+int grouped_splits(int64_t M, int E, int64_t N, int64_t K, int group);
 
 // e4m3 x e4m3 GEMM arguments (scales: pointer with a row stride, or the scalar).
 struct Fp8Args {

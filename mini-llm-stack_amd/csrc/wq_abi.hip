@@ -123,3 +123,33 @@ extern "C" int mls_int4_grouped_gate_up(const void* a, int a_dt, int64_t lda, co
                 "%s: needs K %% 64 == 0, group %% 32 == 0 and 16-byte aligned rows", fn);
   return rc;
 }
+
+extern "C" int mls_int4_grouped_splits(int64_t M_total, int E, int64_t N, int64_t K, int group) {
+  return grouped_splits(M_total, E, N, K, group);
+}
+
+extern "C" int mls_int4_grouped_gemm_partial(const void* a, int a_dt, int64_t lda, const int32_t* seg_off,
+                                             int E, int64_t M_total, const uint8_t* w, int64_t w_estride,
+                                             int64_t ldw, const void* s, int s_dt, int64_t s_estride,
+                                             int64_t ld_sn, int64_t ld_sg, int group, int splits, float* partial,
+                                             int64_t ldp, int64_t split_stride, int64_t N, int64_t K,
+                                             mls_stream_t stream) {
+  const char* fn = "mls_int4_grouped_gemm_partial";
+  GroupedArgs g{{a, a_dt, lda, w, ldw, s, s_dt, ld_sn, ld_sg, group, partial, ldp, M_total, N, K,
+                 (hipStream_t)stream},
+                seg_off, E, w_estride, s_estride};
+  int rc = validate(fn, 4, g.base, a_dt);
+  if (rc != MLS_OK) return rc;
+  if (E < 1) return fail(MLS_ERR_ARG, "%s: E=%d < 1", fn, E);
+  if (splits < 1 || splits > 64) return fail(MLS_ERR_ARG, "%s: splits=%d", fn, splits);
+  if (w_estride < 0 || s_estride < 0 || split_stride < M_total * ldp)
+    return fail(MLS_ERR_ARG, "%s: bad expert or split stride", fn);
+  if (M_total == 0 || N == 0) return MLS_OK;
+  if (!seg_off) return fail(MLS_ERR_ARG, "%s: null seg_off", fn);
+  rc = launch_grouped_int4_partial(g, splits, partial, ldp, split_stride);
+  if (rc == MLS_ERR_UNSUPPORTED)
+    return fail(MLS_ERR_UNSUPPORTED,
+                "%s: needs 16-bit activations, K / splits a multiple of 64 and of the group, 16-byte aligned "
+                "rows", fn);
+  return rc;
+}

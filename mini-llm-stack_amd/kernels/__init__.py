@@ -18,7 +18,7 @@ from pathlib import Path
 # This implementation only ever runs compiled gfx950 code.
 INTERPRETER = False
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 LIB_PATH = Path(os.environ.get("MLS_LIB") or
                 Path(__file__).resolve().parent.parent / "libmls_hip.so")
 
@@ -52,7 +52,10 @@ SIGNATURES = {
                                _I64, _I64, _I, _P, _I, _I64, _I64, _I64, _P], _I),
     "mls_int4_grouped_gate_up": ([_P, _I, _I64, _P, _I, _I64, _P, _P, _I64, _I64, _P, _P, _I,
                                   _I64, _I64, _I64, _I, _P, _I, _I64, _I64, _I64, _P], _I),
-    "mls_moe_combine": ([_P, _I, _I64, _I64, _P, _I, _P, _I64, _I, _P, _I64, _I64, _P], _I),
+    "mls_moe_combine": ([_P, _I, _I64, _I64, _I, _I64, _P, _I, _P, _I64, _I, _P, _I, _I64, _I64, _P], _I),
+    "mls_int4_grouped_splits": ([_I64, _I, _I64, _I64, _I], _I),
+    "mls_int4_grouped_gemm_partial": ([_P, _I, _I64, _P, _I, _I64, _P, _I64, _I64, _P, _I, _I64, _I64, _I64,
+                                       _I, _I, _P, _I64, _I64, _I64, _I64, _P], _I),
     "mls_paged_attention_workspace": ([_I64, _I64, _I64, _I64], _I64),
     "mls_paged_attention_decode": ([_P, _I, _I64, _I64, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _I64,
                                     _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I64, _P], _I),

@@ -111,3 +111,54 @@ def int4_expert_mlp(a_sorted: torch.Tensor, counts_or_offsets: torch.Tensor,
     off = _offsets(counts_or_offsets, E, "int4_expert_mlp")
     h = int4_grouped_gate_up(a_sorted, wg, sg, wu, su, off, group_size)
     return int4_grouped_matmul(h, wd, sd, off, group_size)
+
+
+def grouped_splits(M_total: int, E: int, N: int, K: int, group_size: int) -> int:
+    """K splits the partial-product down projection uses for this shape (1: none)."""
+    return int(kernels.lib().mls_int4_grouped_splits(M_total, E, N, K, group_size))
+
+
+def int4_grouped_matmul_partial(a_sorted: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor,
+                                counts_or_offsets: torch.Tensor, group_size: int, splits: int) -> torch.Tensor:
+    """int4_grouped_matmul as `splits` fp32 partial products over equal K ranges:
+    [splits, M_total, N], whose sum over the first axis is the product (the reduction is
+    left to the consumer, e.g. kernels.moe_routing.combine_partials)."""
+    dev = require_hip("int4_grouped_matmul_partial", a_sorted, w_packed, scale, counts_or_offsets)
+    E, N, Kh = w_packed.shape
+    M, K = a_sorted.shape
+    assert K % group_size == 0 and K == Kh * 2
+    G = K // group_size
+    off = _offsets(counts_or_offsets, E, "int4_grouped_matmul_partial")
+    adt = dt_code(a_sorted.dtype, "int4_grouped_matmul_partial")
+    a = rows(a_sorted)
+    w = w_packed if w_packed.is_contiguous() else w_packed.contiguous()
+    if scale.dtype not in (torch.float32, torch.float16):
+        scale = scale.to(torch.float32)
+    sc = scale if scale.is_contiguous() else scale.contiguous()
+    part = torch.empty(splits, M, N, dtype=torch.float32, device=dev)
+    kernels.check(kernels.lib().mls_int4_grouped_gemm_partial(
+        a.data_ptr(), adt, ld(a), off.data_ptr(), E, M, w.data_ptr(), N * Kh, Kh, sc.data_ptr(),
+        dt_code(sc.dtype, "int4_grouped_matmul_partial scale"), N * G, G, 1, group_size, splits,
+        part.data_ptr(), N, M * N, N, K, stream(dev)), "int4_grouped_matmul_partial")
+    return part
+
+
+def int4_expert_mlp_combine(a_sorted: torch.Tensor, counts_or_offsets: torch.Tensor,
+                            wg: torch.Tensor, sg: torch.Tensor, wu: torch.Tensor, su: torch.Tensor,
+                            wd: torch.Tensor, sd: torch.Tensor, group_size: int,
+                            weights: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+    """The routed MoE layer after dispatch: the INT4 SwiGLU expert MLP of every segment
+    (int4_expert_mlp) and the router-weighted combine back to token order
+    (kernels/moe_routing.py:145-153). When the down projection's output is narrow (few
+    column tiles), it runs as fp32 partial products over K splits that the combine adds,
+    so that it still fills the GPU. Returns [T, D] in a_sorted's dtype."""
+    from kernels.moe_routing import combine_partials, combine_rows
+    E = wg.shape[0]
+    off = _offsets(counts_or_offsets, E, "int4_expert_mlp_combine")
+    h = int4_grouped_gate_up(a_sorted, wg, sg, wu, su, off, group_size)
+    D, H = wd.shape[1], wd.shape[2] * 2
+    splits = grouped_splits(h.shape[0], E, D, H, group_size)
+    if splits > 1:
+        part = int4_grouped_matmul_partial(h, wd, sd, off, group_size, splits)
+        return combine_partials(part, weights, pos, a_sorted.dtype)
+    return combine_rows(int4_grouped_matmul(h, wd, sd, off, group_size), weights, pos)

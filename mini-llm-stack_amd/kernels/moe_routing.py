@@ -9,11 +9,12 @@ GEMM (kernels.moe_grouped). Same conventions as the reference:
 
 - combine_rows: out[t] = sum_k w[t, k] * expert_out[pos[t, k]], one gfx950 block per
   output row, no atomics (kernels/moe_routing.py:52-76, 100-113);
+- combine_partials: the same over the fp32 partial products of a K-split expert GEMM;
 - moe_dispatch_combine: the routed MoE forward (kernels/moe_routing.py:133-153). When
   the experts are SwiGLU MLPs whose projections are INT4 QuantLinear with stacked
   buffers (serve.quantize.quantize_model stacks them), the per-expert loop becomes two
-  grouped launches (kernels.moe_grouped.int4_expert_mlp); otherwise each expert module
-  runs on its segment as in the reference.
+  grouped launches and the combine (kernels.moe_grouped.int4_expert_mlp_combine);
+  otherwise each expert module runs on its segment as in the reference.
 
 sort and gather are index bookkeeping on the device (torch ops).
 """
@@ -60,8 +61,27 @@ def combine_rows(expert_out: torch.Tensor, weights: torch.Tensor, pos: torch.Ten
     p = pos.to(torch.int64).contiguous()
     out = torch.empty(T, D, dtype=x.dtype, device=dev)
     kernels.check(kernels.lib().mls_moe_combine(
-        x.data_ptr(), dt_code(x.dtype, "combine_rows"), ld(x), x.shape[0], w.data_ptr(), dt_code(w.dtype, "combine_rows weights"),
-        p.data_ptr(), T, K, out.data_ptr(), ld(out), D, stream(dev)), "combine_rows")
+        x.data_ptr(), dt_code(x.dtype, "combine_rows"), ld(x), x.shape[0], 1, 0, w.data_ptr(),
+        dt_code(w.dtype, "combine_rows weights"), p.data_ptr(), T, K, out.data_ptr(), dt_code(out.dtype, "combine_rows"),
+        ld(out), D, stream(dev)), "combine_rows")
+    return out
+
+
+def combine_partials(partials: torch.Tensor, weights: torch.Tensor, pos: torch.Tensor,
+                     out_dtype: torch.dtype) -> torch.Tensor:
+    """combine_rows over the fp32 partial products [splits, rows, D] of a K-split expert
+    GEMM: out[t] = sum_k weights[t, k] * sum_p partials[p, pos[t, k]], in out_dtype."""
+    dev = require_hip("combine_partials", partials, weights, pos)
+    S, R, D = partials.shape
+    T, K = pos.shape
+    x = partials.contiguous()
+    w = weights.contiguous()
+    p = pos.to(torch.int64).contiguous()
+    out = torch.empty(T, D, dtype=out_dtype, device=dev)
+    kernels.check(kernels.lib().mls_moe_combine(
+        x.data_ptr(), dt_code(x.dtype, "combine_partials"), D, R, S, R * D, w.data_ptr(),
+        dt_code(w.dtype, "combine_partials weights"), p.data_ptr(), T, K, out.data_ptr(),
+        dt_code(out_dtype, "combine_partials"), ld(out), D, stream(dev)), "combine_partials")
     return out
 
 
@@ -70,7 +90,7 @@ def moe_dispatch_combine(flat: torch.Tensor, weights: torch.Tensor, experts_idx:
     """Routed MoE forward (kernels/moe_routing.py:133-153): sort the (token, slot)
     assignments by expert, gather the rows, run every expert on its contiguous segment,
     combine weighted by the router. flat [T, D], weights [T, k], experts_idx [T, k]."""
-    from kernels.moe_grouped import int4_expert_mlp, segment_offsets
+    from kernels.moe_grouped import int4_expert_mlp_combine, segment_offsets
     from serve.quantize import stacked_int4_experts
 
     n_experts = len(expert_modules)
@@ -78,14 +98,13 @@ def moe_dispatch_combine(flat: torch.Tensor, weights: torch.Tensor, experts_idx:
     dispatched = gather_rows(flat, token_of_slot)
     st = stacked_int4_experts(expert_modules)
     if st is not None and dispatched.dtype in (torch.bfloat16, torch.float16):
-        expert_out = int4_expert_mlp(dispatched, segment_offsets(counts), st["w_gate"][0], st["w_gate"][1],
-                                     st["w_up"][0], st["w_up"][1], st["w_down"][0], st["w_down"][1],
-                                     st["group_size"])
-    else:
-        expert_out = torch.empty_like(dispatched)
-        start = 0
-        for e, cnt in enumerate(counts.tolist()):
-            if cnt:
-                expert_out[start:start + cnt] = expert_modules[e](dispatched[start:start + cnt])
-            start += cnt
+        return int4_expert_mlp_combine(dispatched, segment_offsets(counts), st["w_gate"][0], st["w_gate"][1],
+                                       st["w_up"][0], st["w_up"][1], st["w_down"][0], st["w_down"][1],
+                                       st["group_size"], weights, pos)
+    expert_out = torch.empty_like(dispatched)
+    start = 0
+    for e, cnt in enumerate(counts.tolist()):
+        if cnt:
+            expert_out[start:start + cnt] = expert_modules[e](dispatched[start:start + cnt])
+        start += cnt
     return combine_rows(expert_out, weights, pos)

@@ -24,7 +24,7 @@ def declared_symbols() -> list[str]:
 
 def test_header_declares_the_boundary():
     syms = declared_symbols()
-    assert len(syms) == len(set(syms)) == 18
+    assert len(syms) == len(set(syms)) == 20
     assert set(syms) == set(kernels.SIGNATURES)
 
 
@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = kernels.load_library()
-    assert lib.mls_abi_version() == kernels.ABI_VERSION == 4
+    assert lib.mls_abi_version() == kernels.ABI_VERSION == 5
     assert isinstance(lib.mls_last_error(), bytes)
 
 
@@ -122,11 +122,16 @@ def test_gate_up_and_combine_reject():
     # empty problems are no-ops
     assert L.mls_int4_grouped_gate_up(NULL, bf, 64, NULL, 2, 0, NULL, NULL, 0, 32, NULL, NULL, 0, 2, 1, 1,
                                       32, NULL, bf, 16, 16, 64, NULL) == 0
-    # combine: k < 1, ldo < D, null pos, empty
-    assert L.mls_moe_combine(1, bf, 8, 4, 1, bf, 1, 2, 0, 1, 8, 8, NULL) == kernels.MLS_ERR_ARG
-    assert L.mls_moe_combine(1, bf, 8, 4, 1, bf, 1, 2, 2, 1, 4, 8, NULL) == kernels.MLS_ERR_ARG
-    assert L.mls_moe_combine(1, bf, 8, 4, 1, bf, NULL, 2, 2, 1, 8, 8, NULL) == kernels.MLS_ERR_ARG
-    assert L.mls_moe_combine(NULL, bf, 8, 0, NULL, bf, NULL, 0, 2, NULL, 8, 8, NULL) == 0
+    # combine: k < 1, ldo < D, null pos, splits < 1, overlapping splits, empty
+    assert L.mls_moe_combine(1, bf, 8, 4, 1, 0, 1, bf, 1, 2, 0, 1, bf, 8, 8, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_moe_combine(1, bf, 8, 4, 1, 0, 1, bf, 1, 2, 2, 1, bf, 4, 8, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_moe_combine(1, bf, 8, 4, 1, 0, 1, bf, NULL, 2, 2, 1, bf, 8, 8, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_moe_combine(1, bf, 8, 4, 0, 0, 1, bf, 1, 2, 2, 1, bf, 8, 8, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_moe_combine(1, bf, 8, 4, 2, 16, 1, bf, 1, 2, 2, 1, bf, 8, 8, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_moe_combine(NULL, bf, 8, 0, 1, 0, NULL, bf, NULL, 0, 2, NULL, bf, 8, 8, NULL) == 0
+    # split count: the down projection of config E's expert MLP splits K in 4; a wide output does not
+    assert L.mls_int4_grouped_splits(1024, 8, 4096, 14336, 128) == 4
+    assert L.mls_int4_grouped_splits(1024, 8, 14336, 4096, 128) == 1
 
 
 def test_fp8_train_entry_points_reject():

@@ -18,8 +18,9 @@ import torch.nn.functional as F
 
 from oracle import ref
 
-from kernels.moe_grouped import int4_expert_mlp, int4_grouped_gate_up
-from kernels.moe_routing import combine_rows, moe_dispatch_combine, sort_by_expert
+from kernels.moe_grouped import (grouped_splits, int4_expert_mlp, int4_expert_mlp_combine,
+                                 int4_grouped_gate_up, int4_grouped_matmul_partial)
+from kernels.moe_routing import combine_partials, combine_rows, moe_dispatch_combine, sort_by_expert
 from serve.quantize import QuantLinear, quantize_int4, quantize_model, stacked_int4_experts
 
 pytestmark = pytest.mark.gpu
@@ -245,3 +246,68 @@ def test_quantize_model_stacks_moe_experts(dev):
     st = experts[0].__dict__.get("_int4_stack")
     assert st is not None and st["w_up"][0].shape == (2, 128, 32)
     assert quantize_model(m, bits=8).blocks[1].mlp.experts[0].__dict__.get("_int4_stack") is None
+
+
+@pytest.mark.parametrize("splits,gs,sdt", [(2, 128, torch.float16), (4, 64, torch.float16),
+                                          (4, 128, torch.float32), (8, 32, torch.float16)])
+def test_partial_products(dev, splits, gs, sdt):
+    """The K-split down projection: partial p is the product over K range p (fp32
+    output, so within the fp32 tolerance of the oracle's), and they sum to the whole."""
+    counts = [40, 0, 3, 129, 64, 1, 0, 19]
+    E, N, K = len(counts), 256, 2048
+    W, S = _int4(dev, E, N, K, gs, 31 + splits, sdt)
+    M = sum(counts)
+    a = torch.randn(M, K, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    part = int4_grouped_matmul_partial(a.to(dev), W, S, torch.tensor(counts, device=dev), gs, splits)
+    assert part.shape == (splits, M, N) and part.dtype == torch.float32
+    off = np.concatenate([[0], np.cumsum(counts)])
+    kp = K // splits
+    an, wn, sn = a.float().numpy(), W.cpu().numpy(), S.float().cpu().numpy()
+    total = np.zeros((M, N))
+    for p_ in range(splits):
+        want = ref.grouped_int4_matmul(an[:, p_ * kp:(p_ + 1) * kp], wn[:, :, p_ * kp // 2:(p_ + 1) * kp // 2],
+                                       sn[:, :, p_ * kp // gs:(p_ + 1) * kp // gs], off, gs)
+        ok, worst = ref.close_fp32(part[p_].cpu().numpy(), want)
+        assert ok, f"partial {p_}: worst {worst:.3g}"
+        total += want
+    ok, worst = ref.close_fp32(part.sum(0).cpu().numpy(), total)
+    assert ok, worst
+
+
+def test_combine_partials(dev):
+    g = torch.Generator().manual_seed(3)
+    T, K, D, S = 50, 2, 96, 4
+    part = torch.randn(S, T * K, D, generator=g)
+    w = torch.rand(T, K, generator=g)
+    pos = torch.randperm(T * K, generator=g).reshape(T, K)
+    out = combine_partials(part.to(dev), w.to(dev), pos.to(dev), torch.bfloat16)
+    assert out.dtype == torch.bfloat16
+    want = ref.combine_rows(part.sum(0).numpy(), w.numpy(), pos.numpy())
+    ok, worst = ref.close_bf16(out.float().cpu().numpy(), want)
+    assert ok, worst
+
+
+@pytest.mark.parametrize("sdt", [torch.float16, torch.float32])
+def test_expert_mlp_combine_with_split(dev, sdt):
+    """A narrow down projection (D = 512) takes the K-split path; the combined layer
+    output equals the oracle's expert MLP + combine."""
+    T, E, k, D, H, gs = 512, 8, 2, 512, 2048, 64
+    assert grouped_splits(T * k, E, D, H, gs) > 1
+    WG, SG = _int4(dev, E, H, D, gs, 41, sdt)
+    WU, SU = _int4(dev, E, H, D, gs, 42, sdt)
+    WD, SD = _int4(dev, E, D, H, gs, 43, sdt)
+    w, idx = _route(dev, T, E, k, 44)
+    tok, counts, pos = sort_by_expert(idx, E)
+    x = torch.randn(T, D, generator=torch.Generator().manual_seed(45)).to(torch.bfloat16)
+    a = x.to(dev)[tok]
+    out = int4_expert_mlp_combine(a, counts, WG, SG, WU, SU, WD, SD, gs, w, pos)
+    assert out.shape == (T, D) and out.dtype == torch.bfloat16
+    off = np.concatenate([[0], np.cumsum(counts.cpu().numpy())])
+    # the hidden activation is a bf16 tensor, as in the reference (w_gate(x) etc. on bf16)
+    h = ref.grouped_int4_gate_up(a.float().cpu().numpy(), WG.cpu().numpy(), SG.float().cpu().numpy(),
+                                 WU.cpu().numpy(), SU.float().cpu().numpy(), off, gs)
+    h = torch.from_numpy(h).to(torch.bfloat16).float().numpy()
+    y = ref.grouped_int4_matmul(h, WD.cpu().numpy(), SD.float().cpu().numpy(), off, gs)
+    want = ref.combine_rows(y, w.cpu().numpy(), pos.cpu().numpy())
+    ok, worst = ref.close_bf16(out.float().cpu().numpy(), want)
+    assert ok, worst
