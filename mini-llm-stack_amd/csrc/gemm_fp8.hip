@@ -310,11 +310,16 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void fp8_gemm_dma_kernel(
 #pragma unroll
     for (int i = 0; i < TN; ++i) bop[i] = operand(bs, wn0 + i * 16 + lr);
     aop[0] = operand(as, wm0 + lr);
+    // the scheduler would sink each A read to just before its MFMAs; the group barriers
+    // keep A operand j + 1's reads ahead of MFMA group j
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * (TN + 1), 0);
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
       if (j + 1 < TM) aop[(j + 1) & 1] = operand(as, wm0 + (j + 1) * 16 + lr);
 #pragma unroll
       for (int i = 0; i < TN; ++i) acc[i][j] = mfma_fp8<FA>(bop[i], aop[j & 1], acc[i][j]);
+      if (j + 1 < TM) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, TN, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
