@@ -15,7 +15,8 @@ FP8 e4m3 GEMM, INT4 MoE grouped GEMM) and the whole INT4 SwiGLU expert MLP of a
 routed MoE layer (gate/up, down, combine), FP8Linear's backward at config D's shape
 (e5m2 gradients), paged-attention decode over a bf16 KV cache and the load-time INT4
 quantizer are reported under "extra" with the same protocol, followed by a 256 MiB streaming copy (the bandwidth a plain elementwise
-kernel reaches on this GPU). cpu_baseline times the reference's CPU algorithm (the numpy
+kernel reaches on this GPU) and, as calibration only, the vendor library's GEMMs on config
+D's shape (hipBLASLt through torch: fp8 with per-row and per-tensor scales, bf16). cpu_baseline times the reference's CPU algorithm (the numpy
 restatement in oracle/: dequantize, then fp32 matmul) on the host for a bounded
 sample of the headline workload.
 """
@@ -306,6 +307,45 @@ def copy_calibration(dev, steps: int, warmup: int, nbytes: int = 256 << 20):
     return dict(ms=ms, bytes=2 * nbytes, flops=0, copies=copies)
 
 
+def vendor_gemm(dev, steps: int, warmup: int, kind: str, M=4096, N=8192, K=8192):
+    """Calibration only, never the product path: the vendor library (hipBLASLt, through
+    torch) on config D's shape, timed with the same protocol, so the fp8 rows can be read
+    against what the platform's own GEMM reaches on the same GPU. kind: "fp8_rowwise"
+    (torch._scaled_mm with per-row scales, config D's form), "fp8_tensorwise", or
+    "bf16" (torch.matmul). Returns None when the library path is unavailable."""
+    import torch
+    g = torch.Generator(device=dev).manual_seed(5)
+    try:
+        if kind == "bf16":
+            a = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+            b = torch.randn(N, K, generator=g, device=dev).to(torch.bfloat16).t().contiguous().t()
+            fns = [lambda: torch.matmul(a, b.t())]
+        else:
+            a = torch.randn(M, K, generator=g, device=dev).to(torch.float8_e4m3fn)
+            b = torch.randn(N, K, generator=g, device=dev).to(torch.float8_e4m3fn)
+            if kind == "fp8_rowwise":
+                sa, sb = torch.rand(M, 1, device=dev) + 0.5, torch.rand(1, N, device=dev) + 0.5
+            else:
+                sa, sb = torch.tensor(0.7, device=dev), torch.tensor(1.3, device=dev)
+            fns = [lambda: torch._scaled_mm(a, b.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)]
+        fns[0]()
+        torch.cuda.synchronize()
+    except Exception as ex:  # not every torch build routes these to the GPU library
+        log(f"vendor {kind}: unavailable ({type(ex).__name__}: {str(ex)[:120]})")
+        return None
+    # eager launches (a 0.2 ms GEMM hides the launch cost; no library call under capture)
+    for _ in range(warmup):
+        fns[0]()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
+        fns[0]()
+    end.record()
+    torch.cuda.synchronize()
+    return dict(ms=start.elapsed_time(end) / steps, bytes=0, flops=2 * M * N * K, copies=1)
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 
 
@@ -387,7 +427,8 @@ def main(argv=None) -> int:
                     help="run one workload: int4_gemv, int4_m4, int4_m16, int8_gemv, int8_prefill, "
                          "fp8_gemm, fp8_native, fp8_bwd, fp8_bwd_native, moe_int4, moe_mlp_int4, paged_attn, "
                          "quantize_int4, "
-                         "copy (counter calibration)")
+                         "copy (counter calibration), vendor_fp8_rowwise / vendor_fp8_tensorwise / "
+                         "vendor_bf16 (hipBLASLt calibration)")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
@@ -442,6 +483,12 @@ def main(argv=None) -> int:
         "quantize_int4": lambda: _hbm_row("quantize_int4_14336x4096_g128", quantize_int4_load(dev, small, 4)),
         "copy": lambda: _hbm_row("copy_256MiB", copy_calibration(dev, small, 4)),
     }
+    for kind, peak in (("fp8_rowwise", FP8_PEAK_TFLOPS), ("fp8_tensorwise", FP8_PEAK_TFLOPS),
+                       ("bf16", BF16_PEAK_TFLOPS)):
+        runners["vendor_" + kind] = (lambda kind=kind, peak=peak: (lambda r: None if r is None else _mfma_row(
+            f"vendor_hipblaslt_{kind}_4096x8192x8192", r, peak,
+            {"calibration": "vendor library through torch, not this build's kernels"}))(
+            vendor_gemm(dev, small, 4, kind)))
     if args.only:
         log(f"running {args.only}")
         row = runners[args.only]()
@@ -456,11 +503,12 @@ def main(argv=None) -> int:
     if not args.no_extra:
         for k in ("int4_m4", "int4_m16", "int8_gemv", "int8_prefill", "fp8_gemm", "fp8_native",
                   "fp8_bwd", "fp8_bwd_native", "moe_int4", "moe_mlp_int4", "paged_attn", "quantize_int4",
-                  "copy"):
+                  "copy", "vendor_fp8_rowwise", "vendor_fp8_tensorwise", "vendor_bf16"):
             log(f"{k} ...")
             row = runners[k]()
             log(json.dumps(row))
-            extra.append(row)
+            if row is not None:
+                extra.append(row)
     cpu = None
     if not args.no_cpu:
         log("cpu baseline (oracle on host cores, ~10 s)")
