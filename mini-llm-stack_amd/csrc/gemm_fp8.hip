@@ -403,19 +403,15 @@ static int launch_native(const Fp8Args& f) {
                     f.M < (1 << 30) && f.N < (1 << 30) && f.lda * 256 < (1ll << 31) &&
                     f.ldb * 256 < (1ll << 31);
   if (!fast) return MLS_ERR_UNSUPPORTED;
-  // MLS_FP8_WAVES = 4 (one wavefront per SIMD, 128 x 128 wave tiles) or 8 (default:
-  // two per SIMD, 128 x 64 wave tiles), for tuning sweeps
-  static const bool w8 = [] {
-    const char* e = getenv("MLS_FP8_WAVES");
-    return !(e && e[0] == '4');
-  }();
+  // 8 wavefronts, two per SIMD, 128 x 64 wave tiles (4 wavefronts with 128 x 128 wave
+  // tiles need 256 accumulators per lane and spill)
   static const bool dma = [] {  // MLS_FP8_DMA = 0: register-staged stores instead of LDS DMA
     const char* e = getenv("MLS_FP8_DMA");
     return !(e && e[0] == '0');
   }();
-  if (f.a_e5m2) return launch_native_dma<CT, 2, 4, 1>(f);  // the tuning variants are e4m3-only
-  if (dma) return w8 ? launch_native_dma<CT, 2, 4, 0>(f) : launch_native_dma<CT, 2, 2, 0>(f);
-  return w8 ? launch_native_w<CT, 2, 4, 0>(f) : launch_native_w<CT, 2, 2, 0>(f);
+  if (f.a_e5m2) return launch_native_dma<CT, 2, 4, 1>(f);  // the tuning variant is e4m3-only
+  if (dma) return launch_native_dma<CT, 2, 4, 0>(f);
+  return launch_native_w<CT, 2, 4, 0>(f);
 }
 
 }  // namespace mls

@@ -314,19 +314,26 @@ static int gemv_rows_override() {
   return v;
 }
 
+// Overrides stay within R * CPL <= 16 chunks per lane and MT * R <= 32 (beyond that the
+// kernel spills).
 template <int WBITS, typename AT, typename ST, int MT, int CPL>
 static void launch_one(const WqArgs& p) {
   constexpr int RDEF = CPL >= 8 ? 1 : 8 / CPL;
   int r = gemv_rows_override();
-  if (r == 0 || MT * r > 32) r = RDEF;
+  if (r == 0 || MT * r > 32 || r * CPL > 16) r = RDEF;
   switch (r) {
     case 1: return launch_r<WBITS, AT, ST, MT, CPL, 1>(p);
-    case 2: return launch_r<WBITS, AT, ST, MT, CPL, 2>(p);
-    case 4: return launch_r<WBITS, AT, ST, MT, CPL, 4>(p);
+    case 2:
+      if constexpr (2 * CPL <= 16) return launch_r<WBITS, AT, ST, MT, CPL, 2>(p);
+      break;
+    case 4:
+      if constexpr (4 * CPL <= 16 && MT * 4 <= 32) return launch_r<WBITS, AT, ST, MT, CPL, 4>(p);
+      break;
     default:
-      if constexpr (MT * 8 <= 32) return launch_r<WBITS, AT, ST, MT, CPL, 8>(p);
-      else return launch_r<WBITS, AT, ST, MT, CPL, RDEF>(p);
+      if constexpr (8 * CPL <= 16 && MT * 8 <= 32) return launch_r<WBITS, AT, ST, MT, CPL, 8>(p);
+      break;
   }
+  return launch_r<WBITS, AT, ST, MT, CPL, RDEF>(p);
 }
 
 // Picks MT (rows of x per block) for a given CPL so that the x slice fits in

@@ -224,7 +224,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
   }
 }
 
-// Tuning override for sweeps: MLS_GEMV_MFMA = "R,WAVES" (R in 1, 2; WAVES in 4, 8, 16).
+// Tuning override for sweeps: MLS_GEMV_MFMA = "R,WAVES" (R in 1, 2; WAVES in 4, 8, 16; R = 2
+// takes at most 8).
 int env_pair(int& r, int& waves) {
   const char* v = getenv("MLS_GEMV_MFMA");
   if (!v || !*v) return 0;
@@ -249,9 +250,8 @@ int launch_shape(const WqArgs& p) {
   int r = 1, waves = nsteps >= 64 ? 8 : 4;  // about 8 steps (one chunk) per wavefront
   if (nsteps >= 128) waves = 16;
   env_pair(r, waves);
-  if (r == 2) {
-    if (waves == 16) return launch_one<WBITS, AT, ST, 2, 16>(p);
-    if (waves == 8) return launch_one<WBITS, AT, ST, 2, 8>(p);
+  if (r == 2) {  // two tiles per wavefront: at most 8 wavefronts (16 spill)
+    if (waves >= 8) return launch_one<WBITS, AT, ST, 2, 8>(p);
     return launch_one<WBITS, AT, ST, 2, 4>(p);
   }
   if (waves == 16) return launch_one<WBITS, AT, ST, 1, 16>(p);
