@@ -307,12 +307,15 @@ __global__ __launch_bounds__(64 * WM * WN, 1) void fp8_gemm_dma_kernel(
     dma(P ? A0 : A1, P ? B0 : B1, (kt + 1) * BK);  // past the end: harmless reads
     __builtin_amdgcn_sched_barrier(0);
     i32x8 bop[TN], aop[2];
-#pragma unroll
-    for (int i = 0; i < TN; ++i) bop[i] = operand(bs, wn0 + i * 16 + lr);
+    // B[0] and A[0] first: the first MFMA waits for two operands, not five
+    bop[0] = operand(bs, wn0 + lr);
     aop[0] = operand(as, wm0 + lr);
+#pragma unroll
+    for (int i = 1; i < TN; ++i) bop[i] = operand(bs, wn0 + i * 16 + lr);
     // the scheduler would sink each A read to just before its MFMAs; the group barriers
     // keep A operand j + 1's reads ahead of MFMA group j
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * (TN + 1), 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * (TN - 1), 0);
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
       if (j + 1 < TM) aop[(j + 1) & 1] = operand(as, wm0 + (j + 1) * 16 + lr);
