@@ -311,3 +311,61 @@ def test_expert_mlp_combine_with_split(dev, sdt):
     want = ref.combine_rows(y, w.cpu().numpy(), pos.cpu().numpy())
     ok, worst = ref.close_bf16(out.float().cpu().numpy(), want)
     assert ok, worst
+
+
+def _dequant_int4(p, s, gs):
+    """[N, K/2] packed + [N, K/gs] scales -> fp32 [N, K] on the device (quantize.py:39-47)."""
+    N = p.shape[0]
+    q = torch.empty(N, 2 * p.shape[1], dtype=torch.float32, device=p.device)
+    q[:, 0::2] = (p & 0x0F).float()
+    q[:, 1::2] = (p >> 4).float()
+    return ((q - 8).reshape(N, -1, gs) * s.float()[:, :, None]).reshape(N, -1)
+
+
+def test_expert_mlp_full_size(dev):
+    """The bench's MoE layer at full size: T = 512 tokens, top-2 of 8 experts, D = 4096,
+    H = 14336, g128, fp16 scales (the down projection takes the K-split path). Each GEMM
+    is held to the bf16 tolerance (rtol = atol = 1e-2) against an fp32 dequantize-then-
+    matmul on the GPU (torch, TF32 off): the fused gate/up's h against fp32
+    silu(gate) * up, and the down projection + combine against fp32 on the kernel's own
+    bf16 h. (Against an fp32 reference that rounds its own h to bf16, single bf16
+    rounding flips of h, a summation-order effect, add ~0.01-0.03 absolute through the
+    14336-term down projection, beyond the 0.01 absolute bound on near-zero outputs.)"""
+    T, E, k, D, H, gs = 512, 8, 2, 4096, 14336, 128
+    assert grouped_splits(T * k, E, D, H, gs) > 1
+    WG, SG = _int4(dev, E, H, D, gs, 51, torch.float16)
+    WU, SU = _int4(dev, E, H, D, gs, 52, torch.float16)
+    WD, SD = _int4(dev, E, D, H, gs, 53, torch.float16)
+    w, idx = _route(dev, T, E, k, 54)
+    tok, counts, pos = sort_by_expert(idx, E)
+    x = torch.randn(T, D, generator=torch.Generator(device=dev).manual_seed(55), device=dev).to(torch.bfloat16)
+    a = x[tok]
+    out = int4_expert_mlp_combine(a, counts, WG, SG, WU, SU, WD, SD, gs, w, pos)
+    assert out.shape == (T, D) and out.dtype == torch.bfloat16
+    h = int4_grouped_gate_up(a, WG, SG, WU, SU, counts, gs)
+    assert h.shape == (T * k, H) and h.dtype == torch.bfloat16
+
+    def excess(got, want):
+        return float(((got.float() - want).abs() - (1e-2 + 1e-2 * want.abs())).max())
+
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        off = [0] + torch.cumsum(counts, 0).tolist()
+        y = torch.zeros(T * k, D, dtype=torch.float32, device=dev)
+        worst_h = -1.0
+        for e in range(E):
+            lo, hi = off[e], off[e + 1]
+            if hi == lo:
+                continue
+            ae = a[lo:hi].float()
+            g = ae @ _dequant_int4(WG[e], SG[e], gs).t().contiguous()
+            u = ae @ _dequant_int4(WU[e], SU[e], gs).t().contiguous()
+            worst_h = max(worst_h, excess(h[lo:hi], F.silu(g) * u))
+            y[lo:hi] = h[lo:hi].float() @ _dequant_int4(WD[e], SD[e], gs).t().contiguous()
+        want = (y[pos.reshape(-1).long()].reshape(T, k, D) * w.float()[:, :, None]).sum(1)
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
+    assert worst_h <= 0, f"full-size gate/up: worst excess over tolerance {worst_h:.3g}"
+    worst = excess(out, want)
+    assert worst <= 0, f"full-size down projection + combine: worst excess over tolerance {worst:.3g}"
