@@ -156,3 +156,32 @@ def test_encoders_vector_path(dev, dtype, fmt):
     assert np.array_equal(enc(xt.to(dev), 0.5).cpu().numpy(), want_fn(xt.float().numpy(), 0.5))
     rs = torch.rand(x.shape[0], 1, generator=torch.Generator().manual_seed(2)) + 0.1
     assert np.array_equal(enc(xt.to(dev), rs.to(dev)).cpu().numpy(), want_fn(xt.float().numpy(), rs.numpy()))
+
+
+def test_fp8_linear_backward_config_d(dev):
+    """FP8Linear's kernel backward at config D's shape (4096 tokens, 8192 -> 8192) against
+    the reference's fp32 emulation of the same e4m3 / e5m2 operands (use_kernel=False,
+    train/fp8.py:80-95) on the same weights, input and upstream gradient."""
+    torch.manual_seed(9)
+    M, N, K = 4096, 8192, 8192
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        lin = nn.Linear(K, N, bias=False)
+        mk, me = FP8Linear(lin, use_kernel=True).to(dev), FP8Linear(lin, use_kernel=False).to(dev)
+        g = torch.Generator(device=dev).manual_seed(10)
+        x = torch.randn(M, K, generator=g, device=dev)
+        dy = torch.randn(M, N, generator=g, device=dev) * 1e-2
+        grads = []
+        for m in (mk, me):
+            xi = x.clone().requires_grad_(True)
+            m(xi).backward(dy)
+            grads.append((xi.grad.float(), m.weight.grad.float()))
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = prev
+    (dxk, dwk), (dxe, dwe) = grads
+    for got, want, what in ((dxk, dxe, "dx"), (dwk, dwe, "dw")):
+        # |d| <= 2^-9 max(|want|, rms(want)), elementwise, as ref.close_fp32 states it
+        bound = 2.0 ** -9 * torch.maximum(want.abs(), want.pow(2).mean().sqrt())
+        excess = float(((got - want).abs() - bound).max())
+        assert excess <= 0, f"{what} at config D's shape: worst excess {excess:.3g}"

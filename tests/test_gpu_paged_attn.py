@@ -139,3 +139,29 @@ def test_large_batch_against_torch(dev):
         want = torch.softmax((k @ q[s].float()[:, :, None])[..., 0] * D ** -0.5, -1)[:, None, :] @ v
         ok, worst = ref.close_bf16(out[s].numpy(), want[:, 0].numpy())
         assert ok, f"seq {s} (L={L}): worst {worst:.3g}"
+
+
+def test_bench_shape(dev):
+    """The bench's workload at full size: 64 sequences x 32 heads x 2048 cached tokens,
+    D = 128, bf16 pools in blocks of 16 handed out in a shuffled order. 16 sampled
+    (sequence, head) pairs against torch's attention on the gathered K/V in fp32."""
+    S, H, D, ctx, bs = 64, 32, 128, 2048, 16
+    g = torch.Generator(device=dev).manual_seed(8)
+    nb = S * ctx // bs
+    kp = torch.randn(nb, H, bs, D, generator=g, device=dev).to(torch.bfloat16)
+    vp = torch.randn(nb, H, bs, D, generator=g, device=dev).to(torch.bfloat16)
+    tab = torch.randperm(nb, generator=g, device=dev).to(torch.int32).reshape(S, ctx // bs).contiguous()
+    lens = torch.full((S,), ctx, dtype=torch.int32, device=dev)
+    q = torch.randn(S, H, D, generator=g, device=dev).to(torch.bfloat16)
+    out = paged_attention_decode(q, kp, vp, tab, lens)
+    assert out.shape == (S, H, D) and out.dtype == torch.bfloat16
+    pick = torch.randint(0, S * H, (16,), generator=torch.Generator().manual_seed(3)).tolist()
+    for sh in pick:
+        s, h = divmod(sh, H)
+        blocks = tab[s].long()
+        k = kp[blocks, h].reshape(ctx, D).float()         # [ctx, D] in token order
+        v = vp[blocks, h].reshape(ctx, D).float()
+        p = torch.softmax((k @ q[s, h].float()) * D ** -0.5, 0)
+        want = (p[None, :] @ v)[0]
+        ok, worst = ref.close_bf16(out[s, h].float().cpu().numpy(), want.cpu().numpy())
+        assert ok, f"seq {s} head {h}: worst {worst:.3g}"
