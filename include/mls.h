@@ -157,6 +157,8 @@ int mls_fp8_gemm(const uint8_t* a, int64_t lda, const uint8_t* b, int64_t ldb,
  * expert e's packed weights w + e*w_estride (bytes) with scales s + e*s_estride
  * (elements). seg_off is a DEVICE int32 array of E+1 non-decreasing offsets with
  * seg_off[0] = 0 and seg_off[E] = M_total; it is read on the device (no host sync).
+ * Each segment is clamped to [0, M_total) on the device: offsets that break the
+ * contract give wrong rows, never an access outside a or c.
  * a_dt = c_dt in {F16, BF16}. */
 int mls_int4_grouped_gemm(const void* a, int a_dt, int64_t lda,
                           const int32_t* seg_off, int E, int64_t M_total,

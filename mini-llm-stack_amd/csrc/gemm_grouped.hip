@@ -100,7 +100,11 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   // one XCD next to its column tiles, sharing the chunk's activation rows in L2.
   const int ksn = p.ksplit > 1 ? p.ksplit : 1;
   int chunks = 0;
-  for (int e = 0; e < p.E; ++e) chunks += (p.seg_off[e + 1] - p.seg_off[e] + BMX - 1) / BMX;
+  for (int e = 0; e < p.E; ++e) {
+    int lo, hi;
+    seg_rows(p, e, lo, hi);
+    chunks += (hi - lo + BMX - 1) / BMX;
+  }
   const int items = chunks * p.n_tiles * ksn;
   if ((int)blockIdx.x >= items) return;
   const int L = xcd_remap(blockIdx.x, items);
@@ -109,8 +113,7 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   const int Kp = p.K / ksn, kbase = split * Kp;  // this block's K range
   int e = 0, cum = 0, lo = 0, hi = 0;
   for (; e < p.E; ++e) {
-    lo = p.seg_off[e];
-    hi = p.seg_off[e + 1];
+    seg_rows(p, e, lo, hi);
     const int t = (hi - lo + BMX - 1) / BMX;
     if (chunk < cum + t) break;
     cum += t;

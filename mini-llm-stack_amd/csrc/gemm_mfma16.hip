@@ -60,7 +60,8 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_gemm_kernel(const Mfma16P
   if constexpr (GROUPED) {
     int e = 0, cum = 0, row_lo = 0;
     for (; e < p.E; ++e) {
-      const int lo = p.seg_off[e], hi = p.seg_off[e + 1];
+      int lo, hi;
+      seg_rows(p, e, lo, hi);
       const int t = (hi - lo + BM - 1) / BM;
       if (mt < cum + t) {
         row_lo = lo;
@@ -347,7 +348,8 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_adma_kernel(const Mfma16P
   if constexpr (GROUPED) {
     int e = 0, cum = 0, row_lo = 0;
     for (; e < p.E; ++e) {
-      const int lo = p.seg_off[e], hi = p.seg_off[e + 1];
+      int lo, hi;
+      seg_rows(p, e, lo, hi);
       const int tcount = (hi - lo + BM - 1) / BM;
       if (mt < cum + tcount) {
         row_lo = lo;

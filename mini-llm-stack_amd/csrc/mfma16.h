@@ -144,6 +144,15 @@ __device__ __forceinline__ void widen_e5m2(const uint4& q, uint32_t* o) {
 
 // One 16-byte global chunk per lane straight into LDS (buffer_load_dwordx4 ... lds): lane l
 // writes LDS bytes [16 l, 16 l + 16) above `lds`.
+// Rows [lo, hi) of segment e of a grouped launch, clamped to [0, M). The offsets live on
+// the device and cannot be checked by the host without a sync: offsets that break the
+// contract (negative, decreasing, past M_total) shrink or overlap segments, but never
+// move an access outside the operands.
+__device__ __forceinline__ void seg_rows(const Mfma16Params& p, int e, int& lo, int& hi) {
+  lo = min(max(p.seg_off[e], 0), p.M);
+  hi = min(max(p.seg_off[e + 1], lo), p.M);
+}
+
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds, int voff, int soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff,
                                            soff, 0, 0);

@@ -96,3 +96,21 @@ def test_config_e(dev):
     want = ref.int4_matmul(a[lo:hi].float().cpu().numpy(), P[e].cpu().numpy(), S[e].float().cpu().numpy(), gs)
     ok, w_ = ref.close_bf16(out[lo:hi].float().cpu().numpy(), want)
     assert ok, f"oracle rows worst {w_:.3g}"
+
+
+def test_offsets_past_rows_are_clamped(dev):
+    """Device offsets cannot be checked by the host without a sync; offsets that run past
+    the activation rows (counts summing to more than M_total) are truncated at M_total in
+    the kernels: the result equals the call with the truncated offsets, and nothing is
+    read or written outside the operands."""
+    from kernels.moe_grouped import int4_grouped_gate_up
+    E, N, K, gs, M = 4, 256, 256, 128, 100
+    P, S = _experts(dev, E, N, K, gs, 17)
+    a = torch.randn(M, K, generator=torch.Generator().manual_seed(18)).to(torch.bfloat16).to(dev)
+    bad = torch.tensor([0, 30, 70, 137, 160], dtype=torch.int32, device=dev)
+    good = torch.tensor([0, 30, 70, 100, 100], dtype=torch.int32, device=dev)
+    out = int4_grouped_matmul(a, P, S, bad, gs)
+    assert torch.equal(out, int4_grouped_matmul(a, P, S, good, gs))
+    P2, S2 = _experts(dev, E, N, K, gs, 19)
+    h = int4_grouped_gate_up(a, P, S, P2, S2, bad, gs)
+    assert torch.equal(h, int4_grouped_gate_up(a, P, S, P2, S2, good, gs))
