@@ -39,7 +39,7 @@ enum {
   MLS_ERR_HIP = -3          /* a HIP runtime call failed */
 };
 
-#define MLS_ABI_VERSION 5
+#define MLS_ABI_VERSION 6
 
 /* No reference counterpart: version of this ABI (MLS_ABI_VERSION). */
 int mls_abi_version(void);
@@ -77,6 +77,15 @@ int mls_e4m3_encode(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t
 int mls_e5m2_encode(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
                     float scale, const float* scale_ptr, int64_t scale_stride,
                     uint8_t* out, int64_t ldo, mls_stream_t stream);
+
+/* mls_e5m2_encode that also writes the transposed bytes: out[r][c] and
+ * out_t[c][r] = e5m2(x[r][c] / scale[r]) (same rounding as mls_e5m2_encode).
+ * FP8 training's backward needs the e5m2 gradient in both layouts: dy for
+ * dx = dy W and dy^T for dw = dy^T x (train/fp8.py:88-94); one pass replaces an
+ * encode and a transpose. ldt >= rows. */
+int mls_e5m2_encode_t(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
+                      float scale, const float* scale_ptr, int64_t scale_stride,
+                      uint8_t* out, int64_t ldo, uint8_t* out_t, int64_t ldt, mls_stream_t stream);
 
 /* No single reference counterpart: the byte transpose behind the .t() of fp8
  * operands in FP8 training's backward (train/fp8.py:92-94), which the K-contiguous

@@ -140,6 +140,79 @@ __global__ void fp8_encode_vec_kernel(const T* __restrict__ x, int64_t rows, int
   }
 }
 
+// e5m2 encode with a transposed copy: out[r][c] = out_t[c][r] = e5m2(x[r][c] / s[r]).
+// A 256-thread block encodes a 64 x 64 tile: each thread 16 consecutive elements of one
+// row (written as one 16-byte store), the bytes also go to an LDS tile padded by 4 bytes
+// per row, and after the barrier each thread writes 16 consecutive bytes of one row of
+// the transpose. vec: full tile, 16-byte aligned input rows and output rows.
+template <typename T>
+__global__ __launch_bounds__(256) void e5m2_encode_t_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
+                                                            int64_t ldx, float scale, const float* __restrict__ sp,
+                                                            int64_t sstride, uint8_t* __restrict__ out, int64_t ldo,
+                                                            uint8_t* __restrict__ out_t, int64_t ldt,
+                                                            int64_t col_tiles, bool vec) {
+  constexpr int TS = 64, P = TS + 4;
+  __shared__ uint8_t tile[TS * P];
+  const int64_t bt = blockIdx.x;
+  const int64_t r0 = (bt / col_tiles) * TS, c0 = (bt % col_tiles) * TS;
+  const int tid = threadIdx.x;
+  const int lr = tid >> 2, lc = (tid & 3) * 16;
+  const int64_t r = r0 + lr;
+  const bool full = vec && r0 + TS <= rows && c0 + TS <= cols;
+  uint8_t b[16];
+  if (full) {
+    const float s = sp ? sp[r * sstride] : scale;
+    float v[16];
+    const T* src = x + r * ldx + c0 + lc;
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float4 f = reinterpret_cast<const float4*>(src)[q];
+        v[4 * q + 0] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint4 h = reinterpret_cast<const uint4*>(src)[q];
+        const T* e = reinterpret_cast<const T*>(&h);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[8 * q + k] = to_f32(e[k]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) b[i] = (uint8_t)e5m2_encode(v[i] / s);
+    *reinterpret_cast<uint4*>(out + r * ldo + c0 + lc) = *reinterpret_cast<const uint4*>(b);
+  } else {
+    const float s = r < rows ? (sp ? sp[r * sstride] : scale) : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t c = c0 + lc + i;
+      b[i] = 0;
+      if (r < rows && c < cols) {
+        b[i] = (uint8_t)e5m2_encode(to_f32(x[r * ldx + c]) / s);
+        out[r * ldo + c] = b[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) tile[lr * P + lc + i] = b[i];
+  __syncthreads();
+  // row c0 + lr of the transpose holds source column c0 + lr, bytes of source rows r0 + lc ..
+  const int64_t dr = c0 + lr;
+  if (full) {
+    uint8_t t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[i] = tile[(lc + i) * P + lr];
+    *reinterpret_cast<uint4*>(out_t + dr * ldt + r0 + lc) = *reinterpret_cast<const uint4*>(t);
+  } else if (dr < cols) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t dc = r0 + lc + i;
+      if (dc < rows) out_t[dr * ldt + dc] = tile[(lc + i) * P + lr];
+    }
+  }
+}
+
 static int grid_for(int64_t work, int block) {
   int64_t g = cdiv(work, block);
   if (g > 65536) g = 65536;
@@ -228,4 +301,33 @@ extern "C" int mls_e5m2_encode(const void* x, int x_dt, int64_t rows, int64_t co
                                uint8_t* out, int64_t ldo, mls_stream_t stream) {
   return fp8_encode<true>("mls_e5m2_encode", x, x_dt, rows, cols, ldx, scale, scale_ptr, scale_stride, out,
                           ldo, stream);
+}
+
+extern "C" int mls_e5m2_encode_t(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
+                                 float scale, const float* scale_ptr, int64_t scale_stride,
+                                 uint8_t* out, int64_t ldo, uint8_t* out_t, int64_t ldt, mls_stream_t stream) {
+  const char* fn = "mls_e5m2_encode_t";
+  if (rows < 0 || cols < 0) return fail(MLS_ERR_ARG, "%s: negative size", fn);
+  if (rows == 0 || cols == 0) return MLS_OK;
+  if (!x || !out || !out_t) return fail(MLS_ERR_ARG, "%s: null pointer", fn);
+  if (!is_float_dt(x_dt)) return fail(MLS_ERR_ARG, "%s: bad x dtype %d", fn, x_dt);
+  if (ldx < cols || ldo < cols || ldt < rows || scale_stride < 0)
+    return fail(MLS_ERR_ARG, "%s: bad leading dimension or scale stride", fn);
+  const int64_t rt = cdiv(rows, 64), ct = cdiv(cols, 64);
+  if (rt * ct > 0x7FFFFFFF) return fail(MLS_ERR_UNSUPPORTED, "%s: too large", fn);
+  const int xsz = dt_size(x_dt);
+  const bool vec = aligned(x, 16) && (ldx * xsz) % 16 == 0 && aligned(out, 16) && ldo % 16 == 0 &&
+                   aligned(out_t, 16) && ldt % 16 == 0;
+  const dim3 grid((unsigned)(rt * ct));
+  hipStream_t st = (hipStream_t)stream;
+  if (x_dt == MLS_F32)
+    hipLaunchKernelGGL(e5m2_encode_t_kernel<float>, grid, dim3(256), 0, st, (const float*)x, rows, cols, ldx, scale,
+                       scale_ptr, scale_stride, out, ldo, out_t, ldt, ct, vec);
+  else if (x_dt == MLS_F16)
+    hipLaunchKernelGGL(e5m2_encode_t_kernel<_Float16>, grid, dim3(256), 0, st, (const _Float16*)x, rows, cols, ldx,
+                       scale, scale_ptr, scale_stride, out, ldo, out_t, ldt, ct, vec);
+  else
+    hipLaunchKernelGGL(e5m2_encode_t_kernel<__bf16>, grid, dim3(256), 0, st, (const __bf16*)x, rows, cols, ldx,
+                       scale, scale_ptr, scale_stride, out, ldo, out_t, ldt, ct, vec);
+  return check_launch(fn);
 }

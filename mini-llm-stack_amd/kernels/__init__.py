@@ -18,7 +18,7 @@ from pathlib import Path
 # This implementation only ever runs compiled gfx950 code.
 INTERPRETER = False
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 LIB_PATH = Path(os.environ.get("MLS_LIB") or
                 Path(__file__).resolve().parent.parent / "libmls_hip.so")
 
@@ -39,6 +39,7 @@ SIGNATURES = {
     "mls_e4m3_dequantize": ([_P, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _P], _I),
     "mls_e4m3_encode": ([_P, _I, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _P], _I),
     "mls_e5m2_encode": ([_P, _I, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _P], _I),
+    "mls_e5m2_encode_t": ([_P, _I, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _P, _I64, _P], _I),
     "mls_transpose_u8": ([_P, _I64, _I64, _I64, _P, _I64, _P], _I),
     "mls_quantize_int8": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P], _I),
     "mls_quantize_int4": ([_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P], _I),

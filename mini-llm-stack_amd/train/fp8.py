@@ -21,7 +21,7 @@ import torch
 import torch.nn as nn
 
 from kernels.fp8_matmul import (E4M3_MAX, E5M2_MAX, dequantize_e4m3, fp8_matmul, quantize_e4m3,
-                                quantize_e5m2, transpose_u8)
+                                quantize_e5m2, quantize_e5m2_t, transpose_u8)
 
 
 class DynamicScaler:
@@ -73,11 +73,13 @@ class _FP8LinearFn(torch.autograd.Function):
             sdy = max(float(dy.detach().abs().amax()) / E5M2_MAX, 1e-12)
         else:
             sdy = 1.0
-        dyb = _quant_e5m2(dy, sdy)
         if ctx.use_kernel and dy.device.type == "cuda":
+            # the e5m2 gradient in both layouts from one pass (dy for dx, dy^T for dw)
+            dyb, dybt = quantize_e5m2_t(dy, sdy)
             dx = fp8_matmul(dyb, transpose_u8(wb), sdy, sw, torch.float32, a_format="e5m2")
-            dw = fp8_matmul(transpose_u8(dyb), transpose_u8(xb), sdy, sx, torch.float32, a_format="e5m2")
+            dw = fp8_matmul(dybt, transpose_u8(xb), sdy, sx, torch.float32, a_format="e5m2")
             return dx, dw, None, None, None, None
+        dyb = _quant_e5m2(dy, sdy)
         dyh = _dequant_e5m2(dyb, sdy)
         xh = dequantize_e4m3(xb, sx)
         wh = dequantize_e4m3(wb, sw)

@@ -24,7 +24,7 @@ def declared_symbols() -> list[str]:
 
 def test_header_declares_the_boundary():
     syms = declared_symbols()
-    assert len(syms) == len(set(syms)) == 20
+    assert len(syms) == len(set(syms)) == 21
     assert set(syms) == set(kernels.SIGNATURES)
 
 
@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = kernels.load_library()
-    assert lib.mls_abi_version() == kernels.ABI_VERSION == 5
+    assert lib.mls_abi_version() == kernels.ABI_VERSION == 6
     assert isinstance(lib.mls_last_error(), bytes)
 
 
@@ -141,6 +141,9 @@ def test_fp8_train_entry_points_reject():
         kernels.MLS_ERR_ARG
     assert L.mls_e5m2_encode(1, 5, 2, 2, 2, 1.0, NULL, 0, 1, 2, NULL) == kernels.MLS_ERR_ARG
     assert L.mls_e5m2_encode(1, 0, 2, 4, 2, 1.0, NULL, 0, 1, 4, NULL) == kernels.MLS_ERR_ARG   # ldx < cols
+    assert L.mls_e5m2_encode_t(1, 0, 4, 8, 8, 1.0, NULL, 0, 1, 8, 1, 3, NULL) == kernels.MLS_ERR_ARG  # ldt < rows
+    assert L.mls_e5m2_encode_t(1, 0, 4, 8, 8, 1.0, NULL, 0, 1, 8, NULL, 4, NULL) == kernels.MLS_ERR_ARG  # no out_t
+    assert L.mls_e5m2_encode_t(NULL, 0, 0, 8, 8, 1.0, NULL, 0, NULL, 8, NULL, 0, NULL) == 0
     assert L.mls_transpose_u8(1, 4, 8, 4, 1, 4, NULL) == kernels.MLS_ERR_ARG                  # lds < cols
     assert L.mls_transpose_u8(1, 4, 8, 8, 1, 3, NULL) == kernels.MLS_ERR_ARG                  # ldd < rows
     assert L.mls_transpose_u8(NULL, 0, 8, 8, NULL, 0, NULL) == 0

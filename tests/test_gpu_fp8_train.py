@@ -185,3 +185,34 @@ def test_fp8_linear_backward_config_d(dev):
         bound = 2.0 ** -9 * torch.maximum(want.abs(), want.pow(2).mean().sqrt())
         excess = float(((got - want).abs() - bound).max())
         assert excess <= 0, f"{what} at config D's shape: worst excess {excess:.3g}"
+
+
+@pytest.mark.parametrize("R,C,dtype,per_row,off", [
+    (256, 512, torch.float32, False, 0),     # whole 64 x 64 tiles
+    (130, 300, torch.float32, True, 0),      # ragged edge tiles, per-row scales
+    (1, 1, torch.float32, False, 0),
+    (64, 200, torch.bfloat16, False, 0),
+    (200, 64, torch.float16, True, 0),
+    (96, 128, torch.float32, False, 4),      # strided rows: the byte path for the input
+    (4096, 8192, torch.float32, False, 0),   # config D's gradient
+])
+def test_quantize_e5m2_t(dev, R, C, dtype, per_row, off):
+    """One-pass encode + transpose: both outputs bit-identical to quantize_e5m2 and its
+    byte transpose, boundaries, NaN and saturation included."""
+    from kernels.fp8_matmul import quantize_e5m2_t
+    g = torch.Generator().manual_seed(R * 7 + C)
+    x = torch.randn(R, C + off, generator=g) * 3e3
+    pts = torch.from_numpy(_boundaries())
+    n = min(pts.numel(), x.numel())
+    x.view(-1)[:n] = pts[:n] * 1.7
+    xd = x.to(dtype).to(dev)
+    xs = xd[:, off:] if off else xd
+    scale = (torch.rand(R, 1, generator=g) + 0.25).to(dev) if per_row else 0.37
+    bits, bits_t = quantize_e5m2_t(xs, scale)
+    want = quantize_e5m2(xs.contiguous(), scale)
+    assert bits.shape == (R, C) and bits_t.shape == (C, R) and bits_t.is_contiguous()
+    assert torch.equal(bits, want)
+    assert torch.equal(bits_t, want.t().contiguous())
+    if R * C <= 64 * 1024:
+        sc = scale.cpu().numpy() if per_row else scale
+        assert np.array_equal(bits.cpu().numpy(), ref.quantize_e5m2(xs.float().cpu().numpy(), sc))
