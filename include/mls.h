@@ -87,6 +87,14 @@ int mls_e5m2_encode_t(const void* x, int x_dt, int64_t rows, int64_t cols, int64
                       float scale, const float* scale_ptr, int64_t scale_stride,
                       uint8_t* out, int64_t ldo, uint8_t* out_t, int64_t ldt, mls_stream_t stream);
 
+/* mls_e4m3_encode that also writes the transposed bytes (same rounding): with
+ * FP8Linear's kernels, the forward encodes x and W once into both layouts and keeps
+ * the transposes for the backward (train/fp8.py:68-69, 88-94), which needs x^T and
+ * W^T only. ldt >= rows. */
+int mls_e4m3_encode_t(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
+                      float scale, const float* scale_ptr, int64_t scale_stride,
+                      uint8_t* out, int64_t ldo, uint8_t* out_t, int64_t ldt, mls_stream_t stream);
+
 /* No single reference counterpart: the byte transpose behind the .t() of fp8
  * operands in FP8 training's backward (train/fp8.py:92-94), which the K-contiguous
  * GEMM needs materialised: dst[c][r] = src[r][c] for r < rows, c < cols. */

@@ -140,13 +140,13 @@ __global__ void fp8_encode_vec_kernel(const T* __restrict__ x, int64_t rows, int
   }
 }
 
-// e5m2 encode with a transposed copy: out[r][c] = out_t[c][r] = e5m2(x[r][c] / s[r]).
+// fp8 encode (e5m2 or e4m3) with a transposed copy: out[r][c] = out_t[c][r] = fp8(x[r][c] / s[r]).
 // A 256-thread block encodes a 64 x 64 tile: each thread 16 consecutive elements of one
 // row (written as one 16-byte store), the bytes also go to an LDS tile padded by 4 bytes
 // per row, and after the barrier each thread writes 16 consecutive bytes of one row of
 // the transpose. vec: full tile, 16-byte aligned input rows and output rows.
-template <typename T>
-__global__ __launch_bounds__(256) void e5m2_encode_t_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
+template <typename T, bool E5M2>
+__global__ __launch_bounds__(256) void fp8_encode_t_kernel(const T* __restrict__ x, int64_t rows, int64_t cols,
                                                             int64_t ldx, float scale, const float* __restrict__ sp,
                                                             int64_t sstride, uint8_t* __restrict__ out, int64_t ldo,
                                                             uint8_t* __restrict__ out_t, int64_t ldt,
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void e5m2_encode_t_kernel(const T* __restrict_
       }
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) b[i] = (uint8_t)e5m2_encode(v[i] / s);
+    for (int i = 0; i < 16; ++i) b[i] = (uint8_t)(E5M2 ? e5m2_encode(v[i] / s) : e4m3_encode(v[i] / s));
     *reinterpret_cast<uint4*>(out + r * ldo + c0 + lc) = *reinterpret_cast<const uint4*>(b);
   } else {
     const float s = r < rows ? (sp ? sp[r * sstride] : scale) : 1.0f;
@@ -189,7 +189,8 @@ __global__ __launch_bounds__(256) void e5m2_encode_t_kernel(const T* __restrict_
       const int64_t c = c0 + lc + i;
       b[i] = 0;
       if (r < rows && c < cols) {
-        b[i] = (uint8_t)e5m2_encode(to_f32(x[r * ldx + c]) / s);
+        const float q = to_f32(x[r * ldx + c]) / s;
+        b[i] = (uint8_t)(E5M2 ? e5m2_encode(q) : e4m3_encode(q));
         out[r * ldo + c] = b[i];
       }
     }
@@ -303,10 +304,10 @@ extern "C" int mls_e5m2_encode(const void* x, int x_dt, int64_t rows, int64_t co
                           ldo, stream);
 }
 
-extern "C" int mls_e5m2_encode_t(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
-                                 float scale, const float* scale_ptr, int64_t scale_stride,
-                                 uint8_t* out, int64_t ldo, uint8_t* out_t, int64_t ldt, mls_stream_t stream) {
-  const char* fn = "mls_e5m2_encode_t";
+template <bool E5M2>
+static int fp8_encode_t(const char* fn, const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
+                        float scale, const float* scale_ptr, int64_t scale_stride, uint8_t* out, int64_t ldo,
+                        uint8_t* out_t, int64_t ldt, mls_stream_t stream) {
   if (rows < 0 || cols < 0) return fail(MLS_ERR_ARG, "%s: negative size", fn);
   if (rows == 0 || cols == 0) return MLS_OK;
   if (!x || !out || !out_t) return fail(MLS_ERR_ARG, "%s: null pointer", fn);
@@ -321,13 +322,27 @@ extern "C" int mls_e5m2_encode_t(const void* x, int x_dt, int64_t rows, int64_t 
   const dim3 grid((unsigned)(rt * ct));
   hipStream_t st = (hipStream_t)stream;
   if (x_dt == MLS_F32)
-    hipLaunchKernelGGL(e5m2_encode_t_kernel<float>, grid, dim3(256), 0, st, (const float*)x, rows, cols, ldx, scale,
-                       scale_ptr, scale_stride, out, ldo, out_t, ldt, ct, vec);
+    hipLaunchKernelGGL((fp8_encode_t_kernel<float, E5M2>), grid, dim3(256), 0, st, (const float*)x, rows, cols, ldx,
+                       scale, scale_ptr, scale_stride, out, ldo, out_t, ldt, ct, vec);
   else if (x_dt == MLS_F16)
-    hipLaunchKernelGGL(e5m2_encode_t_kernel<_Float16>, grid, dim3(256), 0, st, (const _Float16*)x, rows, cols, ldx,
-                       scale, scale_ptr, scale_stride, out, ldo, out_t, ldt, ct, vec);
+    hipLaunchKernelGGL((fp8_encode_t_kernel<_Float16, E5M2>), grid, dim3(256), 0, st, (const _Float16*)x, rows, cols,
+                       ldx, scale, scale_ptr, scale_stride, out, ldo, out_t, ldt, ct, vec);
   else
-    hipLaunchKernelGGL(e5m2_encode_t_kernel<__bf16>, grid, dim3(256), 0, st, (const __bf16*)x, rows, cols, ldx,
-                       scale, scale_ptr, scale_stride, out, ldo, out_t, ldt, ct, vec);
+    hipLaunchKernelGGL((fp8_encode_t_kernel<__bf16, E5M2>), grid, dim3(256), 0, st, (const __bf16*)x, rows, cols,
+                       ldx, scale, scale_ptr, scale_stride, out, ldo, out_t, ldt, ct, vec);
   return check_launch(fn);
+}
+
+extern "C" int mls_e5m2_encode_t(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
+                                 float scale, const float* scale_ptr, int64_t scale_stride,
+                                 uint8_t* out, int64_t ldo, uint8_t* out_t, int64_t ldt, mls_stream_t stream) {
+  return fp8_encode_t<true>("mls_e5m2_encode_t", x, x_dt, rows, cols, ldx, scale, scale_ptr, scale_stride, out, ldo,
+                            out_t, ldt, stream);
+}
+
+extern "C" int mls_e4m3_encode_t(const void* x, int x_dt, int64_t rows, int64_t cols, int64_t ldx,
+                                 float scale, const float* scale_ptr, int64_t scale_stride,
+                                 uint8_t* out, int64_t ldo, uint8_t* out_t, int64_t ldt, mls_stream_t stream) {
+  return fp8_encode_t<false>("mls_e4m3_encode_t", x, x_dt, rows, cols, ldx, scale, scale_ptr, scale_stride, out, ldo,
+                             out_t, ldt, stream);
 }

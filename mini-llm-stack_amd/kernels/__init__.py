@@ -40,6 +40,7 @@ SIGNATURES = {
     "mls_e4m3_encode": ([_P, _I, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _P], _I),
     "mls_e5m2_encode": ([_P, _I, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _P], _I),
     "mls_e5m2_encode_t": ([_P, _I, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _P, _I64, _P], _I),
+    "mls_e4m3_encode_t": ([_P, _I, _I64, _I64, _I64, _F, _P, _I64, _P, _I64, _P, _I64, _P], _I),
     "mls_transpose_u8": ([_P, _I64, _I64, _I64, _P, _I64, _P], _I),
     "mls_quantize_int8": ([_P, _I64, _I64, _I64, _P, _I64, _P, _P], _I),
     "mls_quantize_int4": ([_P, _I64, _I64, _I64, _I, _P, _I64, _P, _P], _I),

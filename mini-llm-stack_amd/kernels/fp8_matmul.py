@@ -18,8 +18,8 @@ product per group. Scales are applied in the epilogue and may be Python floats
 
 fp8_matmul(..., a_format="e5m2") takes an e5m2 A operand (FP8 training's gradients;
 e5m2 widens to bf16 exactly, and the native path selects the MFMA's bf8 format);
-quantize_e5m2, quantize_e5m2_t (the encode with a transposed copy) and transpose_u8 are
-the other pieces of that backward.
+quantize_e5m2, transpose_u8 and the encoders with a transposed copy (quantize_e5m2_t,
+quantize_e4m3_t) are the other pieces of that backward.
 
 quantize_e4m3 / dequantize_e4m3 run the gfx950 codec kernels on HIP tensors. On
 host tensors (the load-time and CPU-training callers) they run the reference's
@@ -122,25 +122,37 @@ def quantize_e5m2(x: torch.Tensor, scale) -> torch.Tensor:
     return out.reshape(shape)
 
 
+def _encode_t(fn: str, entry: str, x: torch.Tensor, scale) -> tuple[torch.Tensor, torch.Tensor]:
+    dev = require_hip(fn, x)
+    if x.dim() != 2:
+        raise ValueError(f"{fn}: expected a 2-D tensor, got {tuple(x.shape)}")
+    x2 = rows(x)
+    R, C = x2.shape
+    sa = _row_scale(scale, R, dev, fn, False)
+    if sa is None:
+        raise ValueError(f"{fn}: scale must be a float, a 1-element tensor or [M, 1]")
+    out = torch.empty(R, C, dtype=torch.uint8, device=dev)
+    out_t = torch.empty(C, R, dtype=torch.uint8, device=dev)
+    kernels.check(getattr(kernels.lib(), entry)(
+        x2.data_ptr(), dt_code(x.dtype, fn), R, C, ld(x2), sa[0], sa[1], sa[2],
+        out.data_ptr(), ld(out), out_t.data_ptr(), ld(out_t), stream(dev)), fn)
+    return out, out_t
+
+
 def quantize_e5m2_t(x: torch.Tensor, scale) -> tuple[torch.Tensor, torch.Tensor]:
     """(quantize_e5m2(x, scale), its transpose as a contiguous [cols, rows] uint8 tensor)
     from one pass over a 2-D device tensor x: the gradient operand of FP8 training's
     backward in both layouts it needs (train/fp8.py:88-94). scale: a float, a 1-element
     tensor or [M, 1] per row."""
-    dev = require_hip("quantize_e5m2_t", x)
-    if x.dim() != 2:
-        raise ValueError(f"quantize_e5m2_t: expected a 2-D tensor, got {tuple(x.shape)}")
-    x2 = rows(x)
-    R, C = x2.shape
-    sa = _row_scale(scale, R, dev, "quantize_e5m2_t", False)
-    if sa is None:
-        raise ValueError("quantize_e5m2_t: scale must be a float, a 1-element tensor or [M, 1]")
-    out = torch.empty(R, C, dtype=torch.uint8, device=dev)
-    out_t = torch.empty(C, R, dtype=torch.uint8, device=dev)
-    kernels.check(kernels.lib().mls_e5m2_encode_t(
-        x2.data_ptr(), dt_code(x.dtype, "quantize_e5m2_t"), R, C, ld(x2), sa[0], sa[1], sa[2],
-        out.data_ptr(), ld(out), out_t.data_ptr(), ld(out_t), stream(dev)), "quantize_e5m2_t")
-    return out, out_t
+    return _encode_t("quantize_e5m2_t", "mls_e5m2_encode_t", x, scale)
+
+
+def quantize_e4m3_t(x: torch.Tensor, scale) -> tuple[torch.Tensor, torch.Tensor]:
+    """(quantize_e4m3(x, scale), its transpose as a contiguous [cols, rows] uint8 tensor)
+    from one pass over a 2-D device tensor x: FP8Linear's forward operands, whose
+    transposes its backward needs (train/fp8.py:68-69, 88-94). scale: a float, a
+    1-element tensor or [M, 1] per row."""
+    return _encode_t("quantize_e4m3_t", "mls_e4m3_encode_t", x, scale)
 
 
 def transpose_u8(t: torch.Tensor) -> torch.Tensor:

@@ -21,7 +21,7 @@ import torch
 import torch.nn as nn
 
 from kernels.fp8_matmul import (E4M3_MAX, E5M2_MAX, dequantize_e4m3, fp8_matmul, quantize_e4m3,
-                                quantize_e5m2, quantize_e5m2_t, transpose_u8)
+                                quantize_e4m3_t, quantize_e5m2, quantize_e5m2_t, transpose_u8)
 
 
 class DynamicScaler:
@@ -55,30 +55,44 @@ def _dequant_e5m2(bits: torch.Tensor, scale: float) -> torch.Tensor:
 class _FP8LinearFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w, sx, sw, use_kernel, scale_grads):
-        xb = quantize_e4m3(x, sx)
-        wb = quantize_e4m3(w, sw)
-        ctx.save_for_backward(xb, wb)
         ctx.scales = (sx, sw)
         ctx.scale_grads = scale_grads
         ctx.use_kernel = use_kernel
+        ctx.transposed = False
+        if use_kernel and x.device.type == "cuda" and any(ctx.needs_input_grad[:2]):
+            # x and W encoded once into both layouts: the GEMM takes the row-major bytes,
+            # the kernel backward needs only x^T and W^T, which are what is saved
+            xb, xbt = quantize_e4m3_t(x, sx)
+            wb, wbt = quantize_e4m3_t(w, sw)
+            ctx.save_for_backward(xbt, wbt)
+            ctx.transposed = True
+            return fp8_matmul(xb, wb, sx, sw)
+        xb = quantize_e4m3(x, sx)
+        wb = quantize_e4m3(w, sw)
+        ctx.save_for_backward(xb, wb)
         if use_kernel:
             return fp8_matmul(xb, wb, sx, sw)
         return dequantize_e4m3(xb, sx) @ dequantize_e4m3(wb, sw).t()
 
     @staticmethod
     def backward(ctx, dy):
-        xb, wb = ctx.saved_tensors
         sx, sw = ctx.scales
         if ctx.scale_grads:
             sdy = max(float(dy.detach().abs().amax()) / E5M2_MAX, 1e-12)
         else:
             sdy = 1.0
         if ctx.use_kernel and dy.device.type == "cuda":
+            if ctx.transposed:
+                xbt, wbt = ctx.saved_tensors
+            else:
+                xb, wb = ctx.saved_tensors
+                xbt, wbt = transpose_u8(xb), transpose_u8(wb)
             # the e5m2 gradient in both layouts from one pass (dy for dx, dy^T for dw)
             dyb, dybt = quantize_e5m2_t(dy, sdy)
-            dx = fp8_matmul(dyb, transpose_u8(wb), sdy, sw, torch.float32, a_format="e5m2")
-            dw = fp8_matmul(dybt, transpose_u8(xb), sdy, sx, torch.float32, a_format="e5m2")
+            dx = fp8_matmul(dyb, wbt, sdy, sw, torch.float32, a_format="e5m2")
+            dw = fp8_matmul(dybt, xbt, sdy, sx, torch.float32, a_format="e5m2")
             return dx, dw, None, None, None, None
+        xb, wb = ctx.saved_tensors
         dyb = _quant_e5m2(dy, sdy)
         dyh = _dequant_e5m2(dyb, sdy)
         xh = dequantize_e4m3(xb, sx)

@@ -24,7 +24,7 @@ def declared_symbols() -> list[str]:
 
 def test_header_declares_the_boundary():
     syms = declared_symbols()
-    assert len(syms) == len(set(syms)) == 21
+    assert len(syms) == len(set(syms)) == 22
     assert set(syms) == set(kernels.SIGNATURES)
 
 
@@ -144,6 +144,8 @@ def test_fp8_train_entry_points_reject():
     assert L.mls_e5m2_encode_t(1, 0, 4, 8, 8, 1.0, NULL, 0, 1, 8, 1, 3, NULL) == kernels.MLS_ERR_ARG  # ldt < rows
     assert L.mls_e5m2_encode_t(1, 0, 4, 8, 8, 1.0, NULL, 0, 1, 8, NULL, 4, NULL) == kernels.MLS_ERR_ARG  # no out_t
     assert L.mls_e5m2_encode_t(NULL, 0, 0, 8, 8, 1.0, NULL, 0, NULL, 8, NULL, 0, NULL) == 0
+    assert L.mls_e4m3_encode_t(1, 0, 4, 8, 8, 1.0, NULL, 0, 1, 8, 1, 3, NULL) == kernels.MLS_ERR_ARG  # ldt < rows
+    assert L.mls_e4m3_encode_t(1, 7, 4, 8, 8, 1.0, NULL, 0, 1, 8, 1, 4, NULL) == kernels.MLS_ERR_ARG  # x dtype
     assert L.mls_transpose_u8(1, 4, 8, 4, 1, 4, NULL) == kernels.MLS_ERR_ARG                  # lds < cols
     assert L.mls_transpose_u8(1, 4, 8, 8, 1, 3, NULL) == kernels.MLS_ERR_ARG                  # ldd < rows
     assert L.mls_transpose_u8(NULL, 0, 8, 8, NULL, 0, NULL) == 0

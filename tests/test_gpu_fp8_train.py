@@ -187,6 +187,7 @@ def test_fp8_linear_backward_config_d(dev):
         assert excess <= 0, f"{what} at config D's shape: worst excess {excess:.3g}"
 
 
+@pytest.mark.parametrize("fmt", ["e5m2", "e4m3"])
 @pytest.mark.parametrize("R,C,dtype,per_row,off", [
     (256, 512, torch.float32, False, 0),     # whole 64 x 64 tiles
     (130, 300, torch.float32, True, 0),      # ragged edge tiles, per-row scales
@@ -196,10 +197,12 @@ def test_fp8_linear_backward_config_d(dev):
     (96, 128, torch.float32, False, 4),      # strided rows: the byte path for the input
     (4096, 8192, torch.float32, False, 0),   # config D's gradient
 ])
-def test_quantize_e5m2_t(dev, R, C, dtype, per_row, off):
-    """One-pass encode + transpose: both outputs bit-identical to quantize_e5m2 and its
-    byte transpose, boundaries, NaN and saturation included."""
-    from kernels.fp8_matmul import quantize_e5m2_t
+def test_quantize_fp8_t(dev, R, C, dtype, per_row, off, fmt):
+    """One-pass encode + transpose: both outputs bit-identical to quantize_e5m2 /
+    quantize_e4m3 and its byte transpose, boundaries, NaN and saturation included."""
+    from kernels.fp8_matmul import quantize_e4m3, quantize_e4m3_t, quantize_e5m2_t
+    enc_t, enc = (quantize_e5m2_t, quantize_e5m2) if fmt == "e5m2" else (quantize_e4m3_t, quantize_e4m3)
+    oracle = ref.quantize_e5m2 if fmt == "e5m2" else ref.quantize_e4m3
     g = torch.Generator().manual_seed(R * 7 + C)
     x = torch.randn(R, C + off, generator=g) * 3e3
     pts = torch.from_numpy(_boundaries())
@@ -208,11 +211,25 @@ def test_quantize_e5m2_t(dev, R, C, dtype, per_row, off):
     xd = x.to(dtype).to(dev)
     xs = xd[:, off:] if off else xd
     scale = (torch.rand(R, 1, generator=g) + 0.25).to(dev) if per_row else 0.37
-    bits, bits_t = quantize_e5m2_t(xs, scale)
-    want = quantize_e5m2(xs.contiguous(), scale)
+    bits, bits_t = enc_t(xs, scale)
+    want = enc(xs.contiguous(), scale)
     assert bits.shape == (R, C) and bits_t.shape == (C, R) and bits_t.is_contiguous()
     assert torch.equal(bits, want)
     assert torch.equal(bits_t, want.t().contiguous())
     if R * C <= 64 * 1024:
         sc = scale.cpu().numpy() if per_row else scale
-        assert np.array_equal(bits.cpu().numpy(), ref.quantize_e5m2(xs.float().cpu().numpy(), sc))
+        assert np.array_equal(bits.cpu().numpy(), oracle(xs.float().cpu().numpy(), sc))
+
+
+def test_fp8_linear_no_grad_forward(dev):
+    """Without gradients the kernel forward encodes once (no transposed copies) and gives
+    the same output as the training forward, which writes both layouts."""
+    torch.manual_seed(3)
+    lin = nn.Linear(192, 320, bias=False)
+    m = FP8Linear(lin, use_kernel=True).to(dev)
+    x = torch.randn(2, 33, 192, device=dev)
+    y_train = m(x.clone().requires_grad_(True)).detach()
+    m2 = FP8Linear(lin, use_kernel=True).to(dev)
+    with torch.no_grad():
+        y_inf = m2(x)
+    assert torch.equal(y_train, y_inf)
