@@ -129,3 +129,82 @@ def test_quantized_checkpoint_on_device(dev, tmp_path):
     hl = load_quantized(_Model(), hpath, device=dev)
     for k, v in loaded.state_dict().items():
         assert torch.equal(v, hl.state_dict()[k]), k
+
+
+class _SwiGLU(nn.Module):
+    def __init__(self, d, h):
+        super().__init__()
+        self.w_gate, self.w_up = nn.Linear(d, h, bias=False), nn.Linear(d, h, bias=False)
+        self.w_down = nn.Linear(h, d, bias=False)
+
+    def forward(self, x):
+        return self.w_down(torch.nn.functional.silu(self.w_gate(x)) * self.w_up(x))
+
+
+class _Mix(nn.Module):
+    """A per-token stand-in for attention with the reference's four slots:
+    wo(wv(x) * sigmoid(wq(x) + wk(x)))."""
+
+    def __init__(self, d):
+        super().__init__()
+        self.wq, self.wk, self.wv, self.wo = (nn.Linear(d, d, bias=False) for _ in range(4))
+
+    def forward(self, x):
+        return self.wo(self.wv(x) * torch.sigmoid(self.wq(x) + self.wk(x)))
+
+
+class _Blk(nn.Module):
+    def __init__(self, d, h):
+        super().__init__()
+        self.attn, self.mlp = _Mix(d), _SwiGLU(d, h)
+
+    def forward(self, x):
+        x = x + self.attn(x)
+        return x + self.mlp(x)
+
+
+class _Net(nn.Module):
+    """Input projection and head in full precision, two residual blocks with the
+    reference's block layout and slot names (what quantize_model swaps)."""
+
+    def __init__(self, d_in=64, d=128, h=256, classes=10):
+        super().__init__()
+        self.inp = nn.Linear(d_in, d, bias=False)
+        self.blocks = nn.ModuleList(_Blk(d, h) for _ in range(2))
+        self.head = nn.Linear(d, classes, bias=False)
+
+    def forward(self, x):
+        z = self.inp(x)
+        for b in self.blocks:
+            z = b(z)
+        return self.head(z)
+
+
+def test_quantized_model_accuracy(dev):
+    """test_quantize.py:62-85 of the reference on the kernel path: train briefly in fp32,
+    then the INT8 (INT4 g32) quantized model, run through the HIP kernels, loses at most
+    3% (30%) of cross-entropy."""
+    import torch.nn.functional as F
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(4096, 64, generator=g, device=dev)
+    y = (x @ torch.randn(64, 10, generator=g, device=dev)).argmax(1)
+    torch.manual_seed(5)
+    m = _Net().to(dev)
+    opt = torch.optim.Adam(m.parameters(), lr=1e-3)
+    gb = torch.Generator(device=dev).manual_seed(1)
+    for _ in range(60):
+        idx = torch.randint(0, 4096, (64,), generator=gb, device=dev)
+        loss = F.cross_entropy(m(x[idx]), y[idx])
+        opt.zero_grad()
+        loss.backward()
+        opt.step()
+    xe = x[:512].to(torch.bfloat16)
+    with torch.no_grad():
+        fp = float(F.cross_entropy(m.to(torch.bfloat16)(xe).float(), y[:512]))
+        q8 = quantize_model(m, bits=8, use_kernel=True)
+        q4 = quantize_model(m, bits=4, group_size=32, use_kernel=True)
+        l8 = float(F.cross_entropy(q8(xe).float(), y[:512]))
+        l4 = float(F.cross_entropy(q4(xe).float(), y[:512]))
+    assert sum(isinstance(mm, QuantLinear) for mm in q8.modules()) == 14
+    assert l8 < fp * 1.03, f"int8 {l8:.4f} vs fp {fp:.4f}"
+    assert l4 < fp * 1.30, f"int4 {l4:.4f} vs fp {fp:.4f}"

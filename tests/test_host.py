@@ -180,6 +180,31 @@ def test_fp8_linear_emulation_on_host():
     assert E4M3_MAX == 448.0
 
 
+def test_scale1_underflows_small_values():
+    """test_fp8.py:51-59 of the reference, on the host codec: gradient-sized values flush
+    to zero at scale 1.0 and survive at the amax scale (what dynamic scaling is for)."""
+    torch.manual_seed(0)
+    g = torch.randn(1000) * 1e-4
+    dead = dequantize_e4m3(quantize_e4m3(g, 1.0), 1.0)
+    s = float(g.abs().amax()) / E4M3_MAX
+    alive = dequantize_e4m3(quantize_e4m3(g, s), s)
+    assert (dead == 0).float().mean() > 0.5
+    assert (alive == 0).float().mean() < 0.01
+
+
+def test_delayed_scaler_tracks_amax():
+    """test_fp8.py:62-71 of the reference: the first call uses the just-in-time amax, later
+    calls the amax history, which forgets after `history` calls."""
+    from train.fp8 import DynamicScaler
+    s = DynamicScaler(history=4)
+    t = torch.ones(10)
+    assert abs(s.scale_for(t * 448) - 1.0) < 1e-6
+    assert abs(s.scale_for(t) - 1.0) < 1e-6
+    for _ in range(4):
+        s.scale_for(t)
+    assert s.scale_for(t) < 0.01
+
+
 # ------------------------------------------------------------------ quantized checkpoints
 
 
