@@ -20,47 +20,47 @@ __device__ __forceinline__ float e4m3_value(uint32_t b, bool nan_to_zero) {
   return (b & 0x80u) ? -mag : mag;
 }
 
+// The encoders below are straight-line (selects, no branches): the data decides between
+// the subnormal and normal grids per element, and lanes of one wavefront disagree.
+
 // e4m3 code of a finite magnitude 0 <= a <= 448, round to nearest, ties to even.
 __device__ __forceinline__ uint32_t e4m3_code_of_mag(float a) {
   const uint32_t u = __float_as_uint(a);
-  if (u < 0x3C800000u)  // a < 2^-6: the subnormal grid has step 2^-9; code 8 is 2^-6
-    return (uint32_t)__builtin_rintf(a * 512.0f);
-  // a >= 2^-6: fp32 exponent field E >= 121. Keep the 3 top mantissa bits and
-  // rebias the exponent (127 -> 7); a carry out of the mantissa bumps the exponent.
-  uint32_t code = (u >> 20) - (120u << 3);
-  const uint32_t rem = u & 0xFFFFFu;
-  if (rem > 0x80000u || (rem == 0x80000u && (code & 1u))) code += 1u;
-  return code;
+  // a < 2^-6: the subnormal grid has step 2^-9 (code 8 is 2^-6)
+  const uint32_t sub = (uint32_t)__builtin_rintf(a * 512.0f);
+  // a >= 2^-6 (fp32 exponent field >= 121): round the fp32 pattern to its top 3 mantissa
+  // bits, ties to even (add half - 1 plus the kept bit), and rebias the exponent
+  // (127 -> 7); a carry out of the mantissa bumps the exponent.
+  const uint32_t nrm = ((u + 0x7FFFFu + ((u >> 20) & 1u)) >> 20) - (120u << 3);
+  return u < 0x3C800000u ? sub : nrm;
 }
 
 // Saturating encode of q (already divided by the scale): NaN -> 0x7F | sign,
 // otherwise clamp |q| to 448 and round.
 __device__ __forceinline__ uint32_t e4m3_encode(float q) {
   const uint32_t sign = (__float_as_uint(q) >> 24) & 0x80u;
-  if (__builtin_isnan(q)) return 0x7Fu | sign;
-  return e4m3_code_of_mag(fminf(fabsf(q), 448.0f)) | sign;
+  const uint32_t code = e4m3_code_of_mag(fminf(fabsf(q), 448.0f));
+  return (__builtin_isnan(q) ? 0x7Fu : code) | sign;
 }
 
 // e5m2 code of a finite magnitude 0 <= a <= 57344, round to nearest, ties to even.
 // e5m2: 1 sign, 5 exponent bits (bias 15), 2 mantissa bits; subnormals m/4 * 2^-14.
 __device__ __forceinline__ uint32_t e5m2_code_of_mag(float a) {
   const uint32_t u = __float_as_uint(a);
-  if (u < 0x38800000u)  // a < 2^-14: the subnormal grid has step 2^-16; code 4 is 2^-14
-    return (uint32_t)__builtin_rintf(a * 65536.0f);
-  // a >= 2^-14: fp32 exponent field E >= 113. Keep the 2 top mantissa bits and rebias
-  // the exponent (127 -> 15); a carry out of the mantissa bumps the exponent.
-  uint32_t code = (u >> 21) - (112u << 2);
-  const uint32_t rem = u & 0x1FFFFFu;
-  if (rem > 0x100000u || (rem == 0x100000u && (code & 1u))) code += 1u;
-  return code;
+  // a < 2^-14: the subnormal grid has step 2^-16 (code 4 is 2^-14)
+  const uint32_t sub = (uint32_t)__builtin_rintf(a * 65536.0f);
+  // a >= 2^-14 (fp32 exponent field >= 113): round to the top 2 mantissa bits, ties to
+  // even, and rebias the exponent (127 -> 15); a mantissa carry bumps the exponent.
+  const uint32_t nrm = ((u + 0xFFFFFu + ((u >> 21) & 1u)) >> 21) - (112u << 2);
+  return u < 0x38800000u ? sub : nrm;
 }
 
 // The reference's e5m2 quantization of q (already divided by the scale): clamp to
 // +-57344 (the largest finite e5m2), round; NaN -> 0x7F | sign.
 __device__ __forceinline__ uint32_t e5m2_encode(float q) {
   const uint32_t sign = (__float_as_uint(q) >> 24) & 0x80u;
-  if (__builtin_isnan(q)) return 0x7Fu | sign;
-  return e5m2_code_of_mag(fminf(fabsf(q), 57344.0f)) | sign;
+  const uint32_t code = e5m2_code_of_mag(fminf(fabsf(q), 57344.0f));
+  return (__builtin_isnan(q) ? 0x7Fu : code) | sign;
 }
 
 // vec: bits/out are 16-byte aligned, so the bulk is read 16 bytes per thread.
