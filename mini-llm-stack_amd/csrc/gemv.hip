@@ -139,10 +139,20 @@ __device__ __forceinline__ float load_x_chunk(const AT* __restrict__ xrow, int c
   return x_from_raw<WBITS, AT>(raw, xr);
 }
 
+// (a & m) | c in one instruction. gfx9-family VOP3 encodings take no 32-bit literal,
+// so with literal constants the compiler splits this into v_and_b32 + v_or_b32; the
+// callers pass m and c in VGPRs (made opaque once per kernel) instead.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
+  return r;
+}
+
 // sum_k x_k * u_k over one 16-byte weight chunk, where u_k is the biased code
 // (INT4: nibble + bias of the 16-bit path, or the raw nibble for fp32; INT8: q + 128).
+// nib_mask / magic: 0x000F000F and the 16-bit path's bias pattern, held in registers.
 template <int WBITS, typename AT>
-__device__ __forceinline__ float chunk_dot(const uint4 wq, const uint32_t* xr) {
+__device__ __forceinline__ float chunk_dot(const uint4 wq, const uint32_t* xr, uint32_t nib_mask, uint32_t magic) {
   using S = XSlot<WBITS, AT>;
   const uint32_t q[4] = {wq.x, wq.y, wq.z, wq.w};
   float acc = 0.0f;
@@ -165,10 +175,10 @@ __device__ __forceinline__ float chunk_dot(const uint4 wq, const uint32_t* xr) {
       using H = Half16<AT>;
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const uint32_t p0 = (q[b] & 0x000F000Fu) | H::MAGIC4;
-        const uint32_t p1 = ((q[b] >> 4) & 0x000F000Fu) | H::MAGIC4;
-        const uint32_t p2 = ((q[b] >> 8) & 0x000F000Fu) | H::MAGIC4;
-        const uint32_t p3 = ((q[b] >> 12) & 0x000F000Fu) | H::MAGIC4;
+        const uint32_t p0 = and_or(q[b], nib_mask, magic);
+        const uint32_t p1 = and_or(q[b] >> 4, nib_mask, magic);
+        const uint32_t p2 = and_or(q[b] >> 8, nib_mask, magic);
+        const uint32_t p3 = and_or(q[b] >> 12, nib_mask, magic);
         acc = H::dot2(p0, xr[4 * b + 0], acc);
         acc = H::dot2(p1, xr[4 * b + 1], acc);
         acc = H::dot2(p2, xr[4 * b + 2], acc);
@@ -261,7 +271,11 @@ __global__ __launch_bounds__(256) void gemv_wq_kernel(
 #pragma unroll
     for (int j = 0; j < CPL; ++j) osx[mi][j] = OFF * x_from_raw<WBITS, AT>(xraw[mi][j], xr[mi][j]);
 
-  // 3. dot products
+  // 3. dot products. The INT4 16-bit path's widening constants live in VGPRs (an empty
+  // asm hides their values, so they are not re-materialised as literals; see and_or).
+  uint32_t nib_mask = 0x000F000Fu, magic = 0;
+  if constexpr (WBITS == 4 && !S::F32) magic = Half16<AT>::MAGIC4;
+  asm volatile("" : "+v"(nib_mask), "+v"(magic));
   float part[MT * R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -270,7 +284,7 @@ __global__ __launch_bounds__(256) void gemv_wq_kernel(
       float acc = 0.0f;
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
-        float d = chunk_dot<WBITS, AT>(wv[r][j], xr[mi][j]) - osx[mi][j];
+        float d = chunk_dot<WBITS, AT>(wv[r][j], xr[mi][j], nib_mask, magic) - osx[mi][j];
         if (64 * (j + 1) > nchunks && lane + 64 * j >= nchunks) d = 0.0f;  // past K
         if constexpr (WBITS == 4) acc = fmaf(sc[r][j], d, acc);
         else acc += d;
