@@ -139,14 +139,12 @@ __device__ __forceinline__ float load_x_chunk(const AT* __restrict__ xrow, int c
   return x_from_raw<WBITS, AT>(raw, xr);
 }
 
-// (a & m) | c in one instruction. gfx9-family VOP3 encodings take no 32-bit literal,
-// so with literal constants the compiler splits this into v_and_b32 + v_or_b32; the
-// callers pass m and c in VGPRs (made opaque once per kernel) instead.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(m), "v"(c));
-  return r;
-}
+// (a & m) | c, which the compiler selects as one v_and_or_b32 when m and c are in
+// registers. gfx9-family VOP3 encodings take no 32-bit literal, so with literal constants
+// it splits this into v_and_b32 + v_or_b32; the callers pass m and c as values made
+// opaque once per kernel. (Plain code rather than inline asm: the compiler must see the
+// VALU write to insert the wait states an MFMA reading the result needs.)
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) { return (a & m) | c; }
 
 // sum_k x_k * u_k over one 16-byte weight chunk, where u_k is the biased code
 // (INT4: nibble + bias of the 16-bit path, or the raw nibble for fp32; INT8: q + 128).
