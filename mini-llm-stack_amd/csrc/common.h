@@ -74,6 +74,25 @@ __device__ __forceinline__ float dpp_mov(float v) {
 }
 
 namespace detail {
+// For BIT = 32 (16): v_permlane32_swap (v_permlane16_swap) exchanges the lanes of a
+// with lane & BIT set and the lanes of b without it, each with its xor-BIT partner.
+// The sum of the two swapped registers is then, on lanes without BIT, a + a's partner
+// and, on lanes with BIT, b + b's partner: one exchange and one add, no LDS crossbar.
+template <int BIT>
+__device__ __forceinline__ float swap_add(float a, float b) {
+  static_assert(BIT == 16 || BIT == 32, "lane swaps exist for 16 and 32");
+  const uint32_t ua = __builtin_bit_cast(uint32_t, a), ub = __builtin_bit_cast(uint32_t, b);
+  uint32_t lo, hi;
+  if constexpr (BIT == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(ua, ub, false, false);
+    lo = r[0]; hi = r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(ua, ub, false, false);
+    lo = r[0]; hi = r[1];
+  }
+  return __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
+}
+
 // Halves the live values per step: lanes with lane & BIT keep the upper half,
 // the others the lower half, each adding its xor-partner's copy. With one value
 // left, the lane bits BIT..0 are summed (lowest first, so the mirror patterns
@@ -82,12 +101,17 @@ template <int N, int BIT>
 __device__ __forceinline__ void reduce_split(float* v, int lane) {
   if constexpr (N > 1) {
     constexpr int H = N / 2;
-    const bool upper = (lane & BIT) != 0;
+    if constexpr (BIT >= 16) {
 #pragma unroll
-    for (int i = 0; i < H; ++i) {
-      const float send = upper ? v[i] : v[i + H];
-      const float keep = upper ? v[i + H] : v[i];
-      v[i] = keep + __shfl_xor(send, BIT, 64);
+      for (int i = 0; i < H; ++i) v[i] = swap_add<BIT>(v[i], v[i + H]);
+    } else {
+      const bool upper = (lane & BIT) != 0;
+#pragma unroll
+      for (int i = 0; i < H; ++i) {
+        const float send = upper ? v[i] : v[i + H];
+        const float keep = upper ? v[i + H] : v[i];
+        v[i] = keep + __shfl_xor(send, BIT, 64);
+      }
     }
     reduce_split<H, BIT / 2>(v, lane);
   } else {
@@ -95,8 +119,8 @@ __device__ __forceinline__ void reduce_split(float* v, int lane) {
     if constexpr (BIT >= 2) v[0] += dpp_mov<0x4E>(v[0]);   // quad_perm [2,3,0,1]: lane ^ 2
     if constexpr (BIT >= 4) v[0] += dpp_mov<0x141>(v[0]);  // row_half_mirror: the other quad
     if constexpr (BIT >= 8) v[0] += dpp_mov<0x140>(v[0]);  // row_mirror: the other octet
-    if constexpr (BIT >= 16) v[0] += __shfl_xor(v[0], 16, 64);
-    if constexpr (BIT >= 32) v[0] += __shfl_xor(v[0], 32, 64);
+    if constexpr (BIT >= 16) v[0] = swap_add<16>(v[0], v[0]);
+    if constexpr (BIT >= 32) v[0] = swap_add<32>(v[0], v[0]);
   }
 }
 }  // namespace detail
