@@ -134,6 +134,22 @@ __device__ __forceinline__ void wave_reduce_many(float (&v)[V]) {
   detail::reduce_split<V, 32>(v, threadIdx.x & 63);
 }
 
+// Sum over each aligned group of W lanes (W a power of two, <= 64); every lane of a
+// group receives its group's total, bit-identical to an xor-shuffle butterfly. After
+// the two quad steps all lanes of a quad hold the same sum, so the mirror patterns
+// fetch exactly the value the xor-4 / xor-8 partner holds; 16 and 32 use lane swaps.
+template <int W>
+__device__ __forceinline__ float lane_group_sum(float s) {
+  static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "W must be a power of two <= 64");
+  if constexpr (W >= 2) s += dpp_mov<0xB1>(s);   // lane ^ 1
+  if constexpr (W >= 4) s += dpp_mov<0x4E>(s);   // lane ^ 2
+  if constexpr (W >= 8) s += dpp_mov<0x141>(s);  // row_half_mirror: the other quad
+  if constexpr (W >= 16) s += dpp_mov<0x140>(s); // row_mirror: the other octet
+  if constexpr (W >= 32) s = detail::swap_add<16>(s, s);
+  if constexpr (W >= 64) s = detail::swap_add<32>(s, s);
+  return s;
+}
+
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -11,8 +11,8 @@
 // per (sequence, head, context split). Lane l owns the 16-byte chunk `l % CPT` of
 // token slot `l / CPT` (CPT = 16-byte chunks per row), so one load instruction
 // covers 64 / CPT whole rows and each lane keeps only its EPC elements of q and of
-// the output accumulator. A row's score is reduced over its CPT lanes with xor
-// shuffles. Each lane runs its own online softmax (running max m, sum l,
+// the output accumulator. A row's score is reduced over its CPT lanes with DPP moves
+// and lane swaps (no LDS crossbar). Each lane runs its own online softmax (running max m, sum l,
 // accumulator) over the tokens it sees; at the end the 64 / CPT token slots are
 // merged pairwise (rescaling by exp(m - M)), then, when the context is split over
 // several wavefronts, a second kernel merges the splits the same way from a
@@ -142,8 +142,7 @@ __global__ __launch_bounds__(256) void paged_attn_kernel(const PagedArgs a) {
       float s = 0.0f;
 #pragma unroll
       for (int e = 0; e < EPC; ++e) s = fmaf(q[e], kv[e], s);
-#pragma unroll
-      for (int o = 1; o < CPT; o <<= 1) s += __shfl_xor(s, o);
+      s = lane_group_sum<CPT>(s);
       const int t = t0 + u * TPI + ts;
       sc[u] = (ok && t < a.BS && b * a.BS + t < ctx) ? s * a.scale : NEG_INF;
       mx = fmaxf(mx, sc[u]);
