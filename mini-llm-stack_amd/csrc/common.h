@@ -74,25 +74,6 @@ __device__ __forceinline__ float dpp_mov(float v) {
 }
 
 namespace detail {
-// For BIT = 32 (16): v_permlane32_swap (v_permlane16_swap) exchanges the lanes of a
-// with lane & BIT set and the lanes of b without it, each with its xor-BIT partner.
-// The sum of the two swapped registers is then, on lanes without BIT, a + a's partner
-// and, on lanes with BIT, b + b's partner: one exchange and one add, no LDS crossbar.
-template <int BIT>
-__device__ __forceinline__ float swap_add(float a, float b) {
-  static_assert(BIT == 16 || BIT == 32, "lane swaps exist for 16 and 32");
-  const uint32_t ua = __builtin_bit_cast(uint32_t, a), ub = __builtin_bit_cast(uint32_t, b);
-  uint32_t lo, hi;
-  if constexpr (BIT == 32) {
-    const auto r = __builtin_amdgcn_permlane32_swap(ua, ub, false, false);
-    lo = r[0]; hi = r[1];
-  } else {
-    const auto r = __builtin_amdgcn_permlane16_swap(ua, ub, false, false);
-    lo = r[0]; hi = r[1];
-  }
-  return __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
-}
-
 // Halves the live values per step: lanes with lane & BIT keep the upper half,
 // the others the lower half, each adding its xor-partner's copy. With one value
 // left, the lane bits BIT..0 are summed (lowest first, so the mirror patterns
@@ -101,17 +82,12 @@ template <int N, int BIT>
 __device__ __forceinline__ void reduce_split(float* v, int lane) {
   if constexpr (N > 1) {
     constexpr int H = N / 2;
-    if constexpr (BIT >= 16) {
+    const bool upper = (lane & BIT) != 0;
 #pragma unroll
-      for (int i = 0; i < H; ++i) v[i] = swap_add<BIT>(v[i], v[i + H]);
-    } else {
-      const bool upper = (lane & BIT) != 0;
-#pragma unroll
-      for (int i = 0; i < H; ++i) {
-        const float send = upper ? v[i] : v[i + H];
-        const float keep = upper ? v[i + H] : v[i];
-        v[i] = keep + __shfl_xor(send, BIT, 64);
-      }
+    for (int i = 0; i < H; ++i) {
+      const float send = upper ? v[i] : v[i + H];
+      const float keep = upper ? v[i + H] : v[i];
+      v[i] = keep + __shfl_xor(send, BIT, 64);
     }
     reduce_split<H, BIT / 2>(v, lane);
   } else {
@@ -119,8 +95,8 @@ __device__ __forceinline__ void reduce_split(float* v, int lane) {
     if constexpr (BIT >= 2) v[0] += dpp_mov<0x4E>(v[0]);   // quad_perm [2,3,0,1]: lane ^ 2
     if constexpr (BIT >= 4) v[0] += dpp_mov<0x141>(v[0]);  // row_half_mirror: the other quad
     if constexpr (BIT >= 8) v[0] += dpp_mov<0x140>(v[0]);  // row_mirror: the other octet
-    if constexpr (BIT >= 16) v[0] = swap_add<16>(v[0], v[0]);
-    if constexpr (BIT >= 32) v[0] = swap_add<32>(v[0], v[0]);
+    if constexpr (BIT >= 16) v[0] += __shfl_xor(v[0], 16, 64);
+    if constexpr (BIT >= 32) v[0] += __shfl_xor(v[0], 32, 64);
   }
 }
 }  // namespace detail
@@ -137,7 +113,7 @@ __device__ __forceinline__ void wave_reduce_many(float (&v)[V]) {
 // Sum over each aligned group of W lanes (W a power of two, <= 64); every lane of a
 // group receives its group's total, bit-identical to an xor-shuffle butterfly. After
 // the two quad steps all lanes of a quad hold the same sum, so the mirror patterns
-// fetch exactly the value the xor-4 / xor-8 partner holds; 16 and 32 use lane swaps.
+// fetch exactly the value the xor-4 / xor-8 partner holds.
 template <int W>
 __device__ __forceinline__ float lane_group_sum(float s) {
   static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "W must be a power of two <= 64");
@@ -145,8 +121,21 @@ __device__ __forceinline__ float lane_group_sum(float s) {
   if constexpr (W >= 4) s += dpp_mov<0x4E>(s);   // lane ^ 2
   if constexpr (W >= 8) s += dpp_mov<0x141>(s);  // row_half_mirror: the other quad
   if constexpr (W >= 16) s += dpp_mov<0x140>(s); // row_mirror: the other octet
-  if constexpr (W >= 32) s = detail::swap_add<16>(s, s);
-  if constexpr (W >= 64) s = detail::swap_add<32>(s, s);
+  if constexpr (W >= 32) s += __shfl_xor(s, 16, 64);
+  if constexpr (W >= 64) s += __shfl_xor(s, 32, 64);
+  return s;
+}
+
+// Maximum over each aligned group of W lanes, by the same pattern as lane_group_sum.
+template <int W>
+__device__ __forceinline__ float lane_group_max(float s) {
+  static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "W must be a power of two <= 64");
+  if constexpr (W >= 2) s = fmaxf(s, dpp_mov<0xB1>(s));
+  if constexpr (W >= 4) s = fmaxf(s, dpp_mov<0x4E>(s));
+  if constexpr (W >= 8) s = fmaxf(s, dpp_mov<0x141>(s));
+  if constexpr (W >= 16) s = fmaxf(s, dpp_mov<0x140>(s));
+  if constexpr (W >= 32) s = fmaxf(s, __shfl_xor(s, 16, 64));
+  if constexpr (W >= 64) s = fmaxf(s, __shfl_xor(s, 32, 64));
   return s;
 }
 
@@ -157,11 +146,7 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return lane_group_max<64>(v); }
 
 // Remaps a linear workgroup id so that consecutive logical tiles land on the same
 // XCD. The dispatcher hands workgroup i to XCD i % 8; logical tile t is executed by

@@ -12,7 +12,7 @@
 // token slot `l / CPT` (CPT = 16-byte chunks per row), so one load instruction
 // covers 64 / CPT whole rows and each lane keeps only its EPC elements of q and of
 // the output accumulator. A row's score is reduced over its CPT lanes with DPP moves
-// and lane swaps (no LDS crossbar). Each lane runs its own online softmax (running max m, sum l,
+// (up to 16 lanes; wider rows add xor shuffles). Each lane runs its own online softmax (running max m, sum l,
 // accumulator) over the tokens it sees; at the end the 64 / CPT token slots are
 // merged pairwise (rescaling by exp(m - M)), then, when the context is split over
 // several wavefronts, a second kernel merges the splits the same way from a

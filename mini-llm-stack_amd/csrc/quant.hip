@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void quant_int8_vec_kernel(const float* __rest
 
 // INT4, vector path for power-of-two groups of 8 .. 512: one wavefront per (row, span of
 // 512 k), 8 consecutive k per lane (two 16-byte loads, one 4-byte store of 8 nibbles);
-// a group is GL = group / 8 adjacent lanes, whose amax meets by xor shuffles.
+// a group is GL = group / 8 adjacent lanes, whose amax meets by DPP moves.
 template <int GL>
 __global__ __launch_bounds__(256) void quant_int4_vec_kernel(const float* __restrict__ w, int64_t N, int64_t K,
                                                              int64_t ldw, uint8_t* __restrict__ packed,
@@ -87,8 +87,7 @@ __global__ __launch_bounds__(256) void quant_int4_vec_kernel(const float* __rest
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(e[i]));
-#pragma unroll
-  for (int o = 1; o < GL; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+  amax = lane_group_max<GL>(amax);
   if (!on) return;
   const float s = fmaxf(amax / 7.0f, 1e-8f);
   const int64_t G = K / (8 * GL);
