@@ -71,7 +71,10 @@ def test_respects_context_len(dev):
 
 @pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 128), (torch.float16, 64), (torch.bfloat16, 256),
                                      (torch.float32, 16), (torch.float32, 128), (torch.float32, 24),
-                                     (torch.bfloat16, 80), (torch.float16, 8)])
+                                     (torch.bfloat16, 80), (torch.float16, 8),
+                                     # 16-byte chunks per row of 2 and 64: the narrowest and
+                                     # widest lane groups of the score reduction
+                                     (torch.float32, 8), (torch.bfloat16, 512)])
 @pytest.mark.parametrize("bs", [1, 8, 16, 32])
 def test_dtypes_head_dims_block_sizes(dev, dtype, D, bs):
     lens = [1, bs, bs + 1, 3 * bs + 5, 37]
