@@ -87,6 +87,7 @@ extern "C" int mls_int4_grouped_gemm(const void* a, int a_dt, int64_t lda, const
   int rc = validate(fn, 4, g.base, c_dt);
   if (rc != MLS_OK) return rc;
   if (E < 1) return fail(MLS_ERR_ARG, "%s: E=%d < 1", fn, E);
+  if (K < 1) return fail(MLS_ERR_ARG, "%s: K=%lld must be positive", fn, (long long)K);
   if (w_estride < 0 || s_estride < 0) return fail(MLS_ERR_ARG, "%s: negative expert stride", fn);
   if (M_total == 0 || N == 0) return MLS_OK;
   if (!seg_off) return fail(MLS_ERR_ARG, "%s: null seg_off", fn);
@@ -112,6 +113,7 @@ extern "C" int mls_int4_grouped_gate_up(const void* a, int a_dt, int64_t lda, co
   int rc = validate(fn, 4, g.base, h_dt);
   if (rc != MLS_OK) return rc;
   if (E < 1) return fail(MLS_ERR_ARG, "%s: E=%d < 1", fn, E);
+  if (K < 1) return fail(MLS_ERR_ARG, "%s: K=%lld must be positive", fn, (long long)K);
   if (w_estride < 0 || s_estride < 0) return fail(MLS_ERR_ARG, "%s: negative expert stride", fn);
   if (M_total == 0 || H == 0) return MLS_OK;
   if (!seg_off || !wu || !su) return fail(MLS_ERR_ARG, "%s: null pointer", fn);
@@ -141,6 +143,7 @@ extern "C" int mls_int4_grouped_gemm_partial(const void* a, int a_dt, int64_t ld
   int rc = validate(fn, 4, g.base, a_dt);
   if (rc != MLS_OK) return rc;
   if (E < 1) return fail(MLS_ERR_ARG, "%s: E=%d < 1", fn, E);
+  if (K < 1) return fail(MLS_ERR_ARG, "%s: K=%lld must be positive", fn, (long long)K);
   if (splits < 1 || splits > 64) return fail(MLS_ERR_ARG, "%s: splits=%d", fn, splits);
   if (w_estride < 0 || s_estride < 0 || split_stride < M_total * ldp)
     return fail(MLS_ERR_ARG, "%s: bad expert or split stride", fn);

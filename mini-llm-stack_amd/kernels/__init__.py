@@ -6,13 +6,33 @@ Triton: every kernel entry point calls the hand-written HIP library
 ``libmls_hip.so`` (C ABI in include/mls.h) through ctypes, on HIP device tensors
 only. The library is bound on first use; if it is missing, or a CPU tensor
 reaches a kernel entry point, the call raises instead of computing elsewhere.
+
+Overlay. This package replaces only the reference's quantized-linear modules
+(dequant_matmul, fp8_matmul, moe_routing, paged_attention). Its search path is
+extended over every ``kernels`` directory on ``sys.path`` (pkgutil.extend_path),
+so with this directory first and a reference checkout after it, the reference's
+other modules (attention_fwd, attention_bwd, autograd_ops, moe_backward,
+fusion_compiler) import from the checkout and bind this package's GEMMs. Both
+roots must be on ``sys.path`` before the first ``import kernels``.
 """
 
 from __future__ import annotations
 
 import ctypes
 import os
+import pkgutil
 from pathlib import Path
+
+__path__ = pkgutil.extend_path(__path__, __name__)
+
+import torch  # noqa: E402
+
+# The reference's own Triton modules that this package does not replace read the
+# interpreter switch set by the package import on a machine without a GPU
+# (reference kernels/__init__.py:12-13); it is kept so that they behave as before.
+# Nothing in this package uses Triton.
+if not torch.cuda.is_available():
+    os.environ.setdefault("TRITON_INTERPRET", "1")
 
 # The reference exposes whether it runs interpreted (kernels/__init__.py:15).
 # This implementation only ever runs compiled gfx950 code.

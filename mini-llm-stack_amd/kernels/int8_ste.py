@@ -1,9 +1,15 @@
-"""INT8 straight-through-estimator linear on the gfx950 kernels
-(kernels/autograd_ops.py:95-134 of the reference: its INT8 part only).
+"""INT8 straight-through-estimator linear on the gfx950 kernels: the INT8 part of
+the reference's kernels/autograd_ops.py:95-134, under a module name of its own.
 
-Forward: y = int8_matmul(x, W_q, s). Backward: dx = int8_dgrad(dy, W_q, s) on
-the device, and the fp32 master weight receives dyᵀ @ x (a plain fp GEMM with
-nothing quantized in it).
+The reference's autograd_ops also holds the attention and MoE autograd functions
+(autograd_ops.py:22-92), which this build does not replace. With the reference
+checkout on sys.path after this package, the reference's autograd_ops imports
+unchanged and its Int8MatmulSTE binds this package's int8_matmul / int8_dgrad;
+this module serves callers without the checkout.
+
+Forward: y = int8_matmul(x, W_q, s). Backward: dx = int8_dgrad(dy, W_q, s) on the
+device, and the fp32 master weight receives dy^T @ x (a plain fp GEMM with nothing
+quantized in it).
 """
 
 from __future__ import annotations

@@ -32,13 +32,20 @@ def paged_attention_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
         raise ValueError(f"paged_attention_decode: q {tuple(q.shape)}, pools {tuple(k_pool.shape)} / "
                          f"{tuple(v_pool.shape)} do not match")
     scale = scale if scale is not None else D ** -0.5
-    out = torch.empty_like(q)
+    # a fresh dense output whatever q's layout (empty_like would copy q's strides)
+    out = torch.empty(n_seqs, H, D, dtype=q.dtype, device=dev)
     if n_seqs == 0:
         return out
-    if q.stride(2) != 1:
-        q = q.contiguous()
-    if k_pool.stride(3) != 1 or v_pool.stride() != k_pool.stride():
-        k_pool, v_pool = k_pool.contiguous(), v_pool.contiguous()
+    # the library reads q rows with unit inner stride and non-overlapping heads and
+    # sequences (q_sh >= D, q_ss >= H*D); any other layout is copied dense first
+    # (clone, not contiguous(): a size-1 dimension may keep any stride under contiguous())
+    if q.stride(2) != 1 or q.stride(1) < D or q.stride(0) < H * D:
+        q = q.clone(memory_format=torch.contiguous_format)
+    st = k_pool.stride()
+    if (st[3] != 1 or st[2] < D or st[1] < st[2] * block_size or st[0] < st[1] * H
+            or v_pool.stride() != st):
+        k_pool = k_pool.clone(memory_format=torch.contiguous_format)
+        v_pool = v_pool.clone(memory_format=torch.contiguous_format)
     bt = block_tables.to(torch.int32).contiguous()
     ctx = context_lens.to(torch.int32).contiguous()
     if bt.dim() != 2 or bt.shape[0] != n_seqs or ctx.shape != (n_seqs,):
@@ -52,7 +59,7 @@ def paged_attention_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.
         q.data_ptr(), dt_code(q.dtype, "paged_attention_decode q"), q.stride(0), q.stride(1),
         k_pool.data_ptr(), v_pool.data_ptr(), dt_code(k_pool.dtype, "paged_attention_decode pools"),
         k_pool.stride(0), k_pool.stride(1), k_pool.stride(2), num_blocks,
-        bt.data_ptr(), bt.stride(0), max_blocks, ctx.data_ptr(),
+        bt.data_ptr(), bt.stride(0) if n_seqs > 1 else max_blocks, max_blocks, ctx.data_ptr(),
         out.data_ptr(), out.stride(0), out.stride(1), n_seqs, H, D, block_size, float(scale),
         ws.data_ptr(), ws_n, stream(dev)), "paged_attention_decode")
     return out

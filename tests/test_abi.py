@@ -107,6 +107,22 @@ def test_grouped_rejects():
                                    1, kernels.MLS_F32, 16, 16, 64, NULL) == kernels.MLS_ERR_UNSUPPORTED
 
 
+def test_grouped_reject_empty_k():
+    """K = 0 passes the K % 64 and K % group checks; the grouped kernels would then read
+    scales before the buffer, so the host rejects it first (all three entry points)."""
+    L = kernels.load_library()
+    bf = kernels.MLS_BF16
+    rc, msg = _err(L.mls_int4_grouped_gemm(1, bf, 64, 1, 2, 8, 1, 0, 32, 1, kernels.MLS_F16, 0, 2, 1, 32,
+                                           1, bf, 16, 16, 0, NULL))
+    assert rc == kernels.MLS_ERR_ARG and "K=0" in msg
+    rc, msg = _err(L.mls_int4_grouped_gate_up(1, bf, 64, 1, 2, 8, 1, 1, 0, 32, 1, 1, kernels.MLS_F16, 0, 2, 1,
+                                              32, 1, bf, 16, 16, 0, NULL))
+    assert rc == kernels.MLS_ERR_ARG and "K=0" in msg
+    rc, msg = _err(L.mls_int4_grouped_gemm_partial(1, bf, 64, 1, 2, 8, 1, 0, 32, 1, kernels.MLS_F16, 0, 2, 1,
+                                                   32, 1, 1, 16, 128, 16, 0, NULL))
+    assert rc == kernels.MLS_ERR_ARG and "K=0" in msg
+
+
 def test_gate_up_and_combine_reject():
     L = kernels.load_library()
     bf = kernels.MLS_BF16

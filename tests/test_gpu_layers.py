@@ -9,7 +9,7 @@ import torch.nn as nn
 
 from oracle import ref
 
-from kernels.autograd_ops import Int8MatmulSTE
+from kernels.int8_ste import Int8MatmulSTE, QuantLinearSTE
 from serve.quantize import QuantLinear, dequantize_int8, quantize_int8, quantize_model
 
 pytestmark = pytest.mark.gpu
@@ -66,6 +66,44 @@ def test_int8_ste_matches_reference(dev):
     _close(y.detach(), ref_y.detach(), "STE forward")
     _close(x.grad, x2.grad, "STE input grad")
     _close(master.grad, dy.t() @ x.detach(), "STE master grad")
+
+
+def test_quant_ste_linear_grads(dev):
+    """QuantLinearSTE (reference kernels/autograd_ops.py:120-134) on a 3-d input: the
+    forward quantizes the fp32 master on the device and runs int8_matmul, the input
+    gradient is int8_dgrad of the re-quantized weight and the master receives dy^T x."""
+    torch.manual_seed(3)
+    lin = QuantLinearSTE(48, 40).to(dev)
+    x = torch.randn(2, 7, 48, device=dev, requires_grad=True)
+    y = lin(x)
+    assert y.shape == (2, 7, 40)
+    w_q, s = quantize_int8(lin.weight.detach().cpu())  # host quantizer: bit-identical bytes
+    wd = dequantize_int8(w_q, s).to(dev)
+    _close(y.detach(), x.detach() @ wd.t(), "QuantLinearSTE forward")
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    _close(x.grad, dy @ wd, "QuantLinearSTE input grad")
+    _close(lin.weight.grad, dy.reshape(-1, 40).t() @ x.detach().reshape(-1, 48), "QuantLinearSTE master grad")
+
+
+def test_quant_ste_linear_learns(dev):
+    """test_backward.py:173-190 on the device: a toy regression through the INT8 kernel
+    forward and the int8_dgrad backward must collapse the loss."""
+    torch.manual_seed(2)
+    w_true = torch.randn(16, 32, device=dev)
+    lin = QuantLinearSTE(32, 16).to(dev)
+    opt = torch.optim.Adam(lin.parameters(), lr=3e-2)
+    first = last = None
+    for step in range(150):
+        x = torch.randn(64, 32, device=dev)
+        loss = ((lin(x) - x @ w_true.t()) ** 2).mean()
+        opt.zero_grad()
+        loss.backward()
+        opt.step()
+        if step == 0:
+            first = loss.item()
+        last = loss.item()
+    assert last < first * 0.1, f"loss {first:.3f} -> {last:.3f}"
 
 
 def test_fp8_linear_kernel_vs_emulation(dev):

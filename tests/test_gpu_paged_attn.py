@@ -124,6 +124,30 @@ def test_zero_context_and_invalid_blocks(dev):
         assert np.allclose(out[2, h].numpy(), ref.attention(q[2, h].numpy(), k, v, D ** -0.5), rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("layout", ["heads_major", "one_seq_odd_stride", "one_head_odd_stride"])
+def test_query_layouts(dev, layout):
+    """Dense but permuted or size-1-strided queries (the reference makes q contiguous
+    and accepts any layout): the output is a fresh dense [n_seqs, H, D] tensor equal
+    to the result for the contiguous query."""
+    lens = [9, 30, 17] if layout != "one_seq_odd_stride" else [25]
+    H = 1 if layout == "one_head_odd_stride" else 4
+    kp, vp, tab, ctx = _cache(lens, H, 32, 8, 24, 11)
+    g = torch.Generator().manual_seed(12)
+    n = len(lens)
+    if layout == "heads_major":          # strides (D, n*D, 1): x.transpose(0, 1)
+        q = torch.randn(H, n, 32, generator=g).to(dev).transpose(0, 1)
+    elif layout == "one_seq_odd_stride":  # [1, H, D] view whose seq stride is below H*D
+        q = torch.randn(H, 32, generator=g).to(dev).unsqueeze(0).as_strided((1, H, 32), (1, 32, 1))
+    else:                                # [n, 1, D] view whose head stride is below D
+        q = torch.randn(n, 32, generator=g).to(dev).as_strided((n, 1, 32), (32, 1, 1))
+    out = paged_attention_decode(q, kp.to(dev), vp.to(dev), tab.to(dev), ctx.to(dev))
+    assert out.shape == (n, H, 32) and out.is_contiguous()
+    dense = paged_attention_decode(q.contiguous(), kp.to(dev), vp.to(dev), tab.to(dev), ctx.to(dev))
+    assert torch.equal(out, dense)
+    _check(out, ref.paged_attention_decode(q.cpu().numpy(), kp.numpy(), vp.numpy(), tab.numpy(),
+                                           ctx.numpy()), layout)
+
+
 def test_large_batch_against_torch(dev):
     """A serving-sized batch (64 sequences, 8 heads, D=128, bf16, contexts up to 700)
     against torch's attention on gathered contiguous K/V in fp32."""
