@@ -511,3 +511,43 @@ def test_planted_mistakes_fail_the_pins():
     w = g.random((6, 2))
     pos = g.permutation(12).reshape(6, 2)
     assert not np.allclose(ref.combine_rows(x, w, pos.T.reshape(6, 2)), (x[pos] * w[..., None]).sum(1))
+
+
+# ------------------------------------------------------------------ the reference's torch CPU path
+
+
+def test_torch_cpu_path_matches_oracle():
+    """oracle/torch_cpu.py (the op sequences bench.py's cpu_baseline times) against the
+    numpy oracle: dequantizers bit for bit on the golden quantizer fixtures, the
+    QuantLinear(use_kernel=False) linear and the FP8 emulation within the fp32 bound,
+    the 16-bit linear after its weight rounding to x's dtype within the bf16 bound."""
+    from oracle import torch_cpu as tc
+    d8 = golden("quant_int8")
+    wq8, s8 = torch.from_numpy(d8["w_q"]), torch.from_numpy(d8["scale"])
+    assert np.array_equal(tc.dequantize_int8(wq8, s8).numpy(), ref.dequantize_int8(d8["w_q"], d8["scale"]))
+    g = np.random.default_rng(21)
+    for gs in (32, 128):
+        w = (g.standard_normal((48, 256)) * 0.02).astype(np.float32)
+        p, s = ref.quantize_int4(w, gs)
+        got = tc.dequantize_int4(torch.from_numpy(p), torch.from_numpy(s), gs).numpy()
+        assert np.array_equal(got, ref.dequantize_int4(p, s, gs))
+        x = g.standard_normal((3, 256)).astype(np.float32)
+        y = tc.quant_linear(torch.from_numpy(x), torch.from_numpy(p), torch.from_numpy(s), 4, gs).numpy()
+        assert ref.close_fp32(y, ref.int4_matmul(x, p, s, gs))[0]
+        yb = tc.quant_linear(torch.from_numpy(x).bfloat16(), torch.from_numpy(p), torch.from_numpy(s).half(), 4, gs)
+        assert yb.dtype == torch.bfloat16
+        assert ref.close_bf16(yb.float().numpy(), ref.int4_matmul(x, p, s.astype(np.float16), gs))[0]
+    x = g.standard_normal((5, d8["w_q"].shape[1])).astype(np.float32)
+    y = tc.quant_linear(torch.from_numpy(x), wq8, s8, 8).numpy()
+    assert ref.close_fp32(y, ref.int8_matmul(x, d8["w_q"], d8["scale"]))[0]
+    a, b = g.standard_normal((9, 64)).astype(np.float32), g.standard_normal((7, 64)).astype(np.float32)
+    sa, sb = np.abs(a).max(1) / 448, np.abs(b).max(1) / 448
+    ab, bb = ref.quantize_e4m3(a, sa[:, None]), ref.quantize_e4m3(b, sb[:, None])
+    y = tc.fp8_linear_emulated(torch.from_numpy(ab), torch.from_numpy(bb), torch.from_numpy(sa)[:, None].float(),
+                               torch.from_numpy(sb)[:, None].float()).numpy()
+    assert ref.close_fp32(y, ref.fp8_matmul(ab, bb, sa, sb))[0]
+    # a planted mistake: the nibbles unpacked high-first
+    p, s = ref.quantize_int4((g.standard_normal((8, 64)) * 0.02).astype(np.float32), 32)
+    swapped = ((p >> 4) | ((p & 0x0F) << 4)).astype(np.uint8)
+    assert not np.array_equal(tc.dequantize_int4(torch.from_numpy(swapped), torch.from_numpy(s), 32).numpy(),
+                              ref.dequantize_int4(p, s, 32))
