@@ -247,6 +247,24 @@ int mls_paged_attention_decode(const void* q, int q_dt, int64_t q_ss, int64_t q_
                                int64_t n_seqs, int64_t H, int64_t D, int64_t block_size, float scale,
                                float* workspace, int64_t workspace_floats, mls_stream_t stream);
 
+/* No reference counterpart. For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the same
+ * decode as mls_paged_attention_decode with the context-split workspace taken from a
+ * static device array of MLS_PAGED_SCRATCH_FLOATS floats (8 MiB per GPU, held until the
+ * process ends) instead of a caller buffer. Allocates and frees nothing. A call whose
+ * split needs more than the array (mls_paged_attention_workspace > the maximum; never
+ * for head dims up to 254) returns MLS_ERR_ARG. All calls on one GPU share its array:
+ * calls that overlap on one GPU (two streams, two host threads) race. */
+#define MLS_PAGED_SCRATCH_FLOATS (2 * 1024 * 1024)
+int mls_paged_attention_decode_noalloc(const void* q, int q_dt, int64_t q_ss, int64_t q_sh,
+                                       const void* k_pool, const void* v_pool, int kv_dt,
+                                       int64_t kv_sb, int64_t kv_sh, int64_t kv_st, int64_t num_blocks,
+                                       const int32_t* block_tables, int64_t bt_ss, int64_t max_blocks,
+                                       const int32_t* context_lens,
+                                       void* out, int64_t o_ss, int64_t o_sh,
+                                       int64_t n_seqs, int64_t H, int64_t D, int64_t block_size, float scale,
+                                       mls_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

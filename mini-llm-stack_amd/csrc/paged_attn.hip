@@ -23,6 +23,9 @@
 // [0, num_blocks) is skipped (its tokens weigh 0) rather than dereferenced, and a
 // context longer than the table row covers is cut at the row's end. A zero context
 // gives a zero output, as in the reference.
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 
 namespace mls {
@@ -343,19 +346,24 @@ extern "C" int64_t mls_paged_attention_workspace(int64_t n_seqs, int64_t H, int6
   return s > 1 ? n_seqs * H * s * (D + 2) : 0;
 }
 
-extern "C" int mls_paged_attention_decode(const void* q, int q_dt, int64_t q_ss, int64_t q_sh,
-                                          const void* k_pool, const void* v_pool, int kv_dt, int64_t kv_sb,
-                                          int64_t kv_sh, int64_t kv_st, int64_t num_blocks,
-                                          const int32_t* block_tables, int64_t bt_ss, int64_t max_blocks,
-                                          const int32_t* context_lens, void* out, int64_t o_ss, int64_t o_sh,
-                                          int64_t n_seqs, int64_t H, int64_t D, int64_t block_size, float scale,
-                                          float* workspace, int64_t workspace_floats, mls_stream_t stream) {
-  const char* fn = "mls_paged_attention_decode";
+namespace {
+
+// Validates a decode call and fills `a` (workspace left null). *done: nothing to launch
+// (an empty batch); *need: workspace floats the split merge needs (0: no split).
+int paged_prepare(const char* fn, const void* q, int q_dt, int64_t q_ss, int64_t q_sh, const void* k_pool,
+                  const void* v_pool, int kv_dt, int64_t kv_sb, int64_t kv_sh, int64_t kv_st, int64_t num_blocks,
+                  const int32_t* block_tables, int64_t bt_ss, int64_t max_blocks, const int32_t* context_lens,
+                  void* out, int64_t o_ss, int64_t o_sh, int64_t n_seqs, int64_t H, int64_t D, int64_t block_size,
+                  float scale, PagedArgs& a, int64_t& need, bool& fast, int& cpt, bool& done) {
+  done = false;
   if (n_seqs < 0 || H < 0 || D < 0 || block_size < 1 || max_blocks < 0 || num_blocks < 0)
     return fail(MLS_ERR_ARG, "%s: bad sizes n_seqs=%lld H=%lld D=%lld block_size=%lld", fn, (long long)n_seqs,
                 (long long)H, (long long)D, (long long)block_size);
   if (!is_float_dt(q_dt) || !is_float_dt(kv_dt)) return fail(MLS_ERR_ARG, "%s: bad dtype", fn);
-  if (n_seqs == 0 || H == 0 || D == 0) return MLS_OK;
+  if (n_seqs == 0 || H == 0 || D == 0) {
+    done = true;
+    return MLS_OK;
+  }
   if (!q || !k_pool || !v_pool || !context_lens || !out || (max_blocks > 0 && !block_tables))
     return fail(MLS_ERR_ARG, "%s: null pointer", fn);
   if (q_sh < D || q_ss < H * D || o_sh < D || o_ss < H * D || kv_st < D || kv_sh < kv_st * block_size ||
@@ -366,22 +374,126 @@ extern "C" int mls_paged_attention_decode(const void* q, int q_dt, int64_t q_ss,
   if (n_seqs * H > 0x3FFFFFFF || block_size > 0x3FFFFFFF)
     return fail(MLS_ERR_UNSUPPORTED, "%s: too large", fn);
   const int splits = choose_splits(n_seqs, H, max_blocks);
-  const int64_t need = splits > 1 ? n_seqs * H * splits * (D + 2) : 0;
-  if (need > 0 && (!workspace || workspace_floats < need))
-    return fail(MLS_ERR_ARG, "%s: workspace of %lld floats needed (mls_paged_attention_workspace)", fn,
-                (long long)need);
+  need = splits > 1 ? n_seqs * H * splits * (D + 2) : 0;
   const int esz = dt_size(kv_dt);
   const int64_t row = D * esz;
-  const int cpt = (int)(row / 16);
-  const bool fast = row % 16 == 0 && cpt >= 1 && cpt <= 64 && (cpt & (cpt - 1)) == 0 &&
-                    (kv_st * esz) % 16 == 0 && (kv_sh * esz) % 16 == 0 && (kv_sb * esz) % 16 == 0 &&
-                    aligned(k_pool, 16) && aligned(v_pool, 16);
+  cpt = (int)(row / 16);
+  fast = row % 16 == 0 && cpt >= 1 && cpt <= 64 && (cpt & (cpt - 1)) == 0 && (kv_st * esz) % 16 == 0 &&
+         (kv_sh * esz) % 16 == 0 && (kv_sb * esz) % 16 == 0 && aligned(k_pool, 16) && aligned(v_pool, 16);
   if (!fast && D > 256) return fail(MLS_ERR_UNSUPPORTED, "%s: head dim %lld needs 16-byte rows", fn, (long long)D);
-  const PagedArgs a{q, q_ss, q_sh, k_pool, v_pool, kv_sb, kv_sh, kv_st, num_blocks, block_tables, bt_ss,
-                    max_blocks, context_lens, out, o_ss, o_sh, (int)n_seqs, (int)H, (int)D, (int)block_size,
-                    scale, workspace, splits};
-  hipStream_t st = (hipStream_t)stream;
+  a = PagedArgs{q, q_ss, q_sh, k_pool, v_pool, kv_sb, kv_sh, kv_st, num_blocks, block_tables, bt_ss,
+                max_blocks, context_lens, out, o_ss, o_sh, (int)n_seqs, (int)H, (int)D, (int)block_size,
+                scale, nullptr, splits};
+  return MLS_OK;
+}
+
+int paged_launch(const PagedArgs& a, int q_dt, int kv_dt, bool fast, int cpt, hipStream_t st) {
   if (q_dt == MLS_F32) return launch_paged_kv<float>(a, kv_dt, fast, cpt, st);
   if (q_dt == MLS_F16) return launch_paged_kv<_Float16>(a, kv_dt, fast, cpt, st);
   return launch_paged_kv<__bf16>(a, kv_dt, fast, cpt, st);
+}
+
+}  // namespace
+
+extern "C" int mls_paged_attention_decode(const void* q, int q_dt, int64_t q_ss, int64_t q_sh,
+                                          const void* k_pool, const void* v_pool, int kv_dt, int64_t kv_sb,
+                                          int64_t kv_sh, int64_t kv_st, int64_t num_blocks,
+                                          const int32_t* block_tables, int64_t bt_ss, int64_t max_blocks,
+                                          const int32_t* context_lens, void* out, int64_t o_ss, int64_t o_sh,
+                                          int64_t n_seqs, int64_t H, int64_t D, int64_t block_size, float scale,
+                                          float* workspace, int64_t workspace_floats, mls_stream_t stream) {
+  const char* fn = "mls_paged_attention_decode";
+  PagedArgs a{};
+  int64_t need = 0;
+  bool fast = false, done = false;
+  int cpt = 0;
+  int rc = paged_prepare(fn, q, q_dt, q_ss, q_sh, k_pool, v_pool, kv_dt, kv_sb, kv_sh, kv_st, num_blocks,
+                         block_tables, bt_ss, max_blocks, context_lens, out, o_ss, o_sh, n_seqs, H, D, block_size,
+                         scale, a, need, fast, cpt, done);
+  if (rc != MLS_OK || done) return rc;
+  if (need > 0 && (!workspace || workspace_floats < need))
+    return fail(MLS_ERR_ARG, "%s: workspace of %lld floats needed (mls_paged_attention_workspace)", fn,
+                (long long)need);
+  a.ws = workspace;
+  return paged_launch(a, q_dt, kv_dt, fast, cpt, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------- allocation-free variant
+//
+// The split partials (acc[D], m, l per split) live in `scratch`, a device array of
+// MLS_PAGED_SCRATCH_FLOATS floats (8 MiB) that every GPU this library runs on holds
+// until the process ends. Host code never passes the array's name to a kernel (in host
+// code it names a host-side stand-in): the device address comes from
+// hipGetSymbolAddress, taken once per device with that device current, and is kept in
+// scratch_dev[]. No entry of the workspace needs to start at zero: every split writes
+// its whole (acc, m, l) record, empty splits included, before the merge kernel reads
+// it. All calls on one GPU share its array, so calls that overlap on one GPU (two
+// streams, or two host threads) race on it.
+
+static __device__ __align__(256) float scratch[MLS_PAGED_SCRATCH_FLOATS];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> scratch_dev[kMaxDevices];
+std::mutex scratch_mu;
+
+// The device address of `scratch` on the device that owns stream `st`.
+int scratch_for(hipStream_t st, float** ptr, const char* fn) {
+  int dev = -1;
+  hipError_t e = st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MLS_ERR_HIP, "%s: stream device: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MLS_ERR_UNSUPPORTED, "%s: device %d", fn, dev);
+  float* p = scratch_dev[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    p = scratch_dev[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      int cur = -1;
+      e = hipGetDevice(&cur);
+      if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+      void* sym = nullptr;
+      if (e == hipSuccess) e = hipGetSymbolAddress(&sym, HIP_SYMBOL(scratch));
+      if (cur >= 0 && cur != dev) {
+        const hipError_t e2 = hipSetDevice(cur);
+        if (e == hipSuccess) e = e2;
+      }
+      if (e != hipSuccess || !sym)
+        return fail(MLS_ERR_HIP, "%s: hipGetSymbolAddress(scratch): %s", fn, hipGetErrorString(e));
+      p = static_cast<float*>(sym);
+      scratch_dev[dev].store(p, std::memory_order_release);
+    }
+  }
+  *ptr = p;
+  return MLS_OK;
+}
+
+}  // namespace
+
+extern "C" int mls_paged_attention_decode_noalloc(const void* q, int q_dt, int64_t q_ss, int64_t q_sh,
+                                                  const void* k_pool, const void* v_pool, int kv_dt, int64_t kv_sb,
+                                                  int64_t kv_sh, int64_t kv_st, int64_t num_blocks,
+                                                  const int32_t* block_tables, int64_t bt_ss, int64_t max_blocks,
+                                                  const int32_t* context_lens, void* out, int64_t o_ss,
+                                                  int64_t o_sh, int64_t n_seqs, int64_t H, int64_t D,
+                                                  int64_t block_size, float scale, mls_stream_t stream) {
+  const char* fn = "mls_paged_attention_decode_noalloc";
+  PagedArgs a{};
+  int64_t need = 0;
+  bool fast = false, done = false;
+  int cpt = 0;
+  int rc = paged_prepare(fn, q, q_dt, q_ss, q_sh, k_pool, v_pool, kv_dt, kv_sb, kv_sh, kv_st, num_blocks,
+                         block_tables, bt_ss, max_blocks, context_lens, out, o_ss, o_sh, n_seqs, H, D, block_size,
+                         scale, a, need, fast, cpt, done);
+  if (rc != MLS_OK || done) return rc;
+  if (need > MLS_PAGED_SCRATCH_FLOATS)
+    return fail(MLS_ERR_ARG,
+                "%s: the context split of this call needs %lld workspace floats, above the static scratch of %lld; "
+                "use mls_paged_attention_decode with a caller workspace",
+                fn, (long long)need, (long long)MLS_PAGED_SCRATCH_FLOATS);
+  if (need > 0) {
+    rc = scratch_for((hipStream_t)stream, &a.ws, fn);
+    if (rc != MLS_OK) return rc;
+  }
+  return paged_launch(a, q_dt, kv_dt, fast, cpt, (hipStream_t)stream);
 }

@@ -81,6 +81,8 @@ SIGNATURES = {
     "mls_paged_attention_workspace": ([_I64, _I64, _I64, _I64], _I64),
     "mls_paged_attention_decode": ([_P, _I, _I64, _I64, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _I64,
                                     _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P, _I64, _P], _I),
+    "mls_paged_attention_decode_noalloc": ([_P, _I, _I64, _I64, _P, _P, _I, _I64, _I64, _I64, _I64, _P, _I64,
+                                            _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _F, _P], _I),
 }
 
 
