@@ -307,6 +307,247 @@ __global__ __launch_bounds__(256) void gemv_wq_kernel(
   }
 }
 
+// ------------------------------------------------------------------ M = 1, 16-bit activations
+//
+// The same lane layout and dot products as gemv_wq_kernel, with the loads shaped for the
+// per-CU memory pipeline, which moves about 64 bytes per clock. Every wavefront of the
+// kernel above reads all of x (as many bytes as its weights) and issues one 2-byte scale
+// load per weight chunk, so a wavefront spent ~0.45 us only issuing its loads. Here:
+//  - x goes to LDS once per block: each wavefront brings a quarter with LDS-direct loads
+//    (buffer_load ... lds), issued before anything else;
+//  - a wavefront's INT4 group scales (R rows x K/group, contiguous per row) go to its own
+//    LDS slice with one or two LDS-direct dword loads;
+//  - the weight rows are buffer loads whose row offset sits in an SGPR (no per-lane 64-bit
+//    address arithmetic before the loads issue);
+//  - one wait for the LDS-direct loads (they were issued first and complete first) and one
+//    barrier, which falls inside the weights' HBM latency;
+//  - the cross-lane sums are DPP moves only (row sums, then row_bcast:15 / row_bcast:31), and
+//    lane 63, which ends up holding every row's total, writes the R outputs at once.
+// LDS: x in XI * 4 KiB (the LDS-direct loads past 2K bytes read zeros past the buffer), then
+// 4 scale slices of R * s_dw dwords, each rounded up to SI whole 64-dword LDS-direct
+// instructions.
+
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_add_rows(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWMASK,
+                                                                   0xF, false));
+}
+
+// Wave total into lanes 48..63 (row sums by DPP, then rows 0-2 into row 3 by row_bcast).
+__device__ __forceinline__ float wave_total_dpp(float v) {
+  v = lane_group_sum<16>(v);
+  v = dpp_add_rows<0x142, 0xA>(v);  // row_bcast:15: rows 1, 3 += last lane of rows 0, 2
+  v = dpp_add_rows<0x143, 0xC>(v);  // row_bcast:31: rows 2, 3 += lane 31 (rows 0 + 1)
+  return v;
+}
+
+__device__ __forceinline__ void lds_direct16(__amdgpu_buffer_rsrc_t rs, void* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void lds_direct4(__amdgpu_buffer_rsrc_t rs, void* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 4, voff, soff, 0, 0);
+}
+
+// vmcnt(n) alone (expcnt and lgkmcnt left at their maxima), gfx9 encoding
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+template <int WBITS, typename AT, typename ST, int CPL, int R, int XI, int SI>
+__global__ __launch_bounds__(256) void gemv1_kernel(const AT* __restrict__ x, const uint8_t* __restrict__ w,
+                                                    int ldw, int w_bytes, const ST* __restrict__ s, int s_row_bytes,
+                                                    int s_bytes, int group, AT* __restrict__ y, int N, int K,
+                                                    int s_dw) {
+  using S = XSlot<WBITS, AT>;
+  constexpr int KC = S::KC, NV = S::NV;
+  constexpr float OFF = code_offset<WBITS, AT>();
+  constexpr int S_SLICE = 64 * SI;  // scale dwords per wavefront slice
+  __shared__ __attribute__((aligned(16))) uint8_t smem[XI * 4096 + (WBITS == 4 ? 4 * S_SLICE * 4 : 16)];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nchunks = K / KC;
+  const int n0 = (blockIdx.x * 4 + wave) * R;
+
+  // 1. x into LDS (a quarter per wavefront, 1 KiB per instruction) and this wavefront's
+  //    scales into its slice: issued first, so they complete before any weight load. The
+  //    instructions before the weight loads are kept to a minimum (one buffer descriptor
+  //    per operand from the kernel arguments, row offsets in SGPRs, no per-lane clamps):
+  //    each one delays the weight stream. XI instructions per wavefront cover XI * 4 KiB
+  //    >= 2K bytes; those past x read zeros into LDS padding.
+  const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, K * (int)sizeof(AT), 0x00020000);
+#pragma unroll
+  for (int i = 0; i < XI; ++i) lds_direct16(rsx, smem + wave * 1024 + i * 4096, lane * 16, wave * 1024 + i * 4096);
+  uint8_t* sl = smem + XI * 4096 + wave * (S_SLICE * 4);
+  float srow[R];
+  if constexpr (WBITS == 4) {
+    // slice = the R rows' s_dw scale dwords back to back (rows past N read zeros); lane q of
+    // instruction i loads slice dword 64 i + q, row r = dword / s_dw found by compares (R <= 4);
+    // the lanes past R * s_dw re-read the last dword into the slice's padding
+    const __amdgpu_buffer_rsrc_t rss = __builtin_amdgcn_make_buffer_rsrc((void*)s, (short)0, s_bytes, 0x00020000);
+#pragma unroll
+    for (int i = 0; i < SI; ++i) {
+      const int q = min(64 * i + lane, R * s_dw - 1);
+      int r = 0;
+#pragma unroll
+      for (int t = 1; t < R; ++t) r += q >= t * s_dw;
+      lds_direct4(rss, sl + 256 * i, r * s_row_bytes + (q - r * s_dw) * 4, n0 * s_row_bytes);
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < R; ++r) srow[r] = to_f32(s[min(n0 + r, N - 1)]);  // uniform: scalar loads
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. every weight chunk of this lane: rows past N read zeros (past the descriptor's range);
+  //    chunks past K read whatever follows in memory and their terms are dropped below
+  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, w_bytes, 0x00020000);
+  uint4 wv[R][CPL];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      wv[r][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, lane * 16 + 1024 * j,
+                                                                                 (n0 + r) * ldw, 2));
+
+  // 3. the LDS-direct loads have landed once only the weight loads are outstanding; after
+  //    the barrier every wavefront's quarter of x is there
+  wait_vmcnt<R * CPL>();
+  __builtin_amdgcn_s_barrier();
+  float sc[R][CPL];
+  if constexpr (WBITS == 4) {
+    const ST* st = reinterpret_cast<const ST*>(sl);
+    const int P = s_dw * 4 / (int)sizeof(ST);  // scales per slice row
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) sc[r][j] = to_f32(st[min(r * P + ((lane + 64 * j) * KC) / group, S_SLICE * 4 / (int)sizeof(ST) - 1)]);
+  }
+  XRaw<WBITS, AT> xraw[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const uint4* xl = reinterpret_cast<const uint4*>(smem + (lane + 64 * j) * KC * (int)sizeof(AT));
+#pragma unroll
+    for (int q = 0; q < XRaw<WBITS, AT>::XQ; ++q) xraw[j].v[q] = xl[q];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 4. dot products (as gemv_wq_kernel); a chunk past K adds nothing (its scale may be
+  //    any bits, so the whole term is dropped, not multiplied by zero)
+  uint32_t xr[CPL][NV];
+  float osx[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) osx[j] = OFF * x_from_raw<WBITS, AT>(xraw[j], xr[j]);
+  uint32_t nib_mask = 0x000F000Fu, magic = 0;
+  if constexpr (WBITS == 4) magic = Half16<AT>::MAGIC4;
+  asm volatile("" : "+v"(nib_mask), "+v"(magic));
+  float part[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const float d = chunk_dot<WBITS, AT>(wv[r][j], xr[j], nib_mask, magic) - osx[j];
+      const float t = WBITS == 4 ? fmaf(sc[r][j], d, acc) : acc + d;
+      acc = (64 * (j + 1) > nchunks && lane + 64 * j >= nchunks) ? acc : t;
+    }
+    part[r] = acc;
+  }
+
+  // 5. wave totals by DPP; lane 63 holds every row's and writes them
+#pragma unroll
+  for (int r = 0; r < R; ++r) part[r] = wave_total_dpp(part[r]);
+  const int rows = min(R, N - n0);
+  if (lane == 63 && rows > 0) {
+    float v[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) v[r] = WBITS == 8 ? part[r] * srow[r] : part[r];
+    AT* dst = y + n0;
+    if constexpr (R == 4) {
+      if (rows == 4 && ((uintptr_t)dst & 7) == 0) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_bits(from_f32<AT>(v[0]), from_f32<AT>(v[1])),
+                                                    pack2_bits(from_f32<AT>(v[2]), from_f32<AT>(v[3])));
+        return;
+      }
+    } else if constexpr (R == 2) {
+      if (rows == 2 && ((uintptr_t)dst & 3) == 0) {
+        *reinterpret_cast<uint32_t*>(dst) = pack2_bits(from_f32<AT>(v[0]), from_f32<AT>(v[1]));
+        return;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (r < rows) dst[r] = from_f32<AT>(v[r]);
+  }
+}
+
+template <int WBITS, typename AT, typename ST, int CPL, int SI>
+static int launch_gemv1_si(const WqArgs& p, int s_dw) {
+  constexpr int R = CPL >= 8 ? 1 : 8 / CPL;
+  // x instructions per wavefront: 4 wavefronts x 1 KiB cover 2K bytes (INT4: K <= 2048 CPL;
+  // INT8: K <= 1024 CPL)
+  constexpr int XI = WBITS == 4 ? CPL : (CPL >= 2 ? CPL / 2 : 1);
+  if (p.K * 2 > XI * 4096) return MLS_ERR_UNSUPPORTED;
+  const int s_row_bytes = (int)(p.ld_sn * (int64_t)sizeof(ST));
+  const int s_bytes = WBITS == 4 ? (int)(p.N * p.ld_sn * (int64_t)sizeof(ST)) : 0;
+  hipLaunchKernelGGL((gemv1_kernel<WBITS, AT, ST, CPL, R, XI, SI>), dim3((unsigned)cdiv(p.N, 4 * R)), dim3(256), 0,
+                     p.stream, (const AT*)p.a, p.w, (int)p.ldw, (int)(p.N * p.ldw), (const ST*)p.s, s_row_bytes,
+                     s_bytes, p.group, (AT*)p.c, (int)p.N, (int)p.K, s_dw);
+  return MLS_OK;
+}
+
+template <int WBITS, typename AT, typename ST, int CPL>
+static int launch_gemv1_cpl(const WqArgs& p, int s_dw) {
+  constexpr int R = CPL >= 8 ? 1 : 8 / CPL;
+  if constexpr (WBITS == 8) return launch_gemv1_si<WBITS, AT, ST, CPL, 1>(p, s_dw);
+  const int64_t slice = (int64_t)R * s_dw;  // scale dwords per wavefront
+  if (slice <= 64) return launch_gemv1_si<WBITS, AT, ST, CPL, 1>(p, s_dw);
+  if (slice <= 128) return launch_gemv1_si<WBITS, AT, ST, CPL, 2>(p, s_dw);
+  if (slice <= 256) return launch_gemv1_si<WBITS, AT, ST, CPL, 4>(p, s_dw);
+  return MLS_ERR_UNSUPPORTED;
+}
+
+template <int WBITS, typename AT, typename ST>
+static int launch_gemv1_st(const WqArgs& p) {
+  constexpr int KC = XSlot<WBITS, AT>::KC;
+  int s_dw = 0;
+  if constexpr (WBITS == 4) {
+    const int64_t G = p.K / p.group;
+    // group scales read as whole dwords per row: contiguous groups, rows on dword boundaries
+    if (p.ld_sg != 1 || (G * (int64_t)sizeof(ST)) % 4 != 0 || (p.ld_sn * (int64_t)sizeof(ST)) % 4 != 0 ||
+        !aligned(p.s, 4))
+      return MLS_ERR_UNSUPPORTED;
+    if ((int64_t)p.N * p.ld_sn * (int64_t)sizeof(ST) > 0x7FFFFFFF) return MLS_ERR_UNSUPPORTED;
+    s_dw = (int)(G * (int64_t)sizeof(ST) / 4);
+  }
+  const int64_t cpl = cdiv(p.K / KC, 64);
+  if (cpl <= 1) return launch_gemv1_cpl<WBITS, AT, ST, 1>(p, s_dw);
+  if (cpl <= 2) return launch_gemv1_cpl<WBITS, AT, ST, 2>(p, s_dw);
+  if (cpl <= 4) return launch_gemv1_cpl<WBITS, AT, ST, 4>(p, s_dw);
+  if (cpl <= 8) return launch_gemv1_cpl<WBITS, AT, ST, 8>(p, s_dw);
+  if constexpr (WBITS == 8)  // (INT4 with 16 chunks per lane has K > 16384: x would not fit)
+    if (cpl <= 16) return launch_gemv1_cpl<WBITS, AT, ST, 16>(p, s_dw);
+  return MLS_ERR_UNSUPPORTED;
+}
+
+// M = 1 with 16-bit activations; MLS_ERR_UNSUPPORTED sends the call to gemv_wq_kernel.
+// MLS_GEMV1=0 disables this path (A/B sweeps).
+static int launch_gemv1(int wbits, const WqArgs& p) {
+  static const int enabled = env_int("MLS_GEMV1", 1);
+  if (!enabled || p.M != 1 || p.a_dt == MLS_F32) return MLS_ERR_UNSUPPORTED;
+  // x in LDS (at most 32 KiB); 32-bit buffer offsets into the whole weight matrix
+  if (p.K * 2 > 32768 || (p.N + 4) * p.ldw >= (1ll << 31)) return MLS_ERR_UNSUPPORTED;
+  if (wbits == 4) {
+    if (p.a_dt == MLS_F16) return p.s_dt == MLS_F16 ? launch_gemv1_st<4, _Float16, _Float16>(p)
+                                                    : launch_gemv1_st<4, _Float16, float>(p);
+    return p.s_dt == MLS_F16 ? launch_gemv1_st<4, __bf16, _Float16>(p) : launch_gemv1_st<4, __bf16, float>(p);
+  }
+  if (p.a_dt == MLS_F16) return p.s_dt == MLS_F16 ? launch_gemv1_st<8, _Float16, _Float16>(p)
+                                                  : launch_gemv1_st<8, _Float16, float>(p);
+  return p.s_dt == MLS_F16 ? launch_gemv1_st<8, __bf16, _Float16>(p) : launch_gemv1_st<8, __bf16, float>(p);
+}
+
 template <int WBITS, typename AT, typename ST, int MT, int CPL, int R>
 static void launch_r(const WqArgs& p) {
   const dim3 grid((unsigned)cdiv(p.N, 4 * R), (unsigned)cdiv(p.M, MT));
@@ -389,6 +630,8 @@ int launch_gemv_wq(int wbits, const WqArgs& p) {
   if (!aligned(p.w, 16) || p.ldw % 16 != 0) return MLS_ERR_UNSUPPORTED;
   if (!aligned(p.a, 16) || (p.lda * esz) % 16 != 0) return MLS_ERR_UNSUPPORTED;
   if (p.N > 0x7FFFFFFF / 2 || p.M > 4 * 65535) return MLS_ERR_UNSUPPORTED;  // grid.y = M / MT
+  const int rc = launch_gemv1(wbits, p);
+  if (rc != MLS_ERR_UNSUPPORTED) return rc;
   if (wbits == 4) {
     if (p.a_dt == MLS_F32) return dispatch_st<4, float>(p);
     if (p.a_dt == MLS_F16) return dispatch_st<4, _Float16>(p);

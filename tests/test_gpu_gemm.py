@@ -118,6 +118,48 @@ def test_gemv_other_dtypes(dev, dtype, M):
            ref.int8_matmul(a2.float().numpy(), q.cpu().numpy(), s8.cpu().numpy()), f"int8 {dtype} M={M}")
 
 
+@pytest.mark.parametrize("N,K,gs,dtype,sdt", [
+    (1000, 3072, 32, torch.bfloat16, torch.float16),   # ragged N, chunks past K, 4 scale instructions
+    (777, 4096, 128, torch.float16, torch.float32),    # fp32 scales: 2 scale instructions per wavefront
+    (64, 512, 128, torch.bfloat16, torch.float16),     # one chunk per lane, 8 rows per wavefront
+    (4100, 2048, 64, torch.bfloat16, torch.float16),   # last block holds 4 of its 16 rows
+])
+def test_gemv_m1_edges(dev, N, K, gs, dtype, sdt):
+    """M = 1 with 16-bit activations (x and scales through LDS): ragged N, K not a multiple of the
+    lanes' span, both scale dtypes and slice sizes, weights and scales as views with padded rows."""
+    a, w = _data(1, N, K, 900 + N, 0.02)
+    p, s = quantize_int4(w.to(dev), gs)
+    s = s.to(sdt)
+    pw = torch.zeros(N, K // 2 + 48, dtype=torch.uint8, device=dev)   # ldw = K/2 + 48
+    pw[:, :K // 2] = p
+    sw = torch.zeros(N, K // gs + 6, dtype=sdt, device=dev)            # ld_sn = G + 6
+    sw[:, :K // gs] = s
+    ab = a.to(dtype)
+    want = ref.int4_matmul(ab.float().numpy(), p.cpu().numpy(), s.float().cpu().numpy(), gs)
+    _check(int4_matmul(ab.to(dev), pw[:, :K // 2], sw[:, :K // gs], gs), want, f"int4 M=1 N={N} K={K} g{gs}")
+    q, s8 = quantize_int8(w.to(dev))
+    s8 = s8.to(sdt)
+    _check(int8_matmul(ab.to(dev), q, s8),
+           ref.int8_matmul(ab.float().numpy(), q.cpu().numpy(), s8.float().cpu().numpy()), f"int8 M=1 N={N} K={K}")
+
+
+def test_gemv_m1_unaligned_output_and_long_rows(dev):
+    """Through the C ABI: an output that starts 2 bytes past an 8-byte boundary (element-wise
+    stores), and K = 20480 (x beyond the LDS path: the register GEMV takes it)."""
+    import kernels
+    L = kernels.lib()
+    st = torch.cuda.current_stream(dev).cuda_stream
+    for N, K in ((300, 4096), (256, 20480)):
+        a, p, s, want = _int4_setup(dev, 1, N, K, 128, 950 + K)
+        buf = torch.full((N + 4,), float("nan"), dtype=torch.bfloat16, device=dev)
+        out = buf[1:N + 1]
+        rc = L.mls_int4_gemm(a.data_ptr(), kernels.MLS_BF16, K, p.data_ptr(), p.stride(0), s.data_ptr(),
+                             kernels.MLS_F16, s.stride(0), 1, 128, out.data_ptr(), kernels.MLS_BF16, N, 1, N, K, st)
+        assert rc == 0
+        _check(out.reshape(1, N), want, f"int4 M=1 unaligned output N={N} K={K}")
+        assert torch.isnan(buf[0]) and torch.isnan(buf[N + 1:]).all()
+
+
 def test_gemv_long_k(dev):
     """K = 11008 (the down-projection's input): chunks do not divide evenly across lanes."""
     a, p, s, want = _int4_setup(dev, 1, 4096, 11008, 128, 7)
