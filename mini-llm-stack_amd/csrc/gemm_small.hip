@@ -1,0 +1,346 @@
+// Medium weight-only GEMMs (16 < M <= 256 whose tiled GEMM would not fill the GPU),
+// 16-bit activations, on the 16-bit MFMA with every operand loaded straight into
+// registers.
+//
+// Block = 4 wavefronts on one output tile of TM x TN 16 x 16 MFMA tiles (rows m of x by
+// weight rows n). The K steps are split into 4 contiguous ranges, one per wavefront, so
+// no operand byte is loaded twice inside a block and nothing is staged through LDS on
+// the way in: per step a lane loads its 16-byte pieces of x and of the weights, which
+// are already in MFMA operand layout. The 4 partial tiles meet in LDS once, at the end.
+// D steps of loads are in flight at once (a ring of D register sets).
+//
+// Step = 64 k (INT8: a lane's 16 weight bytes are k [16q, 16q + 16) of its row) or
+// 128 k (INT4: 16 bytes = k [32q, 32q + 32)), q = lane / 16. x pieces follow the same k:
+// INT8 two 16-byte loads, INT4 four. Rows m >= M, rows n >= N and steps past a
+// wavefront's range read zeros (buffer loads past the operand's range).
+//
+// Widening: INT8 bytes to exact 16-bit integers (6 VALU per 4 weights); INT4 nibbles are
+// OR-ed into the mantissa of bf16 128.0 / fp16 1024.0 (one v_and_or per 2 weights, exact
+// 128 + v / 1024 + v, dword j of a piece giving k order 0,4,1,5,2,6,3,7 with x permuted
+// alike) and the offset is removed with x's sums over the step, which one more MFMA
+// against an all-ones operand gives in the same accumulator layout:
+//   sum_k x (v - 8) = sum_k x (128 + v) - 136 sum_k x    (fp16: 1024, 1032).
+// INT4 group scales (group a multiple of 128, so a step lies in one group) multiply each
+// step's partial sums in fp32; the block's scales come into LDS once, by LDS-direct loads
+// issued right after the first two steps' operands. INT8 row scales multiply the reduced
+// tile. The instructions before the first operand loads are kept to a minimum: each one
+// delays the weight stream.
+//
+// The weight operand is MFMA "A" and x is "B", so lane l's accumulator holds
+// C[n = 4 (l / 16) + i][m = l % 16], i = 0..3: 4 consecutive outputs of one row m.
+#include "mfma16.h"
+
+namespace mls {
+
+namespace {
+
+// soffset of a step past a wavefront's range: every access falls outside the operands
+constexpr int kPastEnd = 0x40000000;
+
+template <typename AT> struct Nib;
+template <> struct Nib<__bf16> {
+  static constexpr uint32_t MAGIC = 0x43004300u;  // bf16 (128, 128)
+  static constexpr float OFF = 136.0f;            // 128 + 8
+  static constexpr uint32_t ONE2 = 0x3F803F80u;   // bf16 (1, 1)
+};
+template <> struct Nib<_Float16> {
+  static constexpr uint32_t MAGIC = 0x64006400u;  // fp16 (1024, 1024)
+  static constexpr float OFF = 1032.0f;
+  static constexpr uint32_t ONE2 = 0x3C003C00u;   // fp16 (1, 1)
+};
+
+struct SmallArgs {
+  const void* a;
+  int lda, a_bytes;  // elements; bytes of the M rows
+  const uint8_t* w;
+  int ldw, w_bytes;  // bytes; bytes of the N rows
+  const void* s;
+  int ld_sn, ld_sg, group, s_bytes;  // scale strides (elements), INT4 group, bytes of s
+  void* c;
+  int ldc;
+  int M, N, K;
+  int m_tiles, G;  // row tiles; INT4 groups per weight row
+};
+
+__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0));
+}
+__device__ __forceinline__ uint4 ld16_nt(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 2));
+}
+
+// x piece (8 16-bit values, k order 0..7) -> k order 0,4,1,5,2,6,3,7
+__device__ __forceinline__ uint4 perm_x(const uint4& v) {
+  return make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                    __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
+}
+
+// (a & m) | c with m and c in registers: one v_and_or_b32
+__device__ __forceinline__ uint32_t andor(uint32_t a, uint32_t m, uint32_t c) { return (a & m) | c; }
+
+template <int WBITS, typename AT, typename ST, int TM, int TN, int D>
+__global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
+  using MM = Mfma16<AT>;
+  constexpr bool I4 = WBITS == 4;
+  constexpr int KS = I4 ? 128 : 64;   // k per step
+  constexpr int XP = I4 ? 4 : 2;      // 16-byte x pieces per lane, step and row tile
+  extern __shared__ __align__(16) uint8_t smem[];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, q = lane >> 4;
+  // grid: x = column tile (padded to a multiple of 8), y = row tile. Workgroups go to the 8
+  // XCDs round-robin by linear id, so every row tile of a column tile lands on the same XCD
+  // and the weight tile is fetched from HBM once.
+  const int nt = blockIdx.x, mt = blockIdx.y;
+  const int m0 = mt * 16 * TM, n0 = nt * 16 * TN;
+  if (n0 >= p.N) return;  // padding column tile
+  const int nsteps = p.K / KS;
+  const int s_lo = nsteps * wave / 4, s_hi = nsteps * (wave + 1) / 4;
+
+  // every argument into SGPRs at once (one round of kernel-argument loads)
+  asm volatile("" ::"s"(p.a), "s"(p.lda), "s"(p.a_bytes), "s"(p.w), "s"(p.ldw), "s"(p.w_bytes), "s"(p.s),
+               "s"(p.ld_sn), "s"(p.group), "s"(p.s_bytes), "s"(p.c), "s"(p.ldc), "s"(p.M), "s"(p.N), "s"(p.K),
+               "s"(p.G));
+
+  // ---- operand descriptors and this lane's offsets (nothing else before the first loads)
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc((void*)p.a, (short)0, p.a_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc((void*)p.w, (short)0, p.w_bytes, 0x00020000);
+  int xo[TM];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) xo[tm] = (m0 + 16 * tm + r16) * p.lda * 2 + (I4 ? 64 : 32) * q;
+  int wo[TN];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) wo[tn] = (n0 + 16 * tn + r16) * p.ldw + 16 * q;
+
+  struct Slot {
+    uint4 x[TM][XP];
+    uint4 w[TN];
+  };
+  auto load = [&](Slot& sl, int st) __attribute__((always_inline)) {
+    const int live = st < s_hi;
+    const int sx = live ? st * KS * 2 : kPastEnd, sw = live ? st * 64 : kPastEnd;
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int h = 0; h < XP; ++h) sl.x[tm][h] = ld16(rsa, xo[tm] + 16 * h, sx);
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) sl.w[tn] = ld16_nt(rsw, wo[tn], sw);
+  };
+  Slot sl[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) load(sl[d], s_lo + d);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- INT4 group scales of the block's 16 TN rows into LDS ([row][group] in ST), issued
+  // after the first two steps' operands: the first step waits for nearly all of those
+  // anyway, and the LDS-direct loads complete after them. Row r of table dword d is
+  // d / dw_row, computed in fp32 ((2d + 1) / (2 dw_row) is never within 2^-10 of an
+  // integer, far above the rounding error for these sizes).
+  constexpr int BN = 16 * TN;
+  if constexpr (I4) {
+    const __amdgpu_buffer_rsrc_t rss = __builtin_amdgcn_make_buffer_rsrc((void*)p.s, (short)0, p.s_bytes, 0x00020000);
+    const int dw_row = p.G * (int)sizeof(ST) / 4;  // dwords per row (G * sizeof(ST) % 4 == 0)
+    const float inv2 = 0.5f / (float)dw_row;
+    for (int q0 = wave * 64; q0 < BN * dw_row; q0 += 256) {
+      const int d = min(q0 + lane, BN * dw_row - 1);
+      const int r = (int)((float)(2 * d + 1) * inv2);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rss, (__attribute__((address_space(3))) void*)(smem + q0 * 4), 4,
+                                               (n0 + r) * p.ld_sn * (int)sizeof(ST) + (d - r * dw_row) * 4, 0, 0,
+                                               0);
+    }
+    __builtin_amdgcn_s_waitcnt(0 | 0x70 | 0xF00);  // vmcnt(0): the table and both steps' operands
+    __builtin_amdgcn_s_barrier();
+  }
+
+  f32x4 acc[TN][TM];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = f32x4{0.f, 0.f, 0.f, 0.f};
+  uint32_t nmask = 0x000F000Fu, magic = Nib<AT>::MAGIC;
+  asm volatile("" : "+v"(nmask), "+v"(magic));
+  const uint4 ones = make_uint4(Nib<AT>::ONE2, Nib<AT>::ONE2, Nib<AT>::ONE2, Nib<AT>::ONE2);
+  const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const Slot& sl, int st) __attribute__((always_inline)) {
+    if constexpr (I4) {
+      uint4 xpm[TM][4];
+      f32x4 xs[TM];
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xpm[tm][j] = perm_x(sl.x[tm][j]);
+        xs[tm] = zero;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xs[tm] = MM::mma(ones, xpm[tm][j], xs[tm]);
+      }
+      // scales of rows n = n0 + 16 tn + 4 q + i for this step's group (clamped past K)
+      const int g = min(st * KS / p.group, p.G - 1);
+      const ST* sl_s = reinterpret_cast<const ST*>(smem);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const uint32_t d[4] = {sl.w[tn].x, sl.w[tn].y, sl.w[tn].z, sl.w[tn].w};
+        uint4 wop[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          wop[j] = make_uint4(andor(d[j], nmask, magic), andor(d[j] >> 4, nmask, magic),
+                              andor(d[j] >> 8, nmask, magic), andor(d[j] >> 12, nmask, magic));
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[i] = to_f32(sl_s[(16 * tn + 4 * q + i) * p.G + g]);
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+          f32x4 pp = zero;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pp = MM::mma(wop[j], xpm[tm][j], pp);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[tn][tm][i] = fmaf(sc[i], fmaf(-Nib<AT>::OFF, xs[tm][i], pp[i]), acc[tn][tm][i]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        uint32_t o[8];
+        widen_int8<AT>(sl.w[tn], o);
+        const uint4 w0 = make_uint4(o[0], o[1], o[2], o[3]), w1 = make_uint4(o[4], o[5], o[6], o[7]);
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+          acc[tn][tm] = MM::mma(w0, sl.x[tm][0], acc[tn][tm]);
+          acc[tn][tm] = MM::mma(w1, sl.x[tm][1], acc[tn][tm]);
+        }
+      }
+    }
+  };
+
+  for (int st = s_lo; st < s_hi; st += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      compute(sl[d], st + d);
+      load(sl[d], st + d + D);
+    }
+  }
+
+  // ---- the 4 partial tiles meet in LDS; each thread finishes TN * TM / 4 accumulators
+  __syncthreads();  // (INT4: every wavefront is done with the scale table the buffer reuses)
+  f32x4* red = reinterpret_cast<f32x4*>(smem);  // [4][TN][TM][64]
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) red[((wave * TN + tn) * TM + tm) * 64 + lane] = acc[tn][tm];
+  __syncthreads();
+  AT* c = static_cast<AT*>(p.c);
+  for (int slot = threadIdx.x; slot < TN * TM * 64; slot += 256) {
+    const int l = slot & 63, tm = (slot >> 6) % TM, tn = (slot >> 6) / TM;
+    f32x4 v = red[(tn * TM + tm) * 64 + l];
+#pragma unroll
+    for (int ww = 1; ww < 4; ++ww) v += red[((ww * TN + tn) * TM + tm) * 64 + l];
+    const int m = m0 + 16 * tm + (l & 15), nb = n0 + 16 * tn + 4 * (l >> 4);
+    if (m >= p.M || nb >= p.N) continue;
+    if constexpr (!I4) {
+      const ST* sv = static_cast<const ST*>(p.s);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] *= to_f32(sv[min(nb + i, p.N - 1)]);
+    }
+    AT* dst = c + (int64_t)m * p.ldc + nb;
+    if (nb + 3 < p.N && ((uintptr_t)dst & 7) == 0) {
+      store4<AT>(dst, v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (nb + i < p.N) dst[i] = from_f32<AT>(v[i]);
+    }
+  }
+}
+
+template <int WBITS, typename AT, typename ST, int TM, int TN, int D>
+int launch_small(SmallArgs a, hipStream_t st) {
+  a.m_tiles = (int)cdiv(a.M, 16 * TM);
+  const int64_t nt = cdiv(cdiv(a.N, 16 * TN), 8) * 8;
+  const int red = 4 * TN * TM * 64 * 16;
+  const int sc = WBITS == 4 ? 16 * TN * a.G * (int)sizeof(ST) + 256 * 4 : 0;  // + padding of the last dword load
+  if (a.m_tiles > 65535) return MLS_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((gemm_small_kernel<WBITS, AT, ST, TM, TN, D>), dim3((unsigned)nt, (unsigned)a.m_tiles), dim3(256),
+                     red > sc ? red : sc, st, a);
+  return MLS_OK;
+}
+
+// Time model for a tile of TM x TN: every block loads K * (16 TM * 2 + 16 TN * bytes per
+// weight) bytes through its CU's memory pipeline; blocks beyond one per CU run in
+// further rounds.
+double small_cost(int64_t M, int64_t N, int64_t K, int wbits, int tm, int tn) {
+  const int64_t blocks = cdiv(M, 16 * tm) * cdiv(N, 16 * tn);
+  const double rows_x = (double)(M < 16 * tm ? M : 16 * tm);  // x loads of rows past M are skipped
+  const double per_block = (double)K * (rows_x * 2.0 + 16.0 * tn * (wbits == 4 ? 0.5 : 1.0));
+  return (double)cdiv(blocks, 256) * per_block;
+}
+
+template <int WBITS, typename AT, typename ST>
+int dispatch_small(SmallArgs a, hipStream_t st) {
+  static const int force = env_int("MLS_SMALL_TILE", 0);  // TM * 10 + TN (sweeps)
+  int best_tm = 1, best_tn = 1;
+  double best = 1e300;
+  for (int tm = 1; tm <= 4; tm *= 2)
+    for (int tn = 1; tn <= 4; tn *= 2) {
+      if (tm > 1 && a.M <= 16 * tm / 2) continue;  // a row tile mostly past M
+      if (WBITS == 4 && tm * tn > 8) continue;      // INT4 4 x 4 would spill registers
+      const double c = small_cost(a.M, a.N, a.K, WBITS, tm, tn);
+      if (c < best * 0.999) {
+        best = c;
+        best_tm = tm;
+        best_tn = tn;
+      }
+    }
+  if (force) {
+    best_tm = force / 10;
+    best_tn = force % 10;
+  }
+  // ring depth 2: deeper rings (up to 8 steps in flight) measured slower at M = 4..128
+#define MLS_SMALL(TM_, TN_) \
+  if (best_tm == TM_ && best_tn == TN_) return launch_small<WBITS, AT, ST, TM_, TN_, 2>(a, st)
+  MLS_SMALL(1, 1); MLS_SMALL(1, 2); MLS_SMALL(1, 4);
+  MLS_SMALL(2, 1); MLS_SMALL(2, 2); MLS_SMALL(2, 4);
+  MLS_SMALL(4, 1); MLS_SMALL(4, 2);
+  if constexpr (WBITS == 8) MLS_SMALL(4, 4);
+#undef MLS_SMALL
+  return MLS_ERR_UNSUPPORTED;
+}
+
+}  // namespace
+
+int launch_gemm_small(int wbits, const WqArgs& p) {
+  if (p.a_dt != MLS_BF16 && p.a_dt != MLS_F16) return MLS_ERR_UNSUPPORTED;
+  const int KS = wbits == 4 ? 128 : 64;
+  if (p.K % KS != 0 || p.K < KS) return MLS_ERR_UNSUPPORTED;
+  if (wbits == 4 && p.group % 128 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(p.a, 16) || p.lda % 8 != 0 || !aligned(p.w, 16) || p.ldw % 16 != 0) return MLS_ERR_UNSUPPORTED;
+  // 32-bit buffer offsets below the past-the-end soffset
+  if (p.M * p.lda * 2 >= kPastEnd / 2 || (p.N + 64) * p.ldw >= kPastEnd / 2) return MLS_ERR_UNSUPPORTED;
+  SmallArgs a{};
+  a.a = p.a; a.lda = (int)p.lda; a.a_bytes = (int)(p.M * p.lda * 2);
+  a.w = p.w; a.ldw = (int)p.ldw; a.w_bytes = (int)(p.N * p.ldw);
+  a.s = p.s; a.ld_sn = (int)p.ld_sn; a.ld_sg = (int)p.ld_sg; a.group = p.group;
+  a.c = p.c; a.ldc = (int)p.ldc; a.M = (int)p.M; a.N = (int)p.N; a.K = (int)p.K;
+  const int ssz = p.s_dt == MLS_F16 ? 2 : 4;
+  if (wbits == 4) {
+    a.G = (int)(p.K / p.group);
+    // scales through LDS as whole dwords per row: contiguous groups, dword-aligned rows,
+    // and a table of 64 rows that fits beside the reduction buffer
+    if (p.ld_sg != 1 || (a.G * ssz) % 4 != 0 || (p.ld_sn * ssz) % 4 != 0 || !aligned(p.s, 4))
+      return MLS_ERR_UNSUPPORTED;
+    if (64 * a.G * ssz + 1024 > 65536 || p.N * p.ld_sn * ssz >= kPastEnd / 2) return MLS_ERR_UNSUPPORTED;
+    a.s_bytes = (int)(p.N * p.ld_sn * ssz);
+  }
+  if (wbits == 4) {
+    if (p.a_dt == MLS_BF16) return p.s_dt == MLS_F16 ? dispatch_small<4, __bf16, _Float16>(a, p.stream)
+                                                     : dispatch_small<4, __bf16, float>(a, p.stream);
+    return p.s_dt == MLS_F16 ? dispatch_small<4, _Float16, _Float16>(a, p.stream)
+                             : dispatch_small<4, _Float16, float>(a, p.stream);
+  }
+  if (p.a_dt == MLS_BF16) return p.s_dt == MLS_F16 ? dispatch_small<8, __bf16, _Float16>(a, p.stream)
+                                                   : dispatch_small<8, __bf16, float>(a, p.stream);
+  return p.s_dt == MLS_F16 ? dispatch_small<8, _Float16, _Float16>(a, p.stream)
+                           : dispatch_small<8, _Float16, float>(a, p.stream);
+}
+
+}  // namespace mls

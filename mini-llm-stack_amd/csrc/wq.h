@@ -30,6 +30,10 @@ int launch_gemv_wq(int wbits, const WqArgs& p);
 // MLS_ERR_UNSUPPORTED outside its fast path.
 int launch_gemv_mfma(int wbits, const WqArgs& p);
 
+// Small / medium GEMM for 16-bit activations (MFMA operands straight into registers, K
+// split over a block's wavefronts). MLS_ERR_UNSUPPORTED outside its fast path.
+int launch_gemm_small(int wbits, const WqArgs& p);
+
 // MFMA tiled GEMM for 16-bit activations. MLS_ERR_UNSUPPORTED outside its fast path.
 int launch_gemm_wq_mfma(int wbits, const WqArgs& p);
 

@@ -34,12 +34,27 @@ int validate(const char* fn, int wbits, const WqArgs& p, int c_dt) {
   return MLS_OK;
 }
 
+// Whether a GEMM with 16-bit activations goes to the register-operand medium GEMM rather
+// than the LDS-tiled engine: the engine's 128 x 256 tiles need about 256 blocks to fill
+// the GPU, which a short or narrow problem does not give (2048 x 2048 at M = 128: 8
+// blocks). M <= 16 stays on the skinny GEMV, which measured faster there. MLS_SMALL = 0 / 1
+// forces it off / on for 2 <= M (sweeps).
+bool use_small(const WqArgs& p) {
+  static const int env = env_int("MLS_SMALL", -1);
+  if (p.a_dt == MLS_F32 || p.M < 2) return false;
+  if (env >= 0) return env != 0;
+  if (p.M <= 16) return false;
+  return p.M <= 256 && cdiv(p.M, 128) * cdiv(p.N, 256) < 128;
+}
+
 int run(const char* fn, int wbits, const WqArgs& p) {
   if (p.M == 0 || p.N == 0) return MLS_OK;
   int rc = MLS_ERR_UNSUPPORTED;
   if (p.K > 0) {
+    if (use_small(p)) rc = launch_gemm_small(wbits, p);
     const bool small_m = p.a_dt == MLS_F32 || p.M <= 16;
-    if (small_m) {
+    if (rc != MLS_ERR_UNSUPPORTED) {
+    } else if (small_m) {
       if (p.M >= 2 && p.a_dt != MLS_F32) rc = launch_gemv_mfma(wbits, p);
       if (rc == MLS_ERR_UNSUPPORTED) rc = launch_gemv_wq(wbits, p);
     } else {

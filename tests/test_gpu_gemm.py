@@ -212,6 +212,50 @@ def test_skinny_int8(dev, M, N, K, dtype):
            f"skinny int8 M={M} N={N} K={K}")
 
 
+# --------------------------------------------------------------- medium path (16 < M <= 256, few tiles)
+
+@pytest.mark.parametrize("M,N,K,dtype", [
+    (128, 2048, 2048, torch.float16),    # reference bench shape
+    (17, 1000, 1088, torch.bfloat16),    # one row past a tile, ragged N, 17 steps over 4 wavefronts
+    (100, 333, 64, torch.bfloat16),      # a single step, odd N
+    (250, 4096, 4096, torch.float16),    # near the top of the range: 4 x 4 tiles
+])
+def test_medium_int8(dev, M, N, K, dtype):
+    a, w = _data(M, N, K, 800 + M, 0.02)
+    q, s = quantize_int8(w.to(dev))
+    s16 = s.to(torch.float16)
+    ax = a.to(dtype)
+    _check(int8_matmul(ax.to(dev), q, s16),
+           ref.int8_matmul(ax.float().numpy(), q.cpu().numpy(), s16.float().cpu().numpy()),
+           f"medium int8 M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("M,N,K,gs,dtype", [
+    (128, 2048, 2048, 128, torch.float16),
+    (40, 1000, 1152, 128, torch.bfloat16),   # 9 steps: wavefronts of 2 and 3 steps
+    (200, 520, 768, 256, torch.float16),     # a group spans two steps
+    (33, 4096, 4096, 128, torch.bfloat16),
+    (128, 2048, 2048, 64, torch.float16),    # group 64: not this path (engine), same answer
+])
+def test_medium_int4(dev, M, N, K, gs, dtype):
+    a, p, s, want = _int4_setup(dev, M, N, K, gs, 900 + M, dtype)
+    _check(int4_matmul(a, p, s, gs), want, f"medium int4 M={M} N={N} K={K} g{gs}")
+
+
+def test_medium_f32_scales_strided_rows(dev):
+    M, N, K, gs = 70, 640, 1024, 128
+    a, w = _data(M, N, K, 950, 0.02)
+    p, s = quantize_int4(w.to(dev), gs)  # fp32 scales
+    wide = torch.zeros(M, K + 64, dtype=torch.bfloat16)
+    wide[:, :K] = a.to(torch.bfloat16)
+    x = wide.to(dev)[:, :K]  # lda = K + 64
+    want = ref.int4_matmul(wide[:, :K].float().numpy(), p.cpu().numpy(), s.cpu().numpy(), gs)
+    _check(int4_matmul(x, p, s, gs), want, "medium int4 fp32 scales, strided rows")
+    q, s8 = quantize_int8(w.to(dev))  # fp32 row scales
+    _check(int8_matmul(x, q, s8), ref.int8_matmul(wide[:, :K].float().numpy(), q.cpu().numpy(),
+                                                  s8.cpu().numpy()), "medium int8 fp32 scales")
+
+
 # --------------------------------------------------------------- prefill (MFMA) path
 
 @pytest.mark.parametrize("M,N,K", [(17, 256, 256), (64, 512, 512), (100, 300, 320),
