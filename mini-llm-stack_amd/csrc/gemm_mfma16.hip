@@ -616,7 +616,8 @@ static int pick_bm(int64_t M, int64_t N, int max_bm) {
   return best;
 }
 
-// Tuning overrides for sweeps: MLS_MFMA_WAVES = 4 or 8 wavefronts per block (default 8:
+// Tuning overrides for sweeps: MLS_BYTES = 0 keeps 256-row exact fp8 tiles on the kernel here
+// instead of the byte-operand kernel (gemm_bytes.hip), MLS_MFMA_WAVES = 4 or 8 wavefronts per block (default 8:
 // two per SIMD, so one wavefront's memory waits overlap the other's MFMAs), MLS_MFMA_BM =
 // forced row-tile height (16 .. 256), MLS_MFMA_ADMA = 0 stages 16-bit activations
 // through registers instead of loading them straight into LDS, MLS_MFMA_BN = 256 or 192
@@ -632,6 +633,12 @@ static int dense16(Mfma16Params p, hipStream_t st) {
   p.m_tiles = (int)cdiv(p.M, bm);
   const bool w8 = waves == 8;
   static const bool adma = env_int("MLS_MFMA_ADMA", 1) != 0;
+  static const bool bytes = env_int("MLS_BYTES", 1) != 0;
+  if (bytes && w8 && bm == 256) {
+    if constexpr (AKIND != A_RAW16 && BKIND == B_E4M3)
+      return launch_bytes_fp8(p, st, AKIND == A_E5M2,
+                              __is_same(OT, float) ? MLS_F32 : __is_same(OT, _Float16) ? MLS_F16 : MLS_BF16);
+  }
   if constexpr (AKIND == A_RAW16) {
     if (adma && w8 && bm == 256) {
       if constexpr (MAXBM >= 256) {

@@ -158,6 +158,10 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t rs, void* lds,
                                            soff, 0, 0);
 }
 
+// The exact e4m3 / e5m2 GEMM on 256-row tiles with both operands kept as bytes in LDS
+// (gemm_bytes.hip); c_dt: output type.
+int launch_bytes_fp8(const Mfma16Params& p, hipStream_t st, bool a_e5m2, int c_dt);
+
 // Grouped INT4 GEMM with one block per (expert row chunk, 128 columns) (gemm_grouped.hip);
 // gate_up: the gate/up pair of a SwiGLU expert MLP (p.b/p.s gate, p.b2/p.s2 up), output
 // silu(gate) * up.
