@@ -244,6 +244,28 @@ def int8_prefill(dev, steps: int, warmup: int, M=2048, N=11008, K=4096):
     return dict(ms=ms, bytes=nbytes, flops=2 * M * N * K, copies=copies, parity=par)
 
 
+def int8_dgrad_row(dev, steps: int, warmup: int, M=4096, N=11008, K=4096):
+    """The INT8 STE backward's input gradient at a training shape (kernels/dequant_matmul.py:
+    103-132): dx [M, K] = (dy [M, N] * s) @ W_q [N, K], bf16 dy. One step is the whole op:
+    dy * s to bf16, the transposed weight copy, and the GEMM."""
+    import torch
+    from kernels.dequant_matmul import int8_dgrad
+    from serve.quantize import quantize_int8
+    g = torch.Generator(device=dev).manual_seed(5)
+    q, s = quantize_int8(torch.randn(N, K, generator=g, device=dev) * 0.02)
+    copies = 3
+    dys = [torch.randn(M, N, generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+    qs = [q] + [q.clone() for _ in range(copies - 1)]
+    r = _rows(M)
+    # the reference's arithmetic: dy * s rounded to bf16, then the dot (dequant_matmul.py:128)
+    par = gate(int8_dgrad(dys[0], q, s)[r],
+               (dys[0][r].float() * s.float()[None, :]).to(torch.bfloat16).float() @ q.float(), "bf16")
+    fns = [lambda i=i: int8_dgrad(dys[i], qs[i], s) for i in range(copies)]
+    ms = time_steps(fns, warmup, steps) if par["ok"] else None
+    nbytes = M * N * 2 + N * K + N * 4 + M * K * 2
+    return dict(ms=ms, bytes=nbytes, flops=2 * M * N * K, copies=copies, parity=par)
+
+
 def fp8_gemm(dev, steps: int, warmup: int, M=4096, N=8192, K=8192, native=False):
     import torch
     from kernels.fp8_matmul import E4M3_MAX, fp8_matmul, quantize_e4m3
@@ -729,6 +751,9 @@ def main(argv=None) -> int:
         "int8_gemv": lambda: _hbm_row("int8_gemv_m1", int8_gemv(dev, 1, args.steps, args.warmup)),
         "int8_prefill": lambda: _mfma_row("int8_prefill_2048x11008x4096",
                                           int8_prefill(dev, small, 4), BF16_PEAK_TFLOPS),
+        "int8_dgrad": lambda: _mfma_row("int8_dgrad_4096x11008x4096_bf16", int8_dgrad_row(dev, small, 4),
+                                        BF16_PEAK_TFLOPS,
+                                        {"launches": "dy*s to bf16, W_q^T copy, INT8 MFMA GEMM (unit scales)"}),
         "fp8_gemm": lambda: _mfma_row("fp8_e4m3_4096x8192x8192_exact", fp8_gemm(dev, small, 4),
                                       FP8_PEAK_TFLOPS, {"datapath": "e4m3 widened to bf16, bf16 MFMA",
                                                         "bf16_roofline_frac": None}),
@@ -787,7 +812,7 @@ def main(argv=None) -> int:
         return 1
     extra = []
     if not args.no_extra:
-        for k in ("int4_m4", "int4_m16", "int8_gemv", "int8_prefill", "fp8_gemm", "fp8_native",
+        for k in ("int4_m4", "int4_m16", "int8_gemv", "int8_prefill", "int8_dgrad", "fp8_gemm", "fp8_native",
                   "fp8_bwd", "fp8_bwd_native", "moe_int4", "moe_mlp_int4", "paged_attn", "quantize_int4",
                   "ref_shapes", "copy", "vendor_fp8_rowwise", "vendor_fp8_tensorwise", "vendor_bf16"):
             log(f"{k} ...")

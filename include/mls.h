@@ -144,6 +144,20 @@ int mls_int8_dgrad(const void* dy, int dy_dt, int64_t lddy,
                    void* dx, int dx_dt, int64_t lddx,
                    int64_t M, int64_t N, int64_t K, mls_stream_t stream);
 
+/* The same input gradient on the matrix cores, with the reference's arithmetic
+ * (kernels/dequant_matmul.py:127-128): ys = (dy * s) rounded to dy's dtype, times the int8
+ * weights on the 16-bit MFMA, fp32 accumulation. Needs a caller workspace of
+ * mls_int8_dgrad_workspace(M, N, K, dy_dt) bytes, 256-byte aligned (the scaled dy, the
+ * transposed weights and a vector of ones); 0 means this shape takes mls_int8_dgrad's
+ * route (fp32 dy), for which workspace may be null. Runs on `stream`, three launches. */
+int64_t mls_int8_dgrad_workspace(int64_t M, int64_t N, int64_t K, int dy_dt);
+int mls_int8_dgrad_ws(const void* dy, int dy_dt, int64_t lddy,
+                      const int8_t* w, int64_t ldw,
+                      const void* s, int s_dt,
+                      void* dx, int dx_dt, int64_t lddx,
+                      int64_t M, int64_t N, int64_t K,
+                      void* workspace, int64_t ws_bytes, mls_stream_t stream);
+
 /* Replaces _fp8_matmul_kernel + fp8_matmul (kernels/fp8_matmul.py:50-81, 113-128):
  * c[m][n] = (sum_k e4m3(a[m][k]) * e4m3(b[n][k])) * sa_m * sb_n, fp32 accumulation.
  * sa_m = sa_ptr ? sa_ptr[m * sa_stride] : sa, likewise sb_n: per-tensor (the

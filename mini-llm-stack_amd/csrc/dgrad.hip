@@ -2,10 +2,20 @@
 // (kernels/dequant_matmul.py:103-132): the transpose-side GEMM of the INT8
 // straight-through estimator. Reduction over N, which is the slow axis of wq.
 //
-// Block tile 64 (m) x 64 (k), 256 threads, each computing a 4 x 4 patch with
-// fp32 FMAs from LDS tiles of 32 n: dy*s is formed in fp32 (the reference
-// rounds it to dy's dtype first; fp32 is closer to the dequantize-then-fp32
-// oracle) and int8 weights are exact in fp32.
+// Two routes:
+//  - matrix cores (mls_int8_dgrad_ws, 16-bit dy): the reference's own arithmetic, the
+//    product (dy * s) rounded to dy's dtype (dequant_matmul.py:128) times the int8 weights
+//    (exact in bf16 / fp16) on the 16-bit MFMA with fp32 accumulation. Three launches on
+//    the caller's stream into a caller workspace: (1) ys = dy * s in dy's dtype, columns
+//    padded with zeros to Np = N rounded up to 64, and a vector of K ones; (2) wt = wq^T
+//    [K][Np] (mls_transpose_u8; its padding columns stay unwritten, and multiply only the
+//    zeros of ys); (3) the INT8 weight-only GEMM dx = ys wt^T with unit row scales
+//    (mls_int8_gemm), whose reduction axis is now contiguous in both operands.
+//  - VALU (mls_int8_dgrad, and fp32 dy): block tile 64 (m) x 64 (k), 256 threads, each
+//    computing a 4 x 4 patch with fp32 FMAs from LDS tiles of 32 n, dy * s formed in fp32
+//    (closer to the dequantize-then-fp32 oracle than the reference's rounding).
+#include <algorithm>
+
 #include "common.h"
 
 namespace mls {
@@ -65,9 +75,67 @@ __global__ __launch_bounds__(256) void int8_dgrad_kernel(const T* __restrict__ d
   }
 }
 
+// ys[m][n] = T(dy[m][n] * s[n]) for n < N, 0 for N <= n < Np; ones[k] = 1 for k < K.
+// One thread per 8 consecutive n of a row.
+template <typename T>
+__global__ __launch_bounds__(256) void dgrad_scale_kernel(const T* __restrict__ dy, int64_t lddy,
+                                                          const void* __restrict__ s, int s_dt,
+                                                          T* __restrict__ ys, int64_t Np, float* __restrict__ ones,
+                                                          int M, int N, int K) {
+  const int64_t per_row = Np / 8;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t < K) ones[t] = 1.0f;
+  if (t >= (int64_t)M * per_row) return;
+  const int64_t m = t / per_row;
+  const int n0 = (int)(t - m * per_row) * 8;
+  uint32_t o[4];
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    float v[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int n = n0 + 2 * h + e;
+      v[e] = 0.0f;
+      if (n < N) {
+        const float sn = s_dt == MLS_F16 ? (float)((const _Float16*)s)[n] : ((const float*)s)[n];
+        v[e] = to_f32(dy[m * lddy + n]) * sn;
+      }
+    }
+    o[h] = pack2_bits(from_f32<T>(v[0]), from_f32<T>(v[1]));
+  }
+  *reinterpret_cast<uint4*>(ys + m * Np + n0) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// Workspace layout of the matrix-core route (each part 256-byte aligned).
+struct DgradWs {
+  int64_t Np, ys_off, wt_off, ones_off, bytes;
+};
+DgradWs dgrad_ws(int64_t M, int64_t N, int64_t K) {
+  DgradWs w;
+  w.Np = cdiv(N, 64) * 64;
+  const auto up = [](int64_t b) { return cdiv(b, 256) * 256; };
+  w.ys_off = 0;
+  w.wt_off = up(M * w.Np * 2);
+  w.ones_off = w.wt_off + up(K * w.Np);
+  w.bytes = w.ones_off + up(K * 4);
+  return w;
+}
+
+// Shapes the matrix-core route takes: 16-bit dy, and the INT8 GEMM's 32-bit tile offsets.
+bool dgrad_mfma_ok(int dy_dt, int64_t M, int64_t N, int64_t K) {
+  if (dy_dt != MLS_BF16 && dy_dt != MLS_F16) return false;
+  const int64_t Np = cdiv(N, 64) * 64;
+  return M <= 0x3FFFFFFF && K <= 0x3FFFFFFF && Np * 2 * 256 < (1ll << 31) && M * (Np / 8) < (1ll << 40);
+}
+
 }  // namespace mls
 
 using namespace mls;
+
+extern "C" int64_t mls_int8_dgrad_workspace(int64_t M, int64_t N, int64_t K, int dy_dt) {
+  if (M <= 0 || N <= 0 || K <= 0 || !dgrad_mfma_ok(dy_dt, M, N, K)) return 0;
+  return dgrad_ws(M, N, K).bytes;
+}
 
 extern "C" int mls_int8_dgrad(const void* dy, int dy_dt, int64_t lddy, const int8_t* w, int64_t ldw,
                               const void* s, int s_dt, void* dx, int dx_dt, int64_t lddx, int64_t M,
@@ -95,4 +163,43 @@ extern "C" int mls_int8_dgrad(const void* dy, int dy_dt, int64_t lddy, const int
     hipLaunchKernelGGL(int8_dgrad_kernel<__bf16>, grid, dim3(256), 0, st, (const __bf16*)dy, lddy,
                        w, ldw, s, s_dt, (__bf16*)dx, lddx, (int)M, (int)N, (int)K);
   return check_launch("mls_int8_dgrad");
+}
+
+extern "C" int mls_int8_dgrad_ws(const void* dy, int dy_dt, int64_t lddy, const int8_t* w, int64_t ldw,
+                                 const void* s, int s_dt, void* dx, int dx_dt, int64_t lddx, int64_t M,
+                                 int64_t N, int64_t K, void* workspace, int64_t ws_bytes,
+                                 mls_stream_t stream) {
+  const int64_t need = mls_int8_dgrad_workspace(M, N, K, dy_dt);
+  if (need == 0)  // nothing to do, or the VALU route (fp32 dy): no workspace needed
+    return mls_int8_dgrad(dy, dy_dt, lddy, w, ldw, s, s_dt, dx, dx_dt, lddx, M, N, K, stream);
+  if (dx_dt != dy_dt)
+    return fail(MLS_ERR_ARG, "mls_int8_dgrad_ws: dy/dx dtypes %d/%d (must match)", dy_dt, dx_dt);
+  if (s_dt != MLS_F32 && s_dt != MLS_F16)
+    return fail(MLS_ERR_ARG, "mls_int8_dgrad_ws: scale dtype %d (f32 or f16)", s_dt);
+  if (!dy || !w || !s || !dx) return fail(MLS_ERR_ARG, "mls_int8_dgrad_ws: null pointer");
+  if (lddy < N || ldw < K || lddx < K) return fail(MLS_ERR_ARG, "mls_int8_dgrad_ws: bad leading dimension");
+  if (!workspace || ws_bytes < need || !aligned(workspace, 256))
+    return fail(MLS_ERR_ARG, "mls_int8_dgrad_ws: workspace of %lld bytes at %p (need %lld, 256-byte aligned)",
+                (long long)ws_bytes, workspace, (long long)need);
+  const DgradWs L = dgrad_ws(M, N, K);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  void* ys = ws + L.ys_off;
+  uint8_t* wt = ws + L.wt_off;
+  float* ones = reinterpret_cast<float*>(ws + L.ones_off);
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t threads = std::max<int64_t>(M * (L.Np / 8), K);
+  const dim3 grid((unsigned)cdiv(threads, 256));
+  if (cdiv(threads, 256) > 0x7FFFFFFF) return fail(MLS_ERR_UNSUPPORTED, "mls_int8_dgrad_ws: shape too large");
+  if (dy_dt == MLS_F16)
+    hipLaunchKernelGGL(dgrad_scale_kernel<_Float16>, grid, dim3(256), 0, st, (const _Float16*)dy, lddy, s,
+                       s_dt, (_Float16*)ys, L.Np, ones, (int)M, (int)N, (int)K);
+  else
+    hipLaunchKernelGGL(dgrad_scale_kernel<__bf16>, grid, dim3(256), 0, st, (const __bf16*)dy, lddy, s, s_dt,
+                       (__bf16*)ys, L.Np, ones, (int)M, (int)N, (int)K);
+  int rc = check_launch("mls_int8_dgrad_ws (scale)");
+  if (rc != MLS_OK) return rc;
+  rc = mls_transpose_u8(reinterpret_cast<const uint8_t*>(w), N, K, ldw, wt, L.Np, stream);
+  if (rc != MLS_OK) return rc;
+  return mls_int8_gemm(ys, dy_dt, L.Np, reinterpret_cast<const int8_t*>(wt), L.Np, ones, MLS_F32, dx, dx_dt,
+                       lddx, M, K, L.Np, stream);
 }

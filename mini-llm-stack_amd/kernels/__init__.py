@@ -68,6 +68,9 @@ SIGNATURES = {
     "mls_int4_gemm": ([_P, _I, _I64, _P, _I64, _P, _I, _I64, _I64, _I, _P, _I, _I64,
                        _I64, _I64, _I64, _P], _I),
     "mls_int8_dgrad": ([_P, _I, _I64, _P, _I64, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P], _I),
+    "mls_int8_dgrad_workspace": ([_I64, _I64, _I64, _I], _I64),
+    "mls_int8_dgrad_ws": ([_P, _I, _I64, _P, _I64, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P],
+                          _I),
     "mls_fp8_gemm": ([_P, _I64, _P, _I64, _F, _P, _I64, _F, _P, _I64, _P, _I, _I64,
                       _I64, _I64, _I64, _I, _P], _I),
     "mls_int4_grouped_gemm": ([_P, _I, _I64, _P, _I, _I64, _P, _I64, _I64, _P, _I, _I64,

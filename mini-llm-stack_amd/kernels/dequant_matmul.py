@@ -60,9 +60,14 @@ def int8_dgrad(dy: torch.Tensor, w_q: torch.Tensor, scale: torch.Tensor):
     dy, w_q = rows(dy), rows(w_q)
     s, sdt = scale_vector(scale.reshape(-1).contiguous())
     dx = torch.empty(M, K, dtype=dy.dtype, device=dev)
-    kernels.check(kernels.lib().mls_int8_dgrad(
+    lib = kernels.lib()
+    # 16-bit dy: the matrix-core route, with its scratch (scaled dy, transposed weights)
+    # from torch's caching allocator; fp32 dy: the VALU kernel, no workspace
+    need = lib.mls_int8_dgrad_workspace(M, N, K, ddt)
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    kernels.check(lib.mls_int8_dgrad_ws(
         dy.data_ptr(), ddt, ld(dy), w_q.data_ptr(), ld(w_q), s.data_ptr(), sdt,
-        dx.data_ptr(), ddt, ld(dx), M, N, K, stream(dev)), "int8_dgrad")
+        dx.data_ptr(), ddt, ld(dx), M, N, K, ws.data_ptr(), need, stream(dev)), "int8_dgrad")
     return dx
 
 

@@ -19,6 +19,10 @@ Each function cites the reference code it restates. Pins (see tests/test_oracle.
   dequantize_*     closed form; brute-force per-element loop on tiny inputs.
   *_matmul         fp64 brute-force triple loop on tiny inputs; golden fixture
                    of config A produced by torch's fp32 matmul.
+  int8_dgrad       fp64 brute force on tiny inputs; the rounding of dy * s for 16-bit
+                   dy by known answers where it changes the result (1 + 2^-7 times
+                   1 + 2^-8 is 1 + 2^-6 in bf16) and round_to against torch's bf16 /
+                   fp16 casts on random values and ties.
   route / sort     torch softmax/topk/argsort golden fixture.
   silu             closed forms: silu(0) = 0, silu(x) - silu(-x) = x, silu(x) -> x
                    and -> 0 at the tails; torch.nn.functional.silu on the CPU.
@@ -242,9 +246,27 @@ def int4_matmul(a, packed, scale, group_size) -> np.ndarray:
     return (_f32(a) @ dequantize_int4(packed, scale, group_size).T).astype(np.float32)
 
 
-def int8_dgrad(dy, w_q, scale) -> np.ndarray:
-    """(dy * s) @ w_q in fp32 (kaggle/gpu_smoke.py:133-135; dequant_matmul.py:103-132)."""
-    return ((_f32(dy) * _f32(scale)[None, :]) @ np.asarray(w_q).astype(np.float32)).astype(np.float32)
+def round_to(x, dtype: str) -> np.ndarray:
+    """fp32 values rounded to the nearest bf16 / fp16 (ties to even), returned as fp32.
+    bf16: round the fp32 bit pattern at bit 16 (NaN kept); fp16: numpy's float16 cast."""
+    x = _f32(x)
+    if dtype == "fp16":
+        return x.astype(np.float16).astype(np.float32)
+    assert dtype == "bf16", dtype
+    u = x.view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    return np.where(np.isnan(x), x, r.view(np.float32))
+
+
+def int8_dgrad(dy, w_q, scale, product_dtype: str | None = None) -> np.ndarray:
+    """(dy * s) @ w_q, fp32 accumulation (dequant_matmul.py:103-132; kaggle/gpu_smoke.py:
+    133-135 for fp32 dy). The reference forms dy * s in fp32 and rounds it to dy's dtype
+    before the dot ((dy * s[None, :]).to(dy.dtype), dequant_matmul.py:128): pass
+    product_dtype "bf16" / "fp16" for 16-bit dy, None for fp32 dy (no rounding)."""
+    ys = _f32(dy) * _f32(scale)[None, :]
+    if product_dtype is not None:
+        ys = round_to(ys, product_dtype)
+    return (ys @ np.asarray(w_q).astype(np.float32)).astype(np.float32)
 
 
 def fp8_matmul(a_bits, b_bits, sa, sb) -> np.ndarray:

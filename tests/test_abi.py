@@ -24,7 +24,7 @@ def declared_symbols() -> list[str]:
 
 def test_header_declares_the_boundary():
     syms = declared_symbols()
-    assert len(syms) == len(set(syms)) == 23
+    assert len(syms) == len(set(syms)) == 25
     assert set(syms) == set(kernels.SIGNATURES)
 
 
@@ -121,6 +121,32 @@ def test_grouped_reject_empty_k():
     rc, msg = _err(L.mls_int4_grouped_gemm_partial(1, bf, 64, 1, 2, 8, 1, 0, 32, 1, kernels.MLS_F16, 0, 2, 1,
                                                    32, 1, 1, 16, 128, 16, 0, NULL))
     assert rc == kernels.MLS_ERR_ARG and "K=0" in msg
+
+
+def test_dgrad_workspace_and_rejects():
+    """The matrix-core dgrad's workspace: scaled dy [M][Np] 16-bit + transposed weights
+    [K][Np] bytes + K fp32 ones, Np = N rounded up to 64, each part 256-byte aligned; 0 for
+    fp32 dy (the VALU route). A short or misaligned workspace is rejected on the host."""
+    L = kernels.load_library()
+    bf = kernels.MLS_BF16
+    M, N, K = 40, 100, 72
+    Np = 128
+    up = lambda b: -(-b // 256) * 256
+    assert L.mls_int8_dgrad_workspace(M, N, K, bf) == up(M * Np * 2) + up(K * Np) + up(K * 4)
+    assert L.mls_int8_dgrad_workspace(M, N, K, kernels.MLS_F16) == up(M * Np * 2) + up(K * Np) + up(K * 4)
+    assert L.mls_int8_dgrad_workspace(M, N, K, kernels.MLS_F32) == 0
+    assert L.mls_int8_dgrad_workspace(0, N, K, bf) == 0
+    need = L.mls_int8_dgrad_workspace(M, N, K, bf)
+    args = (1, bf, N, 1, K, 1, kernels.MLS_F32, 1, bf, K, M, N, K)
+    rc, msg = _err(L.mls_int8_dgrad_ws(*args, 256, need - 1, NULL))
+    assert rc == kernels.MLS_ERR_ARG and "workspace" in msg
+    rc, msg = _err(L.mls_int8_dgrad_ws(*args, 256 + 16, need, NULL))
+    assert rc == kernels.MLS_ERR_ARG and "aligned" in msg
+    rc, msg = _err(L.mls_int8_dgrad_ws(*args, NULL, need, NULL))
+    assert rc == kernels.MLS_ERR_ARG
+    rc, msg = _err(L.mls_int8_dgrad_ws(1, bf, N, 1, K, 1, kernels.MLS_F32, 1, kernels.MLS_F16, K, M, N, K,
+                                       256, need, NULL))
+    assert rc == kernels.MLS_ERR_ARG and "dtypes" in msg
 
 
 def test_gate_up_and_combine_reject():

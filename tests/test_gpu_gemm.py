@@ -315,12 +315,48 @@ def test_empty_m(dev):
 
 # --------------------------------------------------------------- INT8 dgrad
 
-@pytest.mark.parametrize("M,N,K", [(9, 24, 32), (33, 256, 512), (130, 300, 70)])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+# the reference rounds dy * s to dy's dtype before the dot (dequant_matmul.py:128)
+_PRODUCT = {torch.float32: None, torch.bfloat16: "bf16", torch.float16: "fp16"}
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 24, 32), (33, 256, 512), (130, 300, 70), (300, 1000, 520)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_int8_dgrad(dev, M, N, K, dtype):
     g = torch.Generator().manual_seed(M + N)
     dy = torch.randn(M, N, generator=g).to(dtype)
     q, s = quantize_int8(torch.randn(N, K, generator=g))
     out = int8_dgrad(dy.to(dev), q.to(dev), s.to(dev))
     assert out.dtype == dtype and out.shape == (M, K)
-    _check(out, ref.int8_dgrad(dy.float().numpy(), q.numpy(), s.numpy()), f"dgrad {M}x{N}x{K}")
+    _check(out, ref.int8_dgrad(dy.float().numpy(), q.numpy(), s.numpy(), _PRODUCT[dtype]),
+           f"dgrad {M}x{N}x{K}")
+
+
+def test_int8_dgrad_training_shape(dev):
+    """The STE backward at a training shape: dy [4096, 11008] bf16 x W_q [11008, 4096] on the
+    matrix cores. Every output against torch fp32 of the reference's product on the GPU
+    ((dy * s) rounded to bf16, times W_q, fp32 accumulation), within the bf16 tolerance
+    |d| <= 1e-2 + 1e-2 |ref|; sampled rows against the CPU oracle."""
+    M, N, K = 4096, 11008, 4096
+    g = torch.Generator(device=dev).manual_seed(7)
+    dy = torch.randn(M, N, generator=g, device=dev).to(torch.bfloat16)
+    q, s = quantize_int8(torch.randn(N, K, generator=g, device=dev) * 0.02)
+    out = int8_dgrad(dy, q, s)
+    assert out.dtype == torch.bfloat16 and out.shape == (M, K)
+    want = (dy.float() * s.float()[None, :]).to(torch.bfloat16).float() @ q.float()
+    err = (out.float() - want).abs() - (1e-2 + 1e-2 * want.abs())
+    assert float(err.max()) <= 0, f"dgrad training shape: worst excess {float(err.max()):.3g}"
+    rows = [0, 1, 2049, 4095]
+    _check(out[rows], ref.int8_dgrad(dy[rows].float().cpu().numpy(), q.cpu().numpy(), s.cpu().numpy(), "bf16"),
+           "dgrad training shape rows")
+
+
+def test_int8_dgrad_strided_and_f16_scales(dev):
+    M, N, K = 70, 192, 256
+    g = torch.Generator().manual_seed(11)
+    wide = torch.randn(M, N + 40, generator=g).to(torch.bfloat16)
+    q, s = quantize_int8(torch.randn(N, K, generator=g))
+    s16 = s.to(torch.float16)
+    dyv = wide.to(dev)[:, 8:8 + N]  # row stride N + 40, offset 16 bytes
+    out = int8_dgrad(dyv, q.to(dev), s16.to(dev))
+    _check(out, ref.int8_dgrad(wide[:, 8:8 + N].float().numpy(), q.numpy(), s16.float().numpy(), "bf16"),
+           "dgrad strided dy, fp16 scales")

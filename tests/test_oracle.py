@@ -201,6 +201,45 @@ def test_int8_dgrad_brute_force():
     assert np.allclose(ref.int8_dgrad(dy, q, s), dx, rtol=1e-5, atol=1e-5)
 
 
+def test_int8_dgrad_rounds_the_product_for_16bit_dy():
+    """The reference rounds dy * s to dy's dtype before the dot (dequant_matmul.py:128).
+    Known answers where that changes the result: bf16 (1 + 2^-7)(1 + 2^-8) = 1 + 1.5 2^-7
+    + 2^-15 rounds up to 1 + 2^-6; fp16 (1 + 2^-10)(1 + 2^-11) rounds up to 1 + 2^-9. A
+    planted omission of the rounding fails both."""
+    one = np.ones((1, 1), dtype=np.int8)
+    dy = np.array([[1 + 2.0 ** -7]], np.float32)
+    s = np.array([1 + 2.0 ** -8], np.float32)
+    assert ref.int8_dgrad(dy, one, s, "bf16")[0, 0] == np.float32(1 + 2.0 ** -6)
+    assert ref.int8_dgrad(dy, one, s)[0, 0] == np.float32((1 + 2.0 ** -7) * (1 + 2.0 ** -8))
+    dy = np.array([[1 + 2.0 ** -10]], np.float32)
+    s = np.array([1 + 2.0 ** -11], np.float32)
+    assert ref.int8_dgrad(dy, one, s, "fp16")[0, 0] == np.float32(1 + 2.0 ** -9)
+    # rounding happens per product, before the sum: 4 products just above a tie
+    q = np.ones((4, 1), dtype=np.int8)
+    dy = np.full((1, 4), 1 + 2.0 ** -7, np.float32)
+    s = np.full(4, 1 + 2.0 ** -8, np.float32)
+    assert ref.int8_dgrad(dy, q, s, "bf16")[0, 0] == np.float32(4 * (1 + 2.0 ** -6))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+def test_round_to_matches_torch_casts(dt):
+    g = np.random.default_rng(9)
+    x = np.concatenate([g.standard_normal(4096).astype(np.float32) * 10.0 ** g.integers(-6, 6, 4096),
+                        np.array([0.0, -0.0, 1.0, 65504.0, 3e38, -3e38, np.inf, -np.inf], np.float32)])
+    # exact ties of the 16-bit grid: halfway points (round to even both ways)
+    base = g.standard_normal(512).astype(np.float32)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    b16 = torch.from_numpy(base).to(tdt)
+    nxt = torch.nextafter(b16.float().to(tdt).float(), torch.full_like(b16.float(), np.inf)).to(tdt)
+    ties = ((b16.float() + nxt.float()) / 2).numpy()
+    x = np.concatenate([x, ties]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        want = torch.from_numpy(x).to(tdt).float().numpy()
+        got = ref.round_to(x, dt)
+    assert np.array_equal(got, want, equal_nan=True)
+    assert np.isnan(ref.round_to(np.array([np.nan], np.float32), dt)).all()
+
+
 def test_fp8_matmul_brute_force_per_row_scales():
     g = np.random.default_rng(5)
     ab = g.integers(0, 256, size=(3, 9), dtype=np.uint8)
