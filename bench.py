@@ -396,14 +396,15 @@ def moe_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=128):
     a = gather_rows(x, tok)
     sets = [_int4_experts(dev, g, E, H, D, gs) for _ in range(2)]
     cl = counts.tolist()
-    y = int4_grouped_matmul(a, sets[0][0], sets[0][1], counts, gs)
+    # the dispatch gather runs inside the grouped kernel's activation load (a_rows = tok)
+    y = int4_grouped_matmul(x, sets[0][0], sets[0][1], counts, gs, a_rows=tok)
     rs, es = _segment_rows(cl)
     want = torch.empty(len(rs), H, device=dev)
     for e in sorted(set(es)):
         sel = [i for i, ee in enumerate(es) if ee == e]
         want[sel] = a[[rs[i] for i in sel]].float() @ _deq4(sets[0][0][e], sets[0][1][e], gs).t()
     par = gate(y[rs], want, "bf16")
-    fns = [lambda st=st: int4_grouped_matmul(a, st[0], st[1], counts, gs) for st in sets]
+    fns = [lambda st=st: int4_grouped_matmul(x, st[0], st[1], counts, gs, a_rows=tok) for st in sets]
     ms = time_steps(fns, warmup, steps) if par["ok"] else None
     rows_ = T * 2
     nbytes = E * H * D // 2 + E * H * (D // gs) * 2 + rows_ * D * 2 + rows_ * H * 2
@@ -411,9 +412,10 @@ def moe_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=128):
 
 
 def moe_mlp_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=128):
-    """The whole INT4 SwiGLU expert MLP of a routed MoE layer after dispatch: the fused
-    gate/up launch (silu(x Wg^T) * x Wu^T), the down launch, and the weighted combine
-    back to token order (kernels/moe_routing.py:145-153 with INT4 experts). The gate
+    """The whole INT4 SwiGLU expert MLP of a routed MoE layer after routing: the fused
+    gate/up launch with the dispatch gather in its activation load (silu(x Wg^T) * x Wu^T),
+    the down launch, and the weighted combine back to token order
+    (kernels/moe_routing.py:144-153 with INT4 experts). The gate
     checks the gate/up output against fp32 silu(gate) * up, and the layer output
     against an fp32 down projection and combine of that bf16 h (one GEMM against its
     fp32 oracle at a time, as the tests do)."""
@@ -435,8 +437,9 @@ def moe_mlp_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=1
         sets.append(mats)
     wg, sg, wu, su, wd, sd = sets[0]
     cl = counts.tolist()
-    h = int4_grouped_gate_up(a, wg, sg, wu, su, off, gs)
-    y = int4_expert_mlp_combine(a, off, *sets[0], gs, w, pos)
+    # the dispatch gather runs inside the gate/up kernel's activation load (a_rows = tok)
+    h = int4_grouped_gate_up(x, wg, sg, wu, su, off, gs, a_rows=tok)
+    y = int4_expert_mlp_combine(x, off, *sets[0], gs, w, pos, a_rows=tok)
     rs, es = _segment_rows(cl)
     hw = torch.empty(len(rs), H, device=dev)
     for e in sorted(set(es)):
@@ -458,7 +461,7 @@ def moe_mlp_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=1
     del deq_d
     p2 = gate(y[toks], want, "bf16")
     par = {"gate_up": p1, "down_combine": p2, "ok": p1["ok"] and p2["ok"]}
-    fns = [lambda m=m: int4_expert_mlp_combine(a, off, *m, gs, w, pos) for m in sets]
+    fns = [lambda m=m: int4_expert_mlp_combine(x, off, *m, gs, w, pos, a_rows=tok) for m in sets]
     ms = time_steps(fns, warmup, steps) if par["ok"] else None
     rows_ = T * 2
     nbytes = 3 * (E * H * D // 2 + E * H * (D // gs) * 2) + rows_ * D * 2 * 2 + rows_ * H * 2 * 2 + T * D * 2

@@ -199,6 +199,20 @@ int mls_int4_grouped_gemm(const void* a, int a_dt, int64_t lda,
                           void* c, int c_dt, int64_t ldc,
                           int64_t N, int64_t K, mls_stream_t stream);
 
+/* mls_int4_grouped_gemm with the dispatch gather fused into the activation load
+ * (replaces gather_rows, kernels/moe_routing.py:89-97 + 144, in front of the per-expert
+ * loop): sorted row m of the product reads row a_rows[m] of a, a [a_src_rows][lda];
+ * a_rows int32 [M_total] on the device (the token of each sorted slot, sort_by_expert's
+ * token_of_slot). A row index outside [0, a_src_rows) reads zeros. */
+int mls_int4_grouped_gemm_rows(const void* a, int a_dt, int64_t lda,
+                               const int32_t* a_rows, int64_t a_src_rows,
+                               const int32_t* seg_off, int E, int64_t M_total,
+                               const uint8_t* w, int64_t w_estride, int64_t ldw,
+                               const void* s, int s_dt, int64_t s_estride,
+                               int64_t ld_sn, int64_t ld_sg, int group,
+                               void* c, int c_dt, int64_t ldc,
+                               int64_t N, int64_t K, mls_stream_t stream);
+
 /* ---------------------------------------------------------------- MoE expert MLP */
 
 /* The gate/up half of the quantized SwiGLU expert MLP (train/model.py:127-135,
@@ -217,6 +231,18 @@ int mls_int4_grouped_gate_up(const void* a, int a_dt, int64_t lda,
                              int64_t ld_sn, int64_t ld_sg, int group,
                              void* h, int h_dt, int64_t ldh,
                              int64_t H, int64_t K, mls_stream_t stream);
+
+/* mls_int4_grouped_gate_up with the dispatch gather fused into the activation load, as
+ * mls_int4_grouped_gemm_rows (gather_rows, kernels/moe_routing.py:89-97 + 144). */
+int mls_int4_grouped_gate_up_rows(const void* a, int a_dt, int64_t lda,
+                                  const int32_t* a_rows, int64_t a_src_rows,
+                                  const int32_t* seg_off, int E, int64_t M_total,
+                                  const uint8_t* wg, const uint8_t* wu,
+                                  int64_t w_estride, int64_t ldw,
+                                  const void* sg, const void* su, int s_dt,
+                                  int64_t s_estride, int64_t ld_sn, int64_t ld_sg, int group,
+                                  void* h, int h_dt, int64_t ldh,
+                                  int64_t H, int64_t K, mls_stream_t stream);
 
 /* Replaces _combine_rows_kernel + combine_rows (kernels/moe_routing.py:52-76, 100-113):
  * out[t][d] = sum_{s<k} w[t][s] * X(pos[t][s], d), fp32 accumulation, one rounding; one block

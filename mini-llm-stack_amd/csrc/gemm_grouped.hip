@@ -4,8 +4,8 @@
 // A block owns one expert's row chunk (up to BMX = 32 TMX rows of its segment; a
 // segment longer than BMX is split into chunks) and 128 weight rows n, and streams K
 // in 64-k stages. So each weight byte is read and widened once per row chunk (once per
-// expert when the segment fits in one chunk, as in config E: 115-136 rows per expert),
-// and only the 16-row subtiles that hold segment rows are multiplied.
+// expert when the segment fits in one chunk, as in config E: 115-136 rows per expert).
+// Rows of the chunk past the segment are zeros and are multiplied too (branch-free).
 //
 // 4 wavefronts as 2 (m) x 2 (n): wavefront (wm, wn) owns columns 64 wn .. 64 wn + 63
 // and the 16-row subtiles 2 t + wm (t < TMX) that the chunk covers. 256 threads and
@@ -22,9 +22,9 @@
 // INT4 widening, exact, 16 VALU per 8 weights: x = d ^ 0x88888888 turns each nibble
 // v into v ^ 8; masking the high nibbles (x & 0xF0F0F0F0) and the shifted low nibbles
 // ((x << 4) & 0xF0F0F0F0) leaves bytes whose signed value is 16 (v - 8); a sign-
-// extending SDWA convert per byte gives the exact float, and the 1/16 is folded into
-// the group scale (a power of two: exact). Group scales apply to fp32 partial sums at
-// every group boundary, as in the dense INT4 kernels.
+// extending SDWA convert per byte gives the exact float, and the 1/16 (a power of two:
+// exact) is applied once to the results. Group scales apply to fp32 partial sums at
+// every group boundary, as in the dense INT4 kernels, and are read only there.
 #include <type_traits>
 
 #include "mfma16.h"
@@ -62,6 +62,10 @@ __device__ __forceinline__ void widen_int4x16(const uint4& q, uint32_t* o) {
 // GU (gate/up of a SwiGLU expert MLP): the block's 128 weight rows are 64 rows of the
 // gate matrix (p.b, p.s) and the same 64 rows of the up matrix (p.b2, p.s2); the
 // epilogue writes h = silu(gate) * up for those 64 columns, from the fp32 accumulators.
+// offset of a gathered activation row that is not there: past any descriptor's range
+// (below 2^31 even with the stage's k offset added)
+constexpr int kPastEndA = 0x40000000;
+
 template <int R>
 struct Ring {
   static constexpr int v = R;
@@ -120,7 +124,6 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
   }
   const int m0 = __builtin_amdgcn_readfirstlane(lo + (chunk - cum) * BMX);
   const int rows = __builtin_amdgcn_readfirstlane(min(BMX, hi - m0));
-  const int nsub = (rows + 15) >> 4;  // active 16-row subtiles
   constexpr int ssz = SCL == 0 ? 4 : 2;
   const uint8_t* bmat = p.b + (int64_t)e * p.b_estride + kbase / 2;
   const uint8_t* smat = (const uint8_t*)p.s + ((int64_t)e * p.s_estride + (int64_t)(kbase / p.group) * p.ld_sg) * ssz;
@@ -138,9 +141,13 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
       GU ? (const uint8_t*)p.s2 + ((int64_t)e * p.s_estride + (int64_t)(kbase / p.group) * p.ld_sg) * ssz : smat;
 
   const int rows_b = __builtin_amdgcn_readfirstlane(min(OUTN, N - n0));
+  // activations: the chunk's rows m0 .. m0 + rows - 1 of a, or with a_rows (the dispatch
+  // gather fused into the load) rows a_rows[m0 + r] of a; rows past the chunk, and source
+  // rows outside a, read zeros
+  const bool gather = p.a_rows != nullptr;
   const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)((const uint8_t*)p.a + ((int64_t)m0 * p.lda + kbase) * 2), (short)0,
-      (int)(rows * p.lda * 2 - kbase * 2), 0x00020000);
+      (void*)((const uint8_t*)p.a + ((gather ? 0 : (int64_t)m0 * p.lda) + kbase) * 2), (short)0,
+      (int)((gather ? p.a_src_rows : rows) * p.lda * 2 - kbase * 2), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(bmat + (int64_t)n0 * p.ldb), (short)0, (int)(rows_b * p.ldb - kbase / 2), 0x00020000);
   // activation slot t = (wave * PW + i) * 64 + lane: row t / 8, logical chunk (t % 8) ^ (row & 7)
@@ -148,7 +155,12 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
 #pragma unroll
   for (int i = 0; i < PW; ++i) {
     const int t = (wave * PW + i) * 64 + lane, row = t >> 3, lc = (t & 7) ^ (row & 7);
-    a_off[i] = row * (int)p.lda * 2 + lc * 16;
+    if (gather) {
+      const int src = row < rows ? p.a_rows[m0 + row] : -1;
+      a_off[i] = (src >= 0 && src < p.a_src_rows) ? src * (int)p.lda * 2 + lc * 16 : kPastEndA;
+    } else {
+      a_off[i] = row * (int)p.lda * 2 + lc * 16;
+    }
   }
   // weights: thread tid stages B row tid / 2 (GU: row (tid / 2) % 64 of its matrix),
   // 16-byte column tid % 2 (32 k) of the stage
@@ -198,8 +210,8 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
       const int kc = min(k0, Kp - BK);  // a stage past the end reuses the last scales
       using ST = std::conditional_t<SCL == 1, _Float16, float>;
       const ST* sp = reinterpret_cast<const ST*>(s_mat) + s_row;
-      s0 = (float)sp[(int64_t)(kc / p.group) * p.ld_sg] * 0.0625f;
-      s1 = (float)sp[(int64_t)((kc + 32) / p.group) * p.ld_sg] * 0.0625f;
+      s0 = (float)sp[(int64_t)(kc / p.group) * p.ld_sg];
+      s1 = (float)sp[(int64_t)((kc + 32) / p.group) * p.ld_sg];
     }
   };
   auto load_w = [&](int k0, uint4& w) __attribute__((always_inline)) {
@@ -264,8 +276,8 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
     store_b(Ring<r ^ 1>{}, wreg(Ring<(q + 1) % 3>{}), sreg0(Ring<(q + 1) % 3>{}), sreg1(Ring<(q + 1) % 3>{}));
     const uint4* as = abuf(rc);
     const uint4* bs = bbuf(rc);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    auto kstep = [&](auto ksc) __attribute__((always_inline)) {
+      constexpr int ks = decltype(ksc)::v;
       uint4 aop[TMX], bop[TN];
       const int ch = ks * 4 + lk;
 #pragma unroll
@@ -278,33 +290,37 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
         const int row = (2 * j + wm) * 16 + lr;
         aop[j] = as[row * 8 + (ch ^ swz(row))];
       }
-      float sc[TN][4];
-      if constexpr (STAB) {
-        const int g = (k0 + 32 * ks) / p.group;
-#pragma unroll
-        for (int i = 0; i < TN; ++i) {
-          const uint2 h2 = *reinterpret_cast<const uint2*>(sT + g * BN + wn * 64 + i * 16 + 4 * lk);
-          const _Float16* h = reinterpret_cast<const _Float16*>(&h2);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) sc[i][q] = (float)h[q] * 0.0625f;
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < TN; ++i) {
-          const float4 s4 = *reinterpret_cast<const float4*>(sS + (r * 2 + ks) * BN + wn * 64 + i * 16 + 4 * lk);
-          sc[i][0] = s4.x;
-          sc[i][1] = s4.y;
-          sc[i][2] = s4.z;
-          sc[i][3] = s4.w;
-        }
-      }
+      // Every subtile is multiplied, those past the segment on zero rows: a branch per
+      // subtile would cut the stage into basic blocks that the widening and the LDS
+      // traffic cannot be scheduled across (measured: config E 224 -> 210 us).
 #pragma unroll
       for (int j = 0; j < TMX; ++j) {
-        if (2 * j + wm >= nsub) continue;  // subtile past the segment: nothing to multiply
 #pragma unroll
         for (int i = 0; i < TN; ++i) accg[i][j] = Mfma16<MT>::mma(bop[i], aop[j], accg[i][j]);
       }
       if ((k0 + 32 * (ks + 1)) % p.group == 0) {  // group ends: acc += s[n] * partial
+        // the group's scales of this lane's 4 TN columns, read only here (the 1/16 of the
+        // widening is applied once, in the epilogue)
+        float sc[TN][4];
+        if constexpr (STAB) {
+          const int g = (k0 + 32 * ks) / p.group;
+#pragma unroll
+          for (int i = 0; i < TN; ++i) {
+            const uint2 h2 = *reinterpret_cast<const uint2*>(sT + g * BN + wn * 64 + i * 16 + 4 * lk);
+            const _Float16* h = reinterpret_cast<const _Float16*>(&h2);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sc[i][q] = (float)h[q];
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < TN; ++i) {
+            const float4 s4 = *reinterpret_cast<const float4*>(sS + (r * 2 + ks) * BN + wn * 64 + i * 16 + 4 * lk);
+            sc[i][0] = s4.x;
+            sc[i][1] = s4.y;
+            sc[i][2] = s4.z;
+            sc[i][3] = s4.w;
+          }
+        }
 #pragma unroll
         for (int i = 0; i < TN; ++i)
 #pragma unroll
@@ -314,7 +330,9 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
             accg[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
           }
       }
-    }
+    };
+    kstep(Ring<0>{});
+    kstep(Ring<1>{});
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt vmcnt(1) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
@@ -361,16 +379,19 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
     // products of the same (m, n) and write silu(gate) * up. Subtile q = 2 j + wm
     // (16 rows x 64 columns fp32, 4 KiB) goes to buffer q % 2 at 4 KiB (q / 2): the
     // TMX subtiles of one parity fill one TMX x 4 KiB buffer exactly.
+    // Inside a subtile, row lr's 16-byte column chunk 4 i + lk sits at chunk (4 i + lk) ^
+    // (lr & 7): rows are 256 bytes apart, so without the XOR the 8 rows of one access
+    // would share their banks.
     auto ubuf = [&](int q) __attribute__((always_inline)) -> float* {
       uint4* b = (q & 1) ? As1 : As0;
       return reinterpret_cast<float*>(b) + (q >> 1) * 1024;
     };
+    auto uoff = [&](int i) __attribute__((always_inline)) { return lr * 64 + (((4 * i + lk) ^ (lr & 7)) * 4); };
     if (wn == 1) {
 #pragma unroll
       for (int i = 0; i < TN; ++i)
 #pragma unroll
-        for (int j = 0; j < TMX; ++j)
-          *reinterpret_cast<f32x4*>(ubuf(2 * j + wm) + lr * 64 + i * 16 + 4 * lk) = acc[i][j];
+        for (int j = 0; j < TMX; ++j) *reinterpret_cast<f32x4*>(ubuf(2 * j + wm) + uoff(i)) = acc[i][j];
     }
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -383,12 +404,12 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
       for (int j = 0; j < TMX; ++j) {
         const int ml = (2 * j + wm) * 16 + lr;
         if (ml >= rows) continue;
-        const f32x4 u = *reinterpret_cast<const f32x4*>(ubuf(2 * j + wm) + lr * 64 + i * 16 + 4 * lk);
+        const f32x4 u = *reinterpret_cast<const f32x4*>(ubuf(2 * j + wm) + uoff(i));
         float v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float g = acc[i][j][r];
-          v[r] = g / (1.0f + __expf(-g)) * u[r];
+          const float g = acc[i][j][r] * 0.0625f;
+          v[r] = g / (1.0f + __expf(-g)) * (u[r] * 0.0625f);
         }
         OT* dst = c + (int64_t)(m0 + ml) * p.ldc + nb;
         if (nb + 3 < N && (p.ldc % 4) == 0) {
@@ -410,12 +431,15 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
       const int ml = (2 * j + wm) * 16 + lr;
       if (ml >= rows) continue;
       OT* dst = c + (int64_t)(m0 + ml) * p.ldc + nb;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] * 0.0625f;  // the widening's 16 (v - 8)
       if (nb + 3 < N && (p.ldc % 4) == 0) {
-        store4<OT>(dst, acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+        store4<OT>(dst, v[0], v[1], v[2], v[3]);
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (nb + r < N) dst[r] = from_f32<OT>(acc[i][j][r]);
+          if (nb + r < N) dst[r] = from_f32<OT>(v[r]);
       }
     }
   }
@@ -427,10 +451,9 @@ static int launch_grouped(Mfma16Params p, hipStream_t st) {
   p.n_tiles = (int)cdiv(p.N, OUTN);
   // upper bound on sum_e ceil(rows_e / BMX) without reading the device offsets
   p.m_tiles = (int)(cdiv(p.M, BMX) + p.E);
-  auto kern = grouped_int4_kernel<MT, OT, TMX, SCL, GU>;
   const int64_t blocks = (int64_t)p.n_tiles * p.m_tiles * (p.ksplit > 1 ? p.ksplit : 1);
   if (blocks > 0x7FFFFFFF) return MLS_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((grouped_int4_kernel<MT, OT, TMX, SCL, GU>), dim3((unsigned)blocks), dim3(256), 0, st, p);
   return check_launch(GU ? "grouped INT4 gate/up GEMM" : "grouped INT4 GEMM");
 }
 

@@ -700,6 +700,8 @@ int launch_gemm_wq_mfma(int wbits, const WqArgs& w) {
 
 int launch_grouped_int4(const GroupedArgs& g) {
   const WqArgs& w = g.base;
+  // gathered rows: offsets into a below the past-the-end offset of a missing row
+  if (g.a_rows && (g.a_src_rows < 1 || g.a_src_rows * w.lda * 2 >= (1ll << 30))) return MLS_ERR_UNSUPPORTED;
   if (w.a_dt != MLS_F16 && w.a_dt != MLS_BF16) return MLS_ERR_UNSUPPORTED;
   if (w.K % 64 != 0 || w.group % 32 != 0) return MLS_ERR_UNSUPPORTED;
   if (!aligned(w.a, 16) || w.lda % 8 != 0) return MLS_ERR_UNSUPPORTED;
@@ -712,10 +714,11 @@ int launch_grouped_int4(const GroupedArgs& g) {
   p.s = w.s; p.s_dt = w.s_dt; p.ld_sn = w.ld_sn; p.ld_sg = w.ld_sg; p.group = w.group;
   p.c = w.c; p.ldc = w.ldc; p.M = (int)w.M; p.N = (int)w.N; p.K = (int)w.K;
   p.seg_off = g.seg_off; p.E = g.E; p.b_estride = g.w_estride; p.s_estride = g.s_estride;
+  p.a_rows = g.a_rows; p.a_src_rows = (int)g.a_src_rows;
   // MLS_GROUPED_TILES = 1: the row-tile kernels below instead of one block per expert
   // row chunk (gemm_grouped.hip)
   static const bool tiles = env_int("MLS_GROUPED_TILES", 0) != 0;
-  if (!tiles) return launch_grouped_seg(p, w.stream, w.a_dt == MLS_BF16, false);
+  if (!tiles || g.a_rows) return launch_grouped_seg(p, w.stream, w.a_dt == MLS_BF16, false);
   // upper bound on sum_e ceil(rows_e / BM) without reading the device offsets
   p.m_tiles = (int)(cdiv(w.M, BM) + g.E);
   static const bool w8 = env_int("MLS_MFMA_WAVES", 8) == 8;
@@ -732,6 +735,8 @@ int launch_grouped_int4(const GroupedArgs& g) {
 
 int launch_grouped_gate_up(const GroupedArgs& g, const uint8_t* wu, const void* su) {
   const WqArgs& w = g.base;
+  // gathered rows: offsets into a below the past-the-end offset of a missing row
+  if (g.a_rows && (g.a_src_rows < 1 || g.a_src_rows * w.lda * 2 >= (1ll << 30))) return MLS_ERR_UNSUPPORTED;
   if (w.a_dt != MLS_F16 && w.a_dt != MLS_BF16) return MLS_ERR_UNSUPPORTED;
   if (w.K % 64 != 0 || w.group % 32 != 0) return MLS_ERR_UNSUPPORTED;
   if (!aligned(w.a, 16) || w.lda % 8 != 0) return MLS_ERR_UNSUPPORTED;
@@ -743,6 +748,7 @@ int launch_grouped_gate_up(const GroupedArgs& g, const uint8_t* wu, const void* 
   p.s = w.s; p.s2 = su; p.s_dt = w.s_dt; p.ld_sn = w.ld_sn; p.ld_sg = w.ld_sg; p.group = w.group;
   p.c = w.c; p.ldc = w.ldc; p.M = (int)w.M; p.N = (int)w.N; p.K = (int)w.K;
   p.seg_off = g.seg_off; p.E = g.E; p.b_estride = g.w_estride; p.s_estride = g.s_estride;
+  p.a_rows = g.a_rows; p.a_src_rows = (int)g.a_src_rows;
   return launch_grouped_seg(p, w.stream, w.a_dt == MLS_BF16, true);
 }
 
@@ -757,6 +763,7 @@ int launch_grouped_int4_partial(const GroupedArgs& g, int splits, float* partial
   p.s = w.s; p.s_dt = w.s_dt; p.ld_sn = w.ld_sn; p.ld_sg = w.ld_sg; p.group = w.group;
   p.c = partial; p.ldc = ldp; p.M = (int)w.M; p.N = (int)w.N; p.K = (int)w.K;
   p.seg_off = g.seg_off; p.E = g.E; p.b_estride = g.w_estride; p.s_estride = g.s_estride;
+  p.a_rows = g.a_rows; p.a_src_rows = (int)g.a_src_rows;
   p.ksplit = splits; p.c_sstride = sstride;
   return launch_grouped_partial(p, w.stream, w.a_dt == MLS_BF16);
 }

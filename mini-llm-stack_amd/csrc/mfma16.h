@@ -34,6 +34,8 @@ struct Mfma16Params {
   const void* s2;
   int ksplit;                     // grouped: K split into this many partial products (0, 1: none)
   int64_t c_sstride;              // grouped split: elements between the partial outputs
+  const int32_t* a_rows;          // grouped: sorted row m is row a_rows[m] of a (null: row m)
+  int a_src_rows;                 // grouped: rows of a when a_rows is set
 };
 
 template <typename T> struct Mfma16;

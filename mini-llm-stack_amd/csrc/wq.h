@@ -47,6 +47,8 @@ struct GroupedArgs {
   int E;
   int64_t w_estride;      // bytes between experts' packed weights
   int64_t s_estride;      // elements between experts' scales
+  const int32_t* a_rows = nullptr;  // device [M_total]: sorted row m is row a_rows[m] of a
+  int64_t a_src_rows = 0;           // rows of a when a_rows is set
 };
 int launch_grouped_int4(const GroupedArgs& p);
 // The gate/up pair of a SwiGLU expert MLP over expert-sorted segments: base.w / base.s

@@ -90,20 +90,22 @@ extern "C" int mls_int4_gemm(const void* a, int a_dt, int64_t lda, const uint8_t
   return run("mls_int4_gemm", 4, p);
 }
 
-extern "C" int mls_int4_grouped_gemm(const void* a, int a_dt, int64_t lda, const int32_t* seg_off,
-                                     int E, int64_t M_total, const uint8_t* w, int64_t w_estride,
-                                     int64_t ldw, const void* s, int s_dt, int64_t s_estride,
-                                     int64_t ld_sn, int64_t ld_sg, int group, void* c, int c_dt,
-                                     int64_t ldc, int64_t N, int64_t K, mls_stream_t stream) {
-  const char* fn = "mls_int4_grouped_gemm";
+namespace {
+
+int grouped_gemm(const char* fn, const void* a, int a_dt, int64_t lda, const int32_t* a_rows,
+                 int64_t a_src_rows, const int32_t* seg_off, int E, int64_t M_total, const uint8_t* w,
+                 int64_t w_estride, int64_t ldw, const void* s, int s_dt, int64_t s_estride, int64_t ld_sn,
+                 int64_t ld_sg, int group, void* c, int c_dt, int64_t ldc, int64_t N, int64_t K,
+                 mls_stream_t stream) {
   GroupedArgs g{{a, a_dt, lda, w, ldw, s, s_dt, ld_sn, ld_sg, group, c, ldc, M_total, N, K,
                  (hipStream_t)stream},
-                seg_off, E, w_estride, s_estride};
+                seg_off, E, w_estride, s_estride, a_rows, a_src_rows};
   int rc = validate(fn, 4, g.base, c_dt);
   if (rc != MLS_OK) return rc;
   if (E < 1) return fail(MLS_ERR_ARG, "%s: E=%d < 1", fn, E);
   if (K < 1) return fail(MLS_ERR_ARG, "%s: K=%lld must be positive", fn, (long long)K);
   if (w_estride < 0 || s_estride < 0) return fail(MLS_ERR_ARG, "%s: negative expert stride", fn);
+  if (a_rows && a_src_rows < 1) return fail(MLS_ERR_ARG, "%s: a_src_rows=%lld < 1", fn, (long long)a_src_rows);
   if (M_total == 0 || N == 0) return MLS_OK;
   if (!seg_off) return fail(MLS_ERR_ARG, "%s: null seg_off", fn);
   if (a_dt != MLS_F16 && a_dt != MLS_BF16)
@@ -111,8 +113,58 @@ extern "C" int mls_int4_grouped_gemm(const void* a, int a_dt, int64_t lda, const
   rc = launch_grouped_int4(g);
   if (rc == MLS_ERR_UNSUPPORTED)
     return fail(MLS_ERR_UNSUPPORTED,
-                "%s: needs K %% 64 == 0, group %% 32 == 0 and 16-byte aligned rows", fn);
+                "%s: needs K %% 64 == 0, group %% 32 == 0, 16-byte aligned rows (and a gathered a under 1 GiB)",
+                fn);
   return rc;
+}
+
+int grouped_gate_up(const char* fn, const void* a, int a_dt, int64_t lda, const int32_t* a_rows,
+                    int64_t a_src_rows, const int32_t* seg_off, int E, int64_t M_total, const uint8_t* wg,
+                    const uint8_t* wu, int64_t w_estride, int64_t ldw, const void* sg, const void* su, int s_dt,
+                    int64_t s_estride, int64_t ld_sn, int64_t ld_sg, int group, void* h, int h_dt, int64_t ldh,
+                    int64_t H, int64_t K, mls_stream_t stream) {
+  GroupedArgs g{{a, a_dt, lda, wg, ldw, sg, s_dt, ld_sn, ld_sg, group, h, ldh, M_total, H, K,
+                 (hipStream_t)stream},
+                seg_off, E, w_estride, s_estride, a_rows, a_src_rows};
+  int rc = validate(fn, 4, g.base, h_dt);
+  if (rc != MLS_OK) return rc;
+  if (E < 1) return fail(MLS_ERR_ARG, "%s: E=%d < 1", fn, E);
+  if (K < 1) return fail(MLS_ERR_ARG, "%s: K=%lld must be positive", fn, (long long)K);
+  if (w_estride < 0 || s_estride < 0) return fail(MLS_ERR_ARG, "%s: negative expert stride", fn);
+  if (a_rows && a_src_rows < 1) return fail(MLS_ERR_ARG, "%s: a_src_rows=%lld < 1", fn, (long long)a_src_rows);
+  if (M_total == 0 || H == 0) return MLS_OK;
+  if (!seg_off || !wu || !su) return fail(MLS_ERR_ARG, "%s: null pointer", fn);
+  if (a_dt != MLS_F16 && a_dt != MLS_BF16)
+    return fail(MLS_ERR_UNSUPPORTED, "%s: activations must be f16 or bf16", fn);
+  rc = launch_grouped_gate_up(g, wu, su);
+  if (rc == MLS_ERR_UNSUPPORTED)
+    return fail(MLS_ERR_UNSUPPORTED,
+                "%s: needs K %% 64 == 0, group %% 32 == 0, 16-byte aligned rows (and a gathered a under 1 GiB)",
+                fn);
+  return rc;
+}
+
+}  // namespace
+
+extern "C" int mls_int4_grouped_gemm(const void* a, int a_dt, int64_t lda, const int32_t* seg_off,
+                                     int E, int64_t M_total, const uint8_t* w, int64_t w_estride,
+                                     int64_t ldw, const void* s, int s_dt, int64_t s_estride,
+                                     int64_t ld_sn, int64_t ld_sg, int group, void* c, int c_dt,
+                                     int64_t ldc, int64_t N, int64_t K, mls_stream_t stream) {
+  return grouped_gemm("mls_int4_grouped_gemm", a, a_dt, lda, nullptr, 0, seg_off, E, M_total, w, w_estride, ldw,
+                      s, s_dt, s_estride, ld_sn, ld_sg, group, c, c_dt, ldc, N, K, stream);
+}
+
+extern "C" int mls_int4_grouped_gemm_rows(const void* a, int a_dt, int64_t lda, const int32_t* a_rows,
+                                          int64_t a_src_rows, const int32_t* seg_off, int E, int64_t M_total,
+                                          const uint8_t* w, int64_t w_estride, int64_t ldw, const void* s,
+                                          int s_dt, int64_t s_estride, int64_t ld_sn, int64_t ld_sg, int group,
+                                          void* c, int c_dt, int64_t ldc, int64_t N, int64_t K,
+                                          mls_stream_t stream) {
+  const char* fn = "mls_int4_grouped_gemm_rows";
+  if (!a_rows) return fail(MLS_ERR_ARG, "%s: null a_rows", fn);
+  return grouped_gemm(fn, a, a_dt, lda, a_rows, a_src_rows, seg_off, E, M_total, w, w_estride, ldw, s, s_dt,
+                      s_estride, ld_sn, ld_sg, group, c, c_dt, ldc, N, K, stream);
 }
 
 extern "C" int mls_int4_grouped_gate_up(const void* a, int a_dt, int64_t lda, const int32_t* seg_off,
@@ -121,24 +173,20 @@ extern "C" int mls_int4_grouped_gate_up(const void* a, int a_dt, int64_t lda, co
                                         int s_dt, int64_t s_estride, int64_t ld_sn, int64_t ld_sg,
                                         int group, void* h, int h_dt, int64_t ldh, int64_t H, int64_t K,
                                         mls_stream_t stream) {
-  const char* fn = "mls_int4_grouped_gate_up";
-  GroupedArgs g{{a, a_dt, lda, wg, ldw, sg, s_dt, ld_sn, ld_sg, group, h, ldh, M_total, H, K,
-                 (hipStream_t)stream},
-                seg_off, E, w_estride, s_estride};
-  int rc = validate(fn, 4, g.base, h_dt);
-  if (rc != MLS_OK) return rc;
-  if (E < 1) return fail(MLS_ERR_ARG, "%s: E=%d < 1", fn, E);
-  if (K < 1) return fail(MLS_ERR_ARG, "%s: K=%lld must be positive", fn, (long long)K);
-  if (w_estride < 0 || s_estride < 0) return fail(MLS_ERR_ARG, "%s: negative expert stride", fn);
-  if (M_total == 0 || H == 0) return MLS_OK;
-  if (!seg_off || !wu || !su) return fail(MLS_ERR_ARG, "%s: null pointer", fn);
-  if (a_dt != MLS_F16 && a_dt != MLS_BF16)
-    return fail(MLS_ERR_UNSUPPORTED, "%s: activations must be f16 or bf16", fn);
-  rc = launch_grouped_gate_up(g, wu, su);
-  if (rc == MLS_ERR_UNSUPPORTED)
-    return fail(MLS_ERR_UNSUPPORTED,
-                "%s: needs K %% 64 == 0, group %% 32 == 0 and 16-byte aligned rows", fn);
-  return rc;
+  return grouped_gate_up("mls_int4_grouped_gate_up", a, a_dt, lda, nullptr, 0, seg_off, E, M_total, wg, wu,
+                         w_estride, ldw, sg, su, s_dt, s_estride, ld_sn, ld_sg, group, h, h_dt, ldh, H, K, stream);
+}
+
+extern "C" int mls_int4_grouped_gate_up_rows(const void* a, int a_dt, int64_t lda, const int32_t* a_rows,
+                                             int64_t a_src_rows, const int32_t* seg_off, int E, int64_t M_total,
+                                             const uint8_t* wg, const uint8_t* wu, int64_t w_estride,
+                                             int64_t ldw, const void* sg, const void* su, int s_dt,
+                                             int64_t s_estride, int64_t ld_sn, int64_t ld_sg, int group, void* h,
+                                             int h_dt, int64_t ldh, int64_t H, int64_t K, mls_stream_t stream) {
+  const char* fn = "mls_int4_grouped_gate_up_rows";
+  if (!a_rows) return fail(MLS_ERR_ARG, "%s: null a_rows", fn);
+  return grouped_gate_up(fn, a, a_dt, lda, a_rows, a_src_rows, seg_off, E, M_total, wg, wu, w_estride, ldw, sg,
+                         su, s_dt, s_estride, ld_sn, ld_sg, group, h, h_dt, ldh, H, K, stream);
 }
 
 extern "C" int mls_int4_grouped_splits(int64_t M_total, int E, int64_t N, int64_t K, int group) {

@@ -77,6 +77,10 @@ SIGNATURES = {
                                _I64, _I64, _I, _P, _I, _I64, _I64, _I64, _P], _I),
     "mls_int4_grouped_gate_up": ([_P, _I, _I64, _P, _I, _I64, _P, _P, _I64, _I64, _P, _P, _I,
                                   _I64, _I64, _I64, _I, _P, _I, _I64, _I64, _I64, _P], _I),
+    "mls_int4_grouped_gemm_rows": ([_P, _I, _I64, _P, _I64, _P, _I, _I64, _P, _I64, _I64, _P, _I, _I64,
+                                    _I64, _I64, _I, _P, _I, _I64, _I64, _I64, _P], _I),
+    "mls_int4_grouped_gate_up_rows": ([_P, _I, _I64, _P, _I64, _P, _I, _I64, _P, _P, _I64, _I64, _P, _P, _I,
+                                       _I64, _I64, _I64, _I, _P, _I, _I64, _I64, _I64, _P], _I),
     "mls_moe_combine": ([_P, _I, _I64, _I64, _I, _I64, _P, _I, _P, _I64, _I, _P, _I, _I64, _I64, _P], _I),
     "mls_int4_grouped_splits": ([_I64, _I, _I64, _I64, _I], _I),
     "mls_int4_grouped_gemm_partial": ([_P, _I, _I64, _P, _I, _I64, _P, _I64, _I64, _P, _I, _I64, _I64, _I64,

@@ -32,17 +32,35 @@ def _offsets(counts_or_offsets: torch.Tensor, E: int, fn: str) -> torch.Tensor:
     raise ValueError(f"{fn}: expected {E} counts or {E + 1} offsets, got {counts_or_offsets.numel()}")
 
 
+def _row_index(a_rows: torch.Tensor | None, M: int, fn: str) -> torch.Tensor | None:
+    if a_rows is None:
+        return None
+    if a_rows.numel() != M:
+        raise ValueError(f"{fn}: a_rows has {a_rows.numel()} entries, expected one per sorted row ({M})")
+    return a_rows.reshape(-1).to(torch.int32).contiguous()
+
+
 def int4_grouped_matmul(a_sorted: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor,
-                        counts_or_offsets: torch.Tensor, group_size: int) -> torch.Tensor:
+                        counts_or_offsets: torch.Tensor, group_size: int,
+                        a_rows: torch.Tensor | None = None) -> torch.Tensor:
     """out[r] = a_sorted[r] @ dequant(w_packed[e], scale[e], group_size).T for every row r
     of expert e's segment. counts_or_offsets: per-expert counts [E] or offsets [E+1]
-    (int, on the device). a_sorted [M_total, K] bf16/fp16 -> out [M_total, N] same dtype."""
+    (int, on the device). a_sorted [M_total, K] bf16/fp16 -> out [M_total, N] same dtype.
+    With a_rows (int [M_total], the token of each sorted slot: sort_by_expert's
+    token_of_slot), a_sorted is the unsorted token matrix and sorted row r is its row
+    a_rows[r]: the dispatch gather (gather_rows, kernels/moe_routing.py:144) happens inside
+    the activation load."""
     dev = require_hip("int4_grouped_matmul", a_sorted, w_packed, scale, counts_or_offsets)
     if w_packed.dim() != 3 or w_packed.dtype != torch.uint8:
         raise ValueError(f"int4_grouped_matmul: w_packed must be uint8 [E, N, K/2], got "
                          f"{w_packed.dtype} {tuple(w_packed.shape)}")
     E, N, Kh = w_packed.shape
     M, K = a_sorted.shape
+    idx = None
+    if a_rows is not None:
+        require_hip("int4_grouped_matmul", a_rows)
+        idx = _row_index(a_rows, a_rows.numel(), "int4_grouped_matmul")
+        M = idx.numel()
     assert K % group_size == 0 and K == Kh * 2
     G = K // group_size
     if tuple(scale.shape) != (E, N, G):
@@ -56,20 +74,28 @@ def int4_grouped_matmul(a_sorted: torch.Tensor, w_packed: torch.Tensor, scale: t
     s = scale if scale.is_contiguous() else scale.contiguous()
     sdt = dt_code(s.dtype, "int4_grouped_matmul scale")
     c = torch.empty(M, N, dtype=a.dtype, device=dev)
-    kernels.check(kernels.lib().mls_int4_grouped_gemm(
-        a.data_ptr(), adt, ld(a), off.data_ptr(), E, M,
-        w.data_ptr(), N * Kh, Kh, s.data_ptr(), sdt, N * G, G, 1, group_size,
-        c.data_ptr(), adt, ld(c), N, K, stream(dev)), "int4_grouped_matmul")
+    if idx is None:
+        kernels.check(kernels.lib().mls_int4_grouped_gemm(
+            a.data_ptr(), adt, ld(a), off.data_ptr(), E, M,
+            w.data_ptr(), N * Kh, Kh, s.data_ptr(), sdt, N * G, G, 1, group_size,
+            c.data_ptr(), adt, ld(c), N, K, stream(dev)), "int4_grouped_matmul")
+    else:
+        kernels.check(kernels.lib().mls_int4_grouped_gemm_rows(
+            a.data_ptr(), adt, ld(a), idx.data_ptr(), a.shape[0], off.data_ptr(), E, M,
+            w.data_ptr(), N * Kh, Kh, s.data_ptr(), sdt, N * G, G, 1, group_size,
+            c.data_ptr(), adt, ld(c), N, K, stream(dev)), "int4_grouped_matmul")
     return c
 
 
 def int4_grouped_gate_up(a_sorted: torch.Tensor, wg_packed: torch.Tensor, sg: torch.Tensor,
                          wu_packed: torch.Tensor, su: torch.Tensor,
-                         counts_or_offsets: torch.Tensor, group_size: int) -> torch.Tensor:
+                         counts_or_offsets: torch.Tensor, group_size: int,
+                         a_rows: torch.Tensor | None = None) -> torch.Tensor:
     """h[r] = silu(a_sorted[r] @ dequant(wg[e]).T) * (a_sorted[r] @ dequant(wu[e]).T) for
     every row r of expert e's segment: the first half of a SwiGLU expert MLP
     (train/model.py:127-135) with INT4 gate/up weights, one launch for all experts.
-    wg/wu packed [E, H, K/2], sg/su [E, H, K/group] (same dtype) -> h [M_total, H]."""
+    wg/wu packed [E, H, K/2], sg/su [E, H, K/group] (same dtype) -> h [M_total, H].
+    a_rows: as for int4_grouped_matmul (the dispatch gather fused into the load)."""
     dev = require_hip("int4_grouped_gate_up", a_sorted, wg_packed, sg, wu_packed, su, counts_or_offsets)
     for w in (wg_packed, wu_packed):
         if w.dim() != 3 or w.dtype != torch.uint8:
@@ -79,6 +105,11 @@ def int4_grouped_gate_up(a_sorted: torch.Tensor, wg_packed: torch.Tensor, sg: to
         raise ValueError("int4_grouped_gate_up: gate and up weights/scales must have equal shapes and dtypes")
     E, H, Kh = wg_packed.shape
     M, K = a_sorted.shape
+    idx = None
+    if a_rows is not None:
+        require_hip("int4_grouped_gate_up", a_rows)
+        idx = _row_index(a_rows, a_rows.numel(), "int4_grouped_gate_up")
+        M = idx.numel()
     assert K % group_size == 0 and K == Kh * 2
     G = K // group_size
     if tuple(sg.shape) != (E, H, G):
@@ -94,10 +125,16 @@ def int4_grouped_gate_up(a_sorted: torch.Tensor, wg_packed: torch.Tensor, sg: to
     su = su if su.is_contiguous() else su.contiguous()
     sdt = dt_code(sg.dtype, "int4_grouped_gate_up scale")
     h = torch.empty(M, H, dtype=a.dtype, device=dev)
-    kernels.check(kernels.lib().mls_int4_grouped_gate_up(
-        a.data_ptr(), adt, ld(a), off.data_ptr(), E, M, wg.data_ptr(), wu.data_ptr(), H * Kh, Kh,
-        sg.data_ptr(), su.data_ptr(), sdt, H * G, G, 1, group_size,
-        h.data_ptr(), adt, ld(h), H, K, stream(dev)), "int4_grouped_gate_up")
+    if idx is None:
+        kernels.check(kernels.lib().mls_int4_grouped_gate_up(
+            a.data_ptr(), adt, ld(a), off.data_ptr(), E, M, wg.data_ptr(), wu.data_ptr(), H * Kh, Kh,
+            sg.data_ptr(), su.data_ptr(), sdt, H * G, G, 1, group_size,
+            h.data_ptr(), adt, ld(h), H, K, stream(dev)), "int4_grouped_gate_up")
+    else:
+        kernels.check(kernels.lib().mls_int4_grouped_gate_up_rows(
+            a.data_ptr(), adt, ld(a), idx.data_ptr(), a.shape[0], off.data_ptr(), E, M, wg.data_ptr(),
+            wu.data_ptr(), H * Kh, Kh, sg.data_ptr(), su.data_ptr(), sdt, H * G, G, 1, group_size,
+            h.data_ptr(), adt, ld(h), H, K, stream(dev)), "int4_grouped_gate_up")
     return h
 
 
@@ -146,16 +183,19 @@ def int4_grouped_matmul_partial(a_sorted: torch.Tensor, w_packed: torch.Tensor, 
 def int4_expert_mlp_combine(a_sorted: torch.Tensor, counts_or_offsets: torch.Tensor,
                             wg: torch.Tensor, sg: torch.Tensor, wu: torch.Tensor, su: torch.Tensor,
                             wd: torch.Tensor, sd: torch.Tensor, group_size: int,
-                            weights: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-    """The routed MoE layer after dispatch: the INT4 SwiGLU expert MLP of every segment
+                            weights: torch.Tensor, pos: torch.Tensor,
+                            a_rows: torch.Tensor | None = None) -> torch.Tensor:
+    """The routed MoE layer after routing: the INT4 SwiGLU expert MLP of every segment
     (int4_expert_mlp) and the router-weighted combine back to token order
-    (kernels/moe_routing.py:145-153). When the down projection's output is narrow (few
+    (kernels/moe_routing.py:144-153). With a_rows (sort_by_expert's token_of_slot),
+    a_sorted is the unsorted token matrix [T, D] and the dispatch gather happens inside the
+    gate/up kernel's activation load. When the down projection's output is narrow (few
     column tiles), it runs as fp32 partial products over K splits that the combine adds,
     so that it still fills the GPU. Returns [T, D] in a_sorted's dtype."""
     from kernels.moe_routing import combine_partials, combine_rows
     E = wg.shape[0]
     off = _offsets(counts_or_offsets, E, "int4_expert_mlp_combine")
-    h = int4_grouped_gate_up(a_sorted, wg, sg, wu, su, off, group_size)
+    h = int4_grouped_gate_up(a_sorted, wg, sg, wu, su, off, group_size, a_rows=a_rows)
     D, H = wd.shape[1], wd.shape[2] * 2
     splits = grouped_splits(h.shape[0], E, D, H, group_size)
     if splits > 1:

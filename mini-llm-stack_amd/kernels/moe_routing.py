@@ -95,12 +95,13 @@ def moe_dispatch_combine(flat: torch.Tensor, weights: torch.Tensor, experts_idx:
 
     n_experts = len(expert_modules)
     token_of_slot, counts, pos = sort_by_expert(experts_idx, n_experts)
-    dispatched = gather_rows(flat, token_of_slot)
     st = stacked_int4_experts(expert_modules)
-    if st is not None and dispatched.dtype in (torch.bfloat16, torch.float16):
-        return int4_expert_mlp_combine(dispatched, segment_offsets(counts), st["w_gate"][0], st["w_gate"][1],
+    if st is not None and flat.dtype in (torch.bfloat16, torch.float16):
+        # the gather runs inside the gate/up kernel's activation load (a_rows)
+        return int4_expert_mlp_combine(flat, segment_offsets(counts), st["w_gate"][0], st["w_gate"][1],
                                        st["w_up"][0], st["w_up"][1], st["w_down"][0], st["w_down"][1],
-                                       st["group_size"], weights, pos)
+                                       st["group_size"], weights, pos, a_rows=token_of_slot)
+    dispatched = gather_rows(flat, token_of_slot)
     expert_out = torch.empty_like(dispatched)
     start = 0
     for e, cnt in enumerate(counts.tolist()):

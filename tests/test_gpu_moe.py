@@ -63,6 +63,30 @@ def test_grouped_group_sizes(dev, gs, dtype):
     assert ok, f"worst {worst:.3g}"
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_grouped_fused_gather(dev, dtype):
+    """a_rows: the dispatch gather inside the activation load gives the same bits as the
+    grouped GEMM on gather_rows' output (same rows, same arithmetic); repeated and unsorted
+    token indices; an index outside the token matrix reads a zero row."""
+    T, E, k, K, N, gs = 90, 5, 2, 384, 256, 64
+    P, S = _experts(dev, E, N, K, gs, 21)
+    x = torch.randn(T, K, device=dev).to(dtype)
+    g = torch.Generator(device=dev).manual_seed(3)
+    ex = torch.randint(0, E, (T, k), generator=g, device=dev)
+    tok, counts, _ = sort_by_expert(ex, E)
+    want = int4_grouped_matmul(gather_rows(x, tok), P, S, counts, gs)
+    got = int4_grouped_matmul(x, P, S, counts, gs, a_rows=tok)
+    assert torch.equal(got, want)
+    bad = tok.clone()
+    bad[3] = T + 5
+    bad[7] = -1
+    got = int4_grouped_matmul(x, P, S, counts, gs, a_rows=bad)
+    assert torch.equal(got[3], torch.zeros_like(got[3])) and torch.equal(got[7], torch.zeros_like(got[7]))
+    keep = torch.ones(T * k, dtype=torch.bool, device=dev)
+    keep[3] = keep[7] = False
+    assert torch.equal(got[keep], want[keep])
+
+
 def test_config_e(dev):
     """512 tokens, hidden 4096, 8 experts with W_up [14336, 4096]
     INT4 g128, top-2 softmax routing from logits ~ N(0, 1), expert-sorted segments."""

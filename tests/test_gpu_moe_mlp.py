@@ -167,6 +167,23 @@ def _quantize_experts(experts, gs):
     return experts
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_gate_up_fused_gather(dev, dt):
+    """The gate/up kernel with the dispatch gather in its activation load equals it on
+    gather_rows' output, bit for bit."""
+    from kernels.moe_routing import gather_rows
+    T, E, k, D, H, gs = 150, 4, 2, 256, 192, 64
+    Pg, Sg = _int4(dev, E, H, D, gs, 31, torch.float16)
+    Pu, Su = _int4(dev, E, H, D, gs, 32, torch.float16)
+    x = torch.randn(T, D, device=dev).to(dt)
+    g = torch.Generator(device=dev).manual_seed(5)
+    ex = torch.randint(0, E, (T, k), generator=g, device=dev)
+    tok, counts, _ = sort_by_expert(ex, E)
+    want = int4_grouped_gate_up(gather_rows(x, tok), Pg, Sg, Pu, Su, counts, gs)
+    got = int4_grouped_gate_up(x, Pg, Sg, Pu, Su, counts, gs, a_rows=tok)
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("T,E,k,D,H,gs,dt", [
     (300, 8, 2, 256, 512, 32, torch.bfloat16),
     (77, 4, 1, 128, 256, 128, torch.float16),
