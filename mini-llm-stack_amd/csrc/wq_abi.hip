@@ -30,7 +30,9 @@ int validate(const char* fn, int wbits, const WqArgs& p, int c_dt) {
   if (p.lda < p.K || p.ldw < wcols || p.ldc < p.N)
     return fail(MLS_ERR_ARG, "%s: bad leading dimension (lda=%lld ldw=%lld ldc=%lld)", fn,
                 (long long)p.lda, (long long)p.ldw, (long long)p.ldc);
-  if (p.M * p.N / 256 > 0x7FFFFFFF) return fail(MLS_ERR_UNSUPPORTED, "%s: M*N too large", fn);
+  // M * N / 256 must fit 31 bits; compared by division (M, N > 0 here), as the product of
+  // two valid int64 sizes can overflow
+  if (p.M > (int64_t)0x7FFFFFFF * 256 / p.N) return fail(MLS_ERR_UNSUPPORTED, "%s: M*N too large", fn);
   return MLS_OK;
 }
 
