@@ -24,6 +24,8 @@
 // is permuted to the same order with v_perm; INT8 and x stay in natural order.
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "wq.h"
 
 namespace mls {
@@ -65,6 +67,19 @@ template <typename ST> __device__ __forceinline__ float ld_scale(const ST* s, in
   return (float)s[i];
 }
 
+// s_waitcnt vmcnt(N) (gfx9 encoding: low 4 bits, high 2 bits at 14; lgkm and exp counts
+// left at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// 16-byte LDS-direct load: lane l writes LDS bytes [16 l, 16 l + 16) above `lds`
+__device__ __forceinline__ void lds_load16x(__amdgpu_buffer_rsrc_t rs, void* lds, int voff, int soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+
 // INT4: the 8 nibbles of dword d (k = 0..7, even k low) -> MFMA operand in k order
 // 0,4,1,5,2,6,3,7, each value the exact MAGIC + v.
 template <typename AT>
@@ -89,7 +104,26 @@ __device__ __forceinline__ uint4 byte_operand(uint32_t d0, uint32_t d1) {
                     Mx<AT>::pack_int((float)((v >> 16) & 0xFFu), (float)(v >> 24)));
 }
 
-template <int WBITS, typename AT, typename ST, int R, int WAVES, int U>
+// INT4 group scales of a wavefront's steps through LDS (SL): the wavefront's slice of the
+// block's scale table, SLG groups from its first step's group g0 by 16 R rows, stored
+// [group][row], one dword per scale (fp16 in the low half), so that a lane's 4
+// consecutive rows are one 16-byte LDS read. It is filled by LDS-direct loads of one
+// scale per lane (SLG * 16 R / 64 instructions),
+// issued before any weight or activation load; the wavefront reads only its own slice,
+// so its own vmcnt wait (which the compiler places before the first LDS read) is the
+// only synchronisation. Without SL, every step loads each lane's 4 scales from global.
+constexpr int SLG = 16;
+
+// x through LDS (XL): with all of a wavefront's steps in one chunk, the wavefront first
+// brings its K range of the M rows of x into its own LDS slice, [step][16 rows][KB k], by
+// LDS-direct loads of whole 16-byte chunks (a row's step is 256 (INT4) or 128 (INT8)
+// contiguous bytes, RPI rows per instruction), issued only for row groups below M. The
+// MFMA operand reads then come from LDS: loaded straight into registers, every 16-byte
+// x piece touched all of a row's cache lines at a quarter of their width, and the L1 and
+// address units (not HBM) bounded the kernel. The 16-byte chunk index of row r is XOR-ed
+// with r & (CH - 1) (conflict-free 16-row reads). Rows of the slice at or past M hold
+// zeros or stale data; they feed only output columns m >= M, which are never stored.
+template <int WBITS, typename AT, typename ST, int R, int WAVES, int U, bool SL, bool XL>
 // One wavefront per SIMD is the design point (a grid of N / 16 blocks of WAVES
 // wavefronts), so the compiler may spend registers on keeping a chunk's loads in flight.
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemv_mfma_kernel(
@@ -99,6 +133,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
   constexpr int KB = WBITS == 4 ? 128 : 64;  // k per step
   constexpr int NMF = WBITS == 4 ? 4 : 2;    // MFMAs per step and 16-row tile
   __shared__ f32x4 red[WAVES][R][64];
+  // one dword per scale: an LDS-direct load of 2 bytes still advances 4 bytes per lane
+  __shared__ __align__(16) uint32_t sls[SL ? WAVES : 1][SL ? SLG * 16 * R : 1];
+  constexpr int XRB = KB * 2, CH = XRB / 16, RPI = 64 / CH;  // x bytes / 16-byte chunks per row-step
+  static_assert(!XL || WAVES * U * 16 * XRB <= 128 * 1024, "x slices fit LDS");
+  __shared__ __align__(16) uint8_t xls[XL ? WAVES : 1][XL ? U * 16 * XRB : 16];
 
   const int lane = threadIdx.x & 63;
   // wave-uniform by construction; readfirstlane lets the compiler keep the step
@@ -111,6 +150,28 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
   const int s_lo = (int)((int64_t)nsteps * wave / WAVES);
   const int s_hi = (int)((int64_t)nsteps * (wave + 1) / WAVES);
 
+  // INT4 with SL: this wavefront's scale slice, before its other loads. Element e of the
+  // slice is group g0 + e / (16 R) of block row e % (16 R); rows past N read zeros.
+  const int spg = WBITS == 4 ? group / KB : 1;  // steps per group (INT4: a multiple of KB here)
+  const float inv_spg = 1.0f / (float)spg;
+  // group of step st: (st + 0.5) / spg is never within 0.5 / spg of an integer, far above
+  // the fp32 rounding error at these sizes, so the truncation is exact
+  auto group_of = [&](int st) __attribute__((always_inline)) { return (int)(((float)st + 0.5f) * inv_spg); };
+  const int g0 = group_of(s_lo);
+  if constexpr (WBITS == 4 && SL) {
+    const __amdgpu_buffer_rsrc_t rss = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(s + (int64_t)n_base * ld_sn), (short)0, (int)(rows_w * ld_sn * (int64_t)sizeof(ST)), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < SLG * 16 * R / 64; ++i) {
+      const int e = 64 * i + lane, row = e % (16 * R), gl = e / (16 * R);
+      const int off = (int)((row * ld_sn + (int64_t)(g0 + gl) * ld_sg) * (int64_t)sizeof(ST));
+      auto* dst = (__attribute__((address_space(3))) void*)(&sls[wave][64 * i]);  // 4 bytes per lane
+      if constexpr (sizeof(ST) == 2)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rss, dst, 2, off, 0, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rss, dst, 4, off, 0, 0, 0);
+    }
+  }
   // rows of x past M and weight rows past N read as zeros
   const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
       (void*)a, (short)0, (int)(M * lda * (int64_t)sizeof(AT)), 0x00020000);
@@ -135,6 +196,20 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
   for (int t = 0; t < R; ++t) acc[t] = zero;
   f32x4 xsum = zero;  // INT8: sum_k x over this wave's steps
 
+  if constexpr (XL) {
+    // the wavefront's x slice (one chunk: s_hi - s_lo <= U); steps past the range load
+    // zeros (an offset past the buffer)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int soff = s_lo + u < s_hi ? (s_lo + u) * XRB : 0x7FFFFFF0;
+#pragma unroll
+      for (int rg = 0; rg < 16 / RPI; ++rg) {
+        if (rg * RPI >= M) break;
+        const int row = rg * RPI + lane / CH, lc = (lane % CH) ^ (row & (CH - 1));
+        lds_load16x(rsx, &xls[wave][(u * 16 + rg * RPI) * XRB], row * (int)lda * (int)sizeof(AT) + lc * 16, soff);
+      }
+    }
+  }
   for (int s0 = s_lo; s0 < s_hi; s0 += U) {
     uint4 wv[U][R], xv[U][NMF];
     float sc[WBITS == 4 ? U : 1][R][4];
@@ -150,17 +225,55 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
       for (int t = 0; t < R; ++t)
         wv[u][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, w_off[t], st * 64, kNonTemporal));
+      if constexpr (!XL) {
 #pragma unroll
-      for (int j = 0; j < NMF; ++j)
-        xv[u][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                 rsx, x_off + 16 * j, xs_off, 0));
-      if constexpr (WBITS == 4) {
+        for (int j = 0; j < NMF; ++j)
+          xv[u][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   rsx, x_off + 16 * j, xs_off, 0));
+      }
+      if constexpr (WBITS == 4 && !SL) {
         const int64_t g = (int64_t)(st * KB / group) * ld_sg;
 #pragma unroll
         for (int t = 0; t < R; ++t)
 #pragma unroll
           for (int i = 0; i < 4; ++i) sc[u][t][i] = ld_scale(s, s_row[t][i] + g);
       }
+    }
+    // The LDS slices (scales, x) were filled by LDS-direct loads issued before the first
+    // chunk's global loads. The compiler does not model the full extent of those loads,
+    // so the wait is explicit: for everything but the chunk's own loads, issued after
+    // them (vector loads complete in order; a count above 63 waits for more, which is
+    // still correct).
+    if constexpr (SL || XL) {
+      constexpr int LPU = R + (XL ? 0 : NMF) + ((WBITS == 4 && !SL) ? 4 * R : 0);
+      if (s0 == s_lo) wait_vmcnt_le<(U * LPU < 63 ? U * LPU : 63)>();
+    }
+    if constexpr (WBITS == 4 && SL) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int gl = min(group_of(min(s0 + u, s_hi - 1)) - g0, SLG - 1);
+#pragma unroll
+        for (int t = 0; t < R; ++t) {
+          const uint4 v = *reinterpret_cast<const uint4*>(&sls[wave][gl * 16 * R + 16 * t + 4 * q]);
+          const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            if constexpr (sizeof(ST) == 2)
+              sc[u][t][i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(d[i] & 0xFFFFu));
+            else
+              sc[u][t][i] = __builtin_bit_cast(float, d[i]);
+          }
+        }
+      }
+    }
+    if constexpr (XL) {
+      // lane (r, q)'s pieces: chunks NMF q + j of row r (the k of the register path)
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int j = 0; j < NMF; ++j)
+          xv[u][j] = *reinterpret_cast<const uint4*>(
+              &xls[wave][(u * 16 + r) * XRB + (((NMF * q + j) ^ (r & (CH - 1))) * 16)]);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -236,10 +349,34 @@ template <int WBITS, typename AT, typename ST, int R, int WAVES>
 int launch_one(const WqArgs& p) {
   constexpr int U = 8;
   const int64_t blocks = cdiv(p.N, 16 * R);
-  hipLaunchKernelGGL((gemv_mfma_kernel<WBITS, AT, ST, R, WAVES, U>), dim3((unsigned)blocks),
-                     dim3(64 * WAVES), 0, p.stream, static_cast<const AT*>(p.a), p.lda, p.w, p.ldw,
-                     static_cast<const ST*>(p.s), p.ld_sn, p.ld_sg, p.group, static_cast<AT*>(p.c),
-                     p.ldc, (int)p.M, (int)p.N, (int)p.K);
+  // the LDS scale slice: every wavefront's steps span at most SLG groups, and the slice's
+  // global offsets stay in 32 bits
+  static const bool sl_env = env_int("MLS_GEMV_MFMA_SL", 1) != 0;
+  const int64_t nsteps = p.K / (WBITS == 4 ? 128 : 64), per_wave = cdiv(nsteps, WAVES);
+  const int64_t spg = WBITS == 4 ? p.group / 128 : 1;
+  const bool sl = WBITS == 4 && sl_env && cdiv(per_wave + spg - 1, spg) + 1 <= SLG &&
+                  16 * R * p.ld_sn * (int64_t)sizeof(ST) < (1ll << 30) && (int64_t)(p.K / p.group) * p.ld_sg * (int64_t)sizeof(ST) < (1ll << 30);
+  // x through LDS: one chunk per wavefront, and the wavefronts' slices within 128 KiB
+  static const bool xl_env = env_int("MLS_GEMV_MFMA_XL", 1) != 0;
+  constexpr bool XL_FITS = WAVES * U * 16 * (WBITS == 4 ? 256 : 128) <= 128 * 1024;
+  const bool xl = XL_FITS && xl_env && per_wave <= U;
+  auto go = [&](auto slc, auto xlc) {
+    hipLaunchKernelGGL((gemv_mfma_kernel<WBITS, AT, ST, R, WAVES, U, decltype(slc)::value, decltype(xlc)::value>),
+                       dim3((unsigned)blocks), dim3(64 * WAVES), 0, p.stream, static_cast<const AT*>(p.a), p.lda, p.w,
+                       p.ldw, static_cast<const ST*>(p.s), p.ld_sn, p.ld_sg, p.group, static_cast<AT*>(p.c), p.ldc,
+                       (int)p.M, (int)p.N, (int)p.K);
+  };
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  if constexpr (XL_FITS) {
+    if (xl) {
+      if (sl) go(T_{}, T_{});
+      else go(F_{}, T_{});
+      return MLS_OK;
+    }
+  }
+  if (sl) go(T_{}, F_{});
+  else go(F_{}, F_{});
   return MLS_OK;
 }
 
