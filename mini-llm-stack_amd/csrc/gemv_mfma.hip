@@ -386,6 +386,7 @@ int launch_shape(const WqArgs& p) {
   const int64_t nsteps = p.K / KB;
   int r = 1, waves = nsteps >= 64 ? 8 : 4;  // about 8 steps (one chunk) per wavefront
   if (nsteps >= 128) waves = 16;
+  // (twice the wavefronts with at most 4 steps each measured slower: M=16 6.05 -> 6.50 us)
   env_pair(r, waves);
   if (r == 2) {  // two tiles per wavefront: at most 8 wavefronts (16 spill)
     if (waves >= 8) return launch_one<WBITS, AT, ST, 2, 8>(p);
