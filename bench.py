@@ -244,6 +244,47 @@ def int8_prefill(dev, steps: int, warmup: int, M=2048, N=11008, K=4096):
     return dict(ms=ms, bytes=nbytes, flops=2 * M * N * K, copies=copies, parity=par)
 
 
+def floor_rows(dev, steps: int, warmup: int, nbytes=8_667_136, copies=125, blocks=256):
+    """The single-launch floor of the M = 1 GEMV rows (calibration kernels of
+    mini-llm-stack_amd/libmls_floor.so, not this build's product): an empty kernel with the
+    GEMV's grid, and a pure streaming read of the headline's bytes per launch, timed with the
+    GEMV's protocol (one HIP graph over `copies` rotated buffers). The GEMV cannot go below
+    the stream row's time; the empty row is the part of every launch that moves no data."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(str(ROOT / "mini-llm-stack_amd" / "libmls_floor.so"))
+    lib.mlsf_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
+    lib.mlsf_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    g = torch.Generator(device=dev).manual_seed(9)
+    bufs = [torch.randint(0, 2**31 - 1, (nbytes // 4,), generator=g, device=dev, dtype=torch.int32)
+            for _ in range(copies)]
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+
+    def st():
+        return torch.cuda.current_stream(dev).cuda_stream
+
+    def call(rc):
+        if rc != 0:
+            raise RuntimeError(f"floor kernel launch failed ({rc})")
+
+    ms_empty = time_steps([lambda: call(lib.mlsf_empty(blocks, st()))], warmup, steps)
+    best = None
+    for nb in (256, 512, 1024):  # blocks of 4 wavefronts (the GEMV: 256)
+        fns = [lambda b=b, nb=nb: call(lib.mlsf_stream(b.data_ptr(), nbytes, nb, sink.data_ptr(), st()))
+               for b in bufs]
+        ms = time_steps(fns, warmup, steps)
+        if best is None or ms < best[0]:
+            best = (ms, nb)
+    ms, nb_best = best
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    note = "calibration kernels (libmls_floor.so), not this build's product; timed like the M=1 GEMV"
+    return [{"name": f"floor_empty_kernel_{blocks}_blocks", "ms_per_step": round(ms_empty, 6), "note": note},
+            {"name": f"floor_stream_read_{nbytes}B", "ms_per_step": round(ms, 6), "TB/s": round(gbs / 1e3, 4),
+             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(gbs / HBM_PEAK_GBS, 4)},
+             "blocks": nb_best, "buffers_rotated": copies, "note": note}]
+
+
 def int8_dgrad_row(dev, steps: int, warmup: int, M=4096, N=11008, K=4096):
     """The INT8 STE backward's input gradient at a training shape (kernels/dequant_matmul.py:
     103-132): dx [M, K] = (dy [M, N] * s) @ W_q [N, K], bf16 dy. One step is the whole op:
@@ -790,6 +831,7 @@ def main(argv=None) -> int:
         "quantize_int4": lambda: _hbm_row("quantize_int4_14336x4096_g128", quantize_int4_load(dev, small, 4)),
         "ref_shapes": lambda: ref_shape_rows(dev, max(64, args.steps // 4), 16),
         "copy": lambda: _hbm_row("copy_256MiB", copy_calibration(dev, small, 4)),
+        "floor": lambda: floor_rows(dev, args.steps, args.warmup),
         "cpu": lambda: cpu_baseline(),
     }
     for kind, peak in (("fp8_rowwise", FP8_PEAK_TFLOPS), ("fp8_tensorwise", FP8_PEAK_TFLOPS),
@@ -817,7 +859,7 @@ def main(argv=None) -> int:
     if not args.no_extra:
         for k in ("int4_m4", "int4_m16", "int8_gemv", "int8_prefill", "int8_dgrad", "fp8_gemm", "fp8_native",
                   "fp8_bwd", "fp8_bwd_native", "moe_int4", "moe_mlp_int4", "paged_attn", "quantize_int4",
-                  "ref_shapes", "copy", "vendor_fp8_rowwise", "vendor_fp8_tensorwise", "vendor_bf16"):
+                  "ref_shapes", "copy", "floor", "vendor_fp8_rowwise", "vendor_fp8_tensorwise", "vendor_bf16"):
             log(f"{k} ...")
             row = runners[k]()
             log(json.dumps(row))

@@ -4,7 +4,8 @@
 
 Each .hip file is compiled by hipcc for --offload-arch=gfx950 into an object
 file under csrc/_build/, then linked into ../libmls_hip.so. Packed-fp32 VALU
-instructions are disabled for all device code (-packed-fp32-ops).
+instructions are disabled for all device code (-packed-fp32-ops). bench.py's
+calibration kernels (floor.hip) go into a separate ../libmls_floor.so.
 """
 
 from __future__ import annotations
@@ -70,7 +71,24 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
     os.replace(tmp, OUT)
+    build_floor(verbose)
     return OUT
+
+
+FLOOR_OUT = PKG / "libmls_floor.so"
+
+
+def build_floor(verbose: bool = False) -> Path:
+    """libmls_floor.so: bench.py's single-launch calibration kernels (floor.hip), kept
+    out of the library and its ABI."""
+    obj = compile_one("floor.hip", verbose)
+    tmp = FLOOR_OUT.with_suffix(".so.tmp")
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", "-Wl,--no-undefined", "-o", str(tmp), str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed (floor):\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, FLOOR_OUT)
+    return FLOOR_OUT
 
 
 def main(argv=None) -> int:
