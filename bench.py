@@ -537,7 +537,11 @@ def quantize_int4_load(dev, steps: int, warmup: int, N=14336, K=4096, gs=128):
     par["scales_exact"] = bool(torch.equal(s[r].cpu(), hs))
     par["ok"] = par["ok"] and par["scales_exact"]
     dp, ds = _quantize_int4_torch(ws[0], gs)
+    # the reference's op sequence run by torch on the GPU (tensor / float multiplies by a
+    # rounded reciprocal there) does not give the CPU bytes this kernel reproduces
     par["torch_device_ops_same_bytes"] = bool(torch.equal(dp, p) and torch.equal(ds, s))
+    par["torch_device_ops_differing_bytes"] = int((dp != p).sum())
+    par["torch_device_ops_differing_scales"] = int((ds != s).sum())
     del dp, ds
     fns = [lambda w=w: quantize_int4(w, gs) for w in ws]
     ms = time_steps(fns, warmup, steps) if par["ok"] else None
