@@ -35,7 +35,9 @@ class Int8MatmulSTE(torch.autograd.Function):
 
 
 class QuantLinearSTE(torch.nn.Module):
-    """Train-time quantized linear: fp32 master weights, INT8 forward."""
+    """Linear layer for quantization-aware training: the parameter stays fp32 and is
+    re-quantized to INT8 (per-row scales) at every forward; its gradient passes straight
+    through the quantizer."""
 
     def __init__(self, in_features: int, out_features: int):
         super().__init__()

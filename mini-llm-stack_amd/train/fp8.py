@@ -25,7 +25,9 @@ from kernels.fp8_matmul import (E4M3_MAX, E5M2_MAX, dequantize_e4m3, fp8_matmul,
 
 
 class DynamicScaler:
-    """Per-tensor delayed scaling: scale_t = max(amax history) / fp8_max."""
+    """One scale per tensor, chosen from the recent past: the largest |value| seen over
+    the last `history` calls, divided by the format's largest finite value. The very
+    first call has no past and uses the tensor's own maximum."""
 
     def __init__(self, fp8_max: float = E4M3_MAX, history: int = 16, enabled: bool = True):
         self.fp8_max = fp8_max
@@ -36,7 +38,7 @@ class DynamicScaler:
         if not self.enabled:
             return 1.0
         amax = float(t.detach().abs().amax())
-        if not self.hist:  # first call: just-in-time amax
+        if not self.hist:  # nothing recorded yet: seed the window with this tensor
             self.hist.append(max(amax, 1e-12))
         s = max(self.hist) / self.fp8_max
         self.hist.append(max(amax, 1e-12))
