@@ -76,34 +76,55 @@ __global__ __launch_bounds__(256) void int8_dgrad_kernel(const T* __restrict__ d
 }
 
 // ys[m][n] = T(dy[m][n] * s[n]) for n < N, 0 for N <= n < Np; ones[k] = 1 for k < K.
-// One thread per 8 consecutive n of a row.
-template <typename T>
+// One thread per 8 consecutive n of a row, consecutive threads on consecutive 16-byte
+// pieces of a row (VEC: one 16-byte load of dy, 16- or 32-byte loads of the scales).
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void dgrad_scale_kernel(const T* __restrict__ dy, int64_t lddy,
                                                           const void* __restrict__ s, int s_dt,
                                                           T* __restrict__ ys, int64_t Np, float* __restrict__ ones,
                                                           int M, int N, int K) {
+  // 2-D grid: x over a row's 8-element pieces (and, in the first row of blocks, the K
+  // ones), y over rows (grid-stride)
   const int64_t per_row = Np / 8;
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t < K) ones[t] = 1.0f;
-  if (t >= (int64_t)M * per_row) return;
-  const int64_t m = t / per_row;
-  const int n0 = (int)(t - m * per_row) * 8;
-  uint32_t o[4];
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (blockIdx.y == 0 && c < K) ones[c] = 1.0f;
+  if (c >= per_row) return;
+  const int n0 = (int)c * 8;
+  // this thread's 8 scales (0 past N), once for all its rows
+  float sv[8];
+  if (VEC && n0 + 8 <= N) {
+    if (s_dt == MLS_F16) {
+      const uint4 h = *reinterpret_cast<const uint4*>((const _Float16*)s + n0);
+      const _Float16* hv = reinterpret_cast<const _Float16*>(&h);
 #pragma unroll
-  for (int h = 0; h < 4; ++h) {
-    float v[2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) {
-      const int n = n0 + 2 * h + e;
-      v[e] = 0.0f;
-      if (n < N) {
-        const float sn = s_dt == MLS_F16 ? (float)((const _Float16*)s)[n] : ((const float*)s)[n];
-        v[e] = to_f32(dy[m * lddy + n]) * sn;
-      }
+      for (int e = 0; e < 8; ++e) sv[e] = (float)hv[e];
+    } else {
+      const float4 a = *reinterpret_cast<const float4*>((const float*)s + n0);
+      const float4 b = *reinterpret_cast<const float4*>((const float*)s + n0 + 4);
+      sv[0] = a.x; sv[1] = a.y; sv[2] = a.z; sv[3] = a.w;
+      sv[4] = b.x; sv[5] = b.y; sv[6] = b.z; sv[7] = b.w;
     }
-    o[h] = pack2_bits(from_f32<T>(v[0]), from_f32<T>(v[1]));
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      sv[e] = n0 + e < N ? (s_dt == MLS_F16 ? (float)((const _Float16*)s)[n0 + e] : ((const float*)s)[n0 + e]) : 0.0f;
   }
-  *reinterpret_cast<uint4*>(ys + m * Np + n0) = make_uint4(o[0], o[1], o[2], o[3]);
+  for (int64_t m = blockIdx.y; m < M; m += gridDim.y) {
+    float v[8];
+    if (VEC && n0 + 8 <= N) {  // one 16-byte load (rows 16-byte aligned: checked on the host)
+      const uint4 d = *reinterpret_cast<const uint4*>(dy + m * lddy + n0);
+      const T* dv = reinterpret_cast<const T*>(&d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = to_f32(dv[e]) * sv[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = n0 + e < N ? to_f32(dy[m * lddy + n0 + e]) * sv[e] : 0.0f;
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) o[h] = pack2_bits(from_f32<T>(v[2 * h]), from_f32<T>(v[2 * h + 1]));
+    *reinterpret_cast<uint4*>(ys + m * Np + n0) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
 }
 
 // Workspace layout of the matrix-core route (each part 256-byte aligned).
@@ -187,15 +208,21 @@ extern "C" int mls_int8_dgrad_ws(const void* dy, int dy_dt, int64_t lddy, const 
   uint8_t* wt = ws + L.wt_off;
   float* ones = reinterpret_cast<float*>(ws + L.ones_off);
   hipStream_t st = (hipStream_t)stream;
-  const int64_t threads = std::max<int64_t>(M * (L.Np / 8), K);
-  const dim3 grid((unsigned)cdiv(threads, 256));
-  if (cdiv(threads, 256) > 0x7FFFFFFF) return fail(MLS_ERR_UNSUPPORTED, "mls_int8_dgrad_ws: shape too large");
-  if (dy_dt == MLS_F16)
-    hipLaunchKernelGGL(dgrad_scale_kernel<_Float16>, grid, dim3(256), 0, st, (const _Float16*)dy, lddy, s,
-                       s_dt, (_Float16*)ys, L.Np, ones, (int)M, (int)N, (int)K);
-  else
-    hipLaunchKernelGGL(dgrad_scale_kernel<__bf16>, grid, dim3(256), 0, st, (const __bf16*)dy, lddy, s, s_dt,
-                       (__bf16*)ys, L.Np, ones, (int)M, (int)N, (int)K);
+  const int64_t gx = cdiv(std::max<int64_t>(L.Np / 8, K), 256);
+  if (gx > 0x7FFFFFFF) return fail(MLS_ERR_UNSUPPORTED, "mls_int8_dgrad_ws: shape too large");
+  // about 8 rows per thread: the scales are loaded once for all of them
+  const dim3 grid((unsigned)gx, (unsigned)std::min<int64_t>(cdiv(M, 8), 65535));
+  // 16-byte accesses when dy's rows and the scale vector are 16-byte aligned
+  const bool vec = aligned(dy, 16) && lddy % 8 == 0 && aligned(s, 16);
+  if (dy_dt == MLS_F16) {
+    auto k = vec ? dgrad_scale_kernel<_Float16, true> : dgrad_scale_kernel<_Float16, false>;
+    hipLaunchKernelGGL(k, grid, dim3(256), 0, st, (const _Float16*)dy, lddy, s, s_dt, (_Float16*)ys, L.Np, ones,
+                       (int)M, (int)N, (int)K);
+  } else {
+    auto k = vec ? dgrad_scale_kernel<__bf16, true> : dgrad_scale_kernel<__bf16, false>;
+    hipLaunchKernelGGL(k, grid, dim3(256), 0, st, (const __bf16*)dy, lddy, s, s_dt, (__bf16*)ys, L.Np, ones,
+                       (int)M, (int)N, (int)K);
+  }
   int rc = check_launch("mls_int8_dgrad_ws (scale)");
   if (rc != MLS_OK) return rc;
   rc = mls_transpose_u8(reinterpret_cast<const uint8_t*>(w), N, K, ldw, wt, L.Np, stream);
