@@ -555,8 +555,206 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_adma_kernel(const Mfma16P
   }
 }
 
+// ---------------------------------------------------------------------------
+// INT8 weight-only GEMM (dense, 256-row tiles) with the weight widening overlapped with
+// the MFMAs. The kernel above widens and stores the next stage's weights at the top of
+// a stage, and both wavefronts of a SIMD reach that point together (the barrier aligns
+// them), so their VALU work and their MFMAs never run at the same time; its barrier
+// also drains the weight loads issued at the top of the same stage. Here, per stage s
+// (activation and widened-weight tiles in separate double-buffered static LDS arrays,
+// so the compiler can tell a pending LDS-direct load from the tiles it reads or writes):
+//   1. read every operand of stage s from LDS,
+//   2. issue the activation loads of stage s + 1 into the other A buffer,
+//   3. the MFMAs of stage s, with stage s + 1's weights (in registers since stage
+//      s - 1) widened and stored into the other B buffer in pieces between groups of
+//      MFMAs,
+//   4. issue stage s + 2's weight loads into the freed registers,
+//   5. wait for this wavefront's loads but those weight loads, and barrier.
+// The weights are staged in 8-byte pieces (8 k of one row), so that every thread
+// issues the same number of loads (BN / 64 of them) whatever BN is: no thread-dependent
+// branch in the loop, and one constant vmcnt.
+// Measured at 2048 x 11008 x 4096 (same box, against the kernel above): MFMA busy 40% ->
+// 45% of the cycles, VALU co-issued with MFMAs 0.2% -> 15% of the MFMA cycles, 220 ->
+// 208 us.
+typedef uint32_t lds16_t __attribute__((ext_vector_type(4)));
+
+template <typename MT, typename OT, int BM, int BN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void mfma16_w8_kernel(const Mfma16Params p) {
+  constexpr int BK = 64;
+  constexpr int NW = WM * WN, NT = 64 * NW;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 16, TN = WTN / 16;
+  constexpr int PW = BM * 8 / NT;  // activation loads per wavefront and stage
+  static_assert(PW >= 1 && BM * 8 % NT == 0, "activation slots");
+  constexpr int B_PC = BN * 8;     // 8-byte weight pieces per stage
+  static_assert(B_PC % NT == 0, "whole pieces per thread");
+  constexpr int B_PT = B_PC / NT;  // per thread
+  static_assert(B_PT <= 15, "vmcnt");
+  constexpr int B_RSTEP = NT / 8;
+
+  __shared__ __align__(16) uint4 As[2][BM * 8];
+  __shared__ __align__(16) uint4 Bs[2][BN * 8];
+
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  const int nt = L / p.m_tiles, mt = L % p.m_tiles;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int M = p.M, N = p.N;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+
+  const int rows_a = min(BM, M - m0), rows_b = min(BN, N - n0);
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint8_t*)p.a + (int64_t)m0 * p.lda * 2), (short)0, (int)(rows_a * p.lda * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.b + (int64_t)n0 * p.ldb), (short)0, (int)(rows_b * p.ldb), 0x00020000);
+  int a_off[PW];
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int s = (wave * PW + i) * 64 + lane, row = s >> 3, lc = (s & 7) ^ (row & 7);
+    a_off[i] = row * (int)p.lda * 2 + lc * 16;
+  }
+  // piece tid + NT i: row (tid >> 3) + B_RSTEP i, k 8 (tid & 7) .. + 7 of the stage; its
+  // widened 16 bytes are LDS chunk (tid & 7) ^ (row & 7) of the row
+  const int b_row0 = tid >> 3, b_kc = tid & 7;
+  const int b_off0 = b_row0 * (int)p.ldb + b_kc * 8;
+  const int b_lds0 = b_row0 * 8 + (b_kc ^ swz(b_row0));  // B_RSTEP is a multiple of 8
+
+  uint2 rb[B_PT];
+  auto load_b = [&](int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < B_PT; ++i)
+      rb[i] = __builtin_bit_cast(
+          uint2, __builtin_amdgcn_raw_buffer_load_b64(rsb, b_off0 + B_RSTEP * i * (int)p.ldb, k0, 0));
+  };
+  auto store_piece = [&](uint4* bs, int i) __attribute__((always_inline)) {
+    const uint32_t d0 = rb[i].x, d1 = rb[i].y;
+    bs[b_lds0 + B_RSTEP * 8 * i] =
+        make_uint4(pack_exact2<MT>(sbyte_f32<0>(d0), sbyte_f32<1>(d0)), pack_exact2<MT>(sbyte_f32<2>(d0), sbyte_f32<3>(d0)),
+                   pack_exact2<MT>(sbyte_f32<0>(d1), sbyte_f32<1>(d1)), pack_exact2<MT>(sbyte_f32<2>(d1), sbyte_f32<3>(d1)));
+  };
+  auto dma_a = [&](uint4* as, int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < PW; ++i) lds_load16(rsa, as + (wave * PW + i) * 64, a_off[i], k0 * 2);
+  };
+
+  f32x4 acc[TN][TM];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int lr = lane & 15, lk = lane >> 4;
+  const int nk = p.K / BK;
+
+  // prologue: stage 0 in buffers 0, stage 1's weights in registers
+  dma_a(As[0], 0);
+  load_b(0);
+#pragma unroll
+  for (int i = 0; i < B_PT; ++i) store_piece(Bs[0], i);
+  load_b(BK);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int r = kt & 1;
+    // operand reads through an opaque base: otherwise the compiler may keep one address
+    // register per tile read live across the loop
+    uint32_t abase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)As[r];
+    uint32_t bbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)Bs[r];
+    asm volatile("" : "+v"(abase), "+v"(bbase));
+    const auto* as = reinterpret_cast<const __attribute__((address_space(3))) lds16_t*>(abase);
+    const auto* bs = reinterpret_cast<const __attribute__((address_space(3))) lds16_t*>(bbase);
+    uint4* as_next = As[r ^ 1];
+    uint4* bs_next = Bs[r ^ 1];
+    const int k0 = kt * BK;
+    uint4 aop[2][TM], bop[2][TN];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int ch = ks * 4 + lk;
+#pragma unroll
+      for (int i = 0; i < TN; ++i) {
+        const int row = wn0 + i * 16 + lr;
+        bop[ks][i] = __builtin_bit_cast(uint4, bs[row * 8 + (ch ^ swz(row))]);
+      }
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        const int row = wm0 + j * 16 + lr;
+        aop[ks][j] = __builtin_bit_cast(uint4, as[row * 8 + (ch ^ swz(row))]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    dma_a(as_next, k0 + BK);  // stage kt + 1 (past the end: zeros / unused)
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      // the 2 TN TM MFMAs in B_PT groups; each group also widens and stores one weight
+      // piece, which the scheduler interleaves with the group's MFMAs
+      constexpr int PER = 2 * TN * TM / B_PT;
+      static_assert(2 * TN * TM % B_PT == 0, "MFMA groups");
+#pragma unroll
+      for (int gi = 0; gi < B_PT; ++gi) {
+#pragma unroll
+        for (int x = gi * PER; x < (gi + 1) * PER; ++x) {
+          const int ks = x / (TN * TM), i = (x / TM) % TN, j = x % TM;
+          acc[i][j] = Mfma16<MT>::mma(bop[ks][i], aop[ks][j], acc[i][j]);
+        }
+        store_piece(bs_next, gi);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_b(k0 + 2 * BK);  // stage kt + 2 (past the end: harmless)
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    // everything but the weight loads just issued (vector loads complete in order),
+    // and the widened-weight stores
+    __builtin_amdgcn_s_waitcnt(B_PT | 0x70);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- epilogue: acc[i][j][r] = C[m = m0+wm0+16j+lr][n = n0+wn0+16i+4lk+r]
+  OT* c = static_cast<OT*>(p.c);
+#pragma unroll
+  for (int i = 0; i < TN; ++i) {
+    const int nb = n0 + wn0 + i * 16 + 4 * lk;
+    float sn[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sn[r] = scale_at(p.s, p.s_dt, (int64_t)min(nb + r, N - 1) * p.ld_sn);
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      const int m = m0 + wm0 + j * 16 + lr;
+      if (m >= M) continue;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] * sn[r];
+      OT* dst = c + (int64_t)m * p.ldc + nb;
+      if (nb + 3 < N && (p.ldc % 4) == 0) {
+        store4<OT>(dst, v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (nb + r < N) dst[r] = from_f32<OT>(v[r]);
+      }
+    }
+  }
+}
+
+template <typename MT, typename OT, int BN>
+static int launch_w8(Mfma16Params p, hipStream_t st) {
+  p.n_tiles = (int)cdiv(p.N, BN);
+  const int64_t blocks = (int64_t)p.n_tiles * p.m_tiles;
+  hipLaunchKernelGGL((mfma16_w8_kernel<MT, OT, 256, BN, 2, 4>), dim3((unsigned)blocks), dim3(512), 0, st, p);
+  return check_launch("INT8 GEMM");
+}
+
 template <int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN, bool GROUPED>
 static int launch_adma(Mfma16Params p, hipStream_t st) {
+  if constexpr (BKIND == B_INT8 && !GROUPED && BM == 256 && WM == 2 && WN == 4) {
+    static const bool w8 = env_int("MLS_W8", 1) != 0;  // 0: the kernel above, for A/B runs
+    if (w8) return launch_w8<MT, OT, BN>(p, st);
+
+  }
   p.n_tiles = (int)cdiv(p.N, BN);
   const size_t lds = (size_t)2 * (BM + BN) * 8 * 16 + (BKIND == B_INT4 ? (size_t)2 * 2 * BN * 4 : 0);
   auto kern = mfma16_adma_kernel<BKIND, MT, OT, BM, BN, WM, WN, GROUPED>;
