@@ -240,6 +240,7 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
     }
 
   const int nk = Kp / BK;
+  const int G_blk = Kp / p.group;  // groups of this block's K range
   if constexpr (STAB) {
     // scale table: row n0 + r holds G fp16 scales; 16-byte piece c = tid + 256 i is
     // row c / (G / 8), groups 8 (c % (G / 8)) .. + 7, written transposed to sT[g][r]
@@ -298,19 +299,33 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
 #pragma unroll
         for (int i = 0; i < TN; ++i) accg[i][j] = Mfma16<MT>::mma(bop[i], aop[j], accg[i][j]);
       }
-      if ((k0 + 32 * (ks + 1)) % p.group == 0) {  // group ends: acc += s[n] * partial
-        // the group's scales of this lane's 4 TN columns, read only here (the 1/16 of the
+      if ((k0 + 32 * (ks + 1)) % p.group == 0) {  // group ends
+        // the scales of this lane's 4 TN columns, read only here (the 1/16 of the
         // widening is applied once, in the epilogue)
         float sc[TN][4];
         if constexpr (STAB) {
+          // accg is never cleared: it holds T_g = P_0 + ... + P_g, the products of all
+          // groups so far, and sum_g s_g P_g = sum_g (s_g - s_{g+1}) T_g with s_G = 0
+          // (summation by parts), one FMA per accumulator and group instead of an FMA
+          // and a clear
           const int g = (k0 + 32 * ks) / p.group;
+          const int gn = min(g + 1, G_blk - 1);
+          const float keep = g + 1 < G_blk ? 1.f : 0.f;
 #pragma unroll
           for (int i = 0; i < TN; ++i) {
             const uint2 h2 = *reinterpret_cast<const uint2*>(sT + g * BN + wn * 64 + i * 16 + 4 * lk);
+            const uint2 n2 = *reinterpret_cast<const uint2*>(sT + gn * BN + wn * 64 + i * 16 + 4 * lk);
             const _Float16* h = reinterpret_cast<const _Float16*>(&h2);
+            const _Float16* hn = reinterpret_cast<const _Float16*>(&n2);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) sc[i][q] = (float)h[q];
+            for (int q = 0; q < 4; ++q) sc[i][q] = fmaf(-keep, (float)hn[q], (float)h[q]);
           }
+#pragma unroll
+          for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TMX; ++j)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) acc[i][j][q] = fmaf(sc[i][q], accg[i][j][q], acc[i][j][q]);
         } else {
 #pragma unroll
           for (int i = 0; i < TN; ++i) {
@@ -320,15 +335,16 @@ __global__ __launch_bounds__(256, 2) void grouped_int4_kernel(const Mfma16Params
             sc[i][2] = s4.z;
             sc[i][3] = s4.w;
           }
+          // acc += s[n] * partial, and a fresh partial for the next group
+#pragma unroll
+          for (int i = 0; i < TN; ++i)
+#pragma unroll
+            for (int j = 0; j < TMX; ++j) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) acc[i][j][q] = fmaf(sc[i][q], accg[i][j][q], acc[i][j][q]);
+              accg[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
         }
-#pragma unroll
-        for (int i = 0; i < TN; ++i)
-#pragma unroll
-          for (int j = 0; j < TMX; ++j) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) acc[i][j][q] = fmaf(sc[i][q], accg[i][j][q], acc[i][j][q]);
-            accg[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-          }
       }
     };
     kstep(Ring<0>{});
