@@ -255,10 +255,11 @@ def floor_rows(dev, steps: int, warmup: int, nbytes=8_667_136, copies=125, block
     lib = ctypes.CDLL(str(ROOT / "mini-llm-stack_amd" / "libmls_floor.so"))
     lib.mlsf_empty.argtypes = [ctypes.c_int, ctypes.c_void_p]
     lib.mlsf_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.mlsf_stream_store.argtypes = lib.mlsf_stream.argtypes
     g = torch.Generator(device=dev).manual_seed(9)
     bufs = [torch.randint(0, 2**31 - 1, (nbytes // 4,), generator=g, device=dev, dtype=torch.int32)
             for _ in range(copies)]
-    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    sink = torch.zeros(1024 * 8, dtype=torch.int32, device=dev)  # 8 bytes per wavefront of 1024 blocks
 
     def st():
         return torch.cuda.current_stream(dev).cuda_stream
@@ -277,12 +278,23 @@ def floor_rows(dev, steps: int, warmup: int, nbytes=8_667_136, copies=125, block
             best = (ms, nb)
     ms, nb_best = best
     gbs = nbytes / (ms * 1e-3) / 1e9
+    # the same read at the GEMV's grid, every wavefront then storing one 8-byte word as the
+    # GEMV does: what a launch that also writes its result costs
+    fns = [lambda b=b: call(lib.mlsf_stream_store(b.data_ptr(), nbytes, blocks, sink.data_ptr(), st()))
+           for b in bufs]
+    ms_st = time_steps(fns, warmup, steps)
+    gbs_st = nbytes / (ms_st * 1e-3) / 1e9
     note = "calibration kernels (libmls_floor.so), not this build's product; timed like the M=1 GEMV"
     return [{"name": f"floor_empty_kernel_{blocks}_blocks", "ms_per_step": round(ms_empty, 6), "note": note},
             {"name": f"floor_stream_read_{nbytes}B", "ms_per_step": round(ms, 6), "TB/s": round(gbs / 1e3, 4),
              "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(gbs / HBM_PEAK_GBS, 4)},
-             "blocks": nb_best, "buffers_rotated": copies, "note": note}]
+             "blocks": nb_best, "buffers_rotated": copies, "note": note},
+            {"name": f"floor_stream_read_store_{nbytes}B", "ms_per_step": round(ms_st, 6),
+             "TB/s": round(gbs_st / 1e3, 4),
+             "roofline": {"bound": "hbm", "achieved": round(gbs_st, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(gbs_st / HBM_PEAK_GBS, 4)},
+             "blocks": blocks, "buffers_rotated": copies, "stored_bytes": blocks * 4 * 8, "note": note}]
 
 
 def int8_dgrad_row(dev, steps: int, warmup: int, M=4096, N=11008, K=4096):

@@ -8,6 +8,9 @@
 //                non-temporal loads, no arithmetic beyond an xor of what was read, which is
 //                stored only if it equals a value the data does not hold, so the loads are
 //                not removed): the most a single launch can move through HBM at this size.
+//   mlsf_stream_store: the same read, and every wavefront then stores 8 bytes (the xor,
+//                twice) as the GEMV's wavefronts store their 4 outputs: the read plus the
+//                cost of a kernel that writes its result.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -20,7 +23,7 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // Wavefront w of the grid reads the contiguous chunks [w * per_wave, (w + 1) * per_wave):
 // each load instruction covers 1 KiB, and all L loads of a lane are issued before any
 // is used, as in the GEMV (one wavefront per SIMD, 256 blocks for the headline).
-template <int L>
+template <int L, bool STORE>
 __global__ __launch_bounds__(256) void floor_stream_kernel(const u32x4_t* __restrict__ buf, int64_t chunks,
                                                            int64_t per_wave, uint32_t* __restrict__ sink) {
   const int lane = threadIdx.x & 63;
@@ -34,10 +37,18 @@ __global__ __launch_bounds__(256) void floor_stream_kernel(const u32x4_t* __rest
     const int64_t c = c0 + min<int64_t>(64 * i + lane, per_wave - 1);
     d[i] = __builtin_nontemporal_load(buf + min<int64_t>(c, chunks - 1));
   }
+  __builtin_amdgcn_sched_barrier(0);  // every load issued before any is used
   uint32_t v = 0;
 #pragma unroll
   for (int i = 0; i < L; ++i) v ^= d[i].x ^ d[i].y ^ d[i].z ^ d[i].w;
-  if (v == 0x9E3779B9u) sink[0] = v;
+  if constexpr (STORE) {
+    // lane 63 holds the wavefront's value after the same kind of cross-lane steps the
+    // GEMV's reduction takes (one DPP row broadcast), and stores one 8-byte word per wavefront
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    if (lane == 63) reinterpret_cast<uint2*>(sink)[w] = make_uint2(v, v);
+  } else {
+    if (v == 0x9E3779B9u) sink[0] = v;
+  }
 }
 
 }  // namespace
@@ -49,8 +60,9 @@ extern "C" int mlsf_empty(int blocks, hipStream_t st) {
 }
 
 // `blocks` blocks of 4 wavefronts share `bytes` (a multiple of 16) in equal contiguous
-// spans; each lane issues up to 16 16-byte loads
-extern "C" int mlsf_stream(const void* buf, int64_t bytes, int blocks, uint32_t* sink, hipStream_t st) {
+// spans; each lane issues up to 16 16-byte loads. store: `sink` holds 8 bytes per
+// wavefront (blocks * 32 bytes), one word written by each.
+static int stream(const void* buf, int64_t bytes, int blocks, uint32_t* sink, hipStream_t st, bool store) {
   if (!buf || !sink || bytes <= 0 || bytes % 16 != 0 || blocks < 1) return -1;
   const int64_t chunks = bytes / 16;
   const int64_t per_wave = (chunks + 4LL * blocks - 1) / (4LL * blocks);
@@ -58,12 +70,25 @@ extern "C" int mlsf_stream(const void* buf, int64_t bytes, int blocks, uint32_t*
   const auto* p = static_cast<const u32x4_t*>(buf);
   const dim3 g((unsigned)blocks), b(256);
   switch (lpl) {
-#define MLSF_L(L_) \
-  case L_: hipLaunchKernelGGL(floor_stream_kernel<L_>, g, b, 0, st, p, chunks, per_wave, sink); break;
+#define MLSF_L(L_)                                                                               \
+  case L_:                                                                                       \
+    if (store)                                                                                   \
+      hipLaunchKernelGGL((floor_stream_kernel<L_, true>), g, b, 0, st, p, chunks, per_wave, sink);  \
+    else                                                                                         \
+      hipLaunchKernelGGL((floor_stream_kernel<L_, false>), g, b, 0, st, p, chunks, per_wave, sink); \
+    break;
     MLSF_L(1) MLSF_L(2) MLSF_L(3) MLSF_L(4) MLSF_L(5) MLSF_L(6) MLSF_L(7) MLSF_L(8)
     MLSF_L(9) MLSF_L(10) MLSF_L(11) MLSF_L(12) MLSF_L(13) MLSF_L(14) MLSF_L(15) MLSF_L(16)
 #undef MLSF_L
     default: return -1;
   }
   return hipGetLastError() == hipSuccess ? 0 : -2;
+}
+
+extern "C" int mlsf_stream(const void* buf, int64_t bytes, int blocks, uint32_t* sink, hipStream_t st) {
+  return stream(buf, bytes, blocks, sink, st, false);
+}
+
+extern "C" int mlsf_stream_store(const void* buf, int64_t bytes, int blocks, uint32_t* sink, hipStream_t st) {
+  return stream(buf, bytes, blocks, sink, st, true);
 }
