@@ -21,7 +21,8 @@
 // against an all-ones operand gives in the same accumulator layout:
 //   sum_k x (v - 8) = sum_k x (128 + v) - 136 sum_k x    (fp16: 1024, 1032).
 // INT4 group scales (group a multiple of 128, so a step lies in one group) multiply each
-// step's partial sums in fp32; the block's scales come into LDS once, by LDS-direct loads
+// step's partial sums in fp32 (groups of 64: steps of 64 k, a lane's 8 weight bytes
+// k [16q, 16q + 16), so that a step again lies in one group); the block's scales come into LDS once, by LDS-direct loads
 // issued right after the first two steps' operands. INT8 row scales multiply the reduced
 // tile. The instructions before the first operand loads are kept to a minimum: each one
 // delays the weight stream.
@@ -78,12 +79,14 @@ __device__ __forceinline__ uint4 perm_x(const uint4& v) {
 // (a & m) | c with m and c in registers: one v_and_or_b32
 __device__ __forceinline__ uint32_t andor(uint32_t a, uint32_t m, uint32_t c) { return (a & m) | c; }
 
-template <int WBITS, typename AT, typename ST, int TM, int TN, int D>
+template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64 = false>
 __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
   using MM = Mfma16<AT>;
   constexpr bool I4 = WBITS == 4;
-  constexpr int KS = I4 ? 128 : 64;   // k per step
-  constexpr int XP = I4 ? 4 : 2;      // 16-byte x pieces per lane, step and row tile
+  static_assert(!S64 || I4, "64-k INT4 steps");
+  constexpr int KS = I4 && !S64 ? 128 : 64;  // k per step
+  constexpr int XP = I4 && !S64 ? 4 : 2;     // 16-byte x pieces per lane, step and row tile
+  constexpr int WB = I4 && S64 ? 8 : 16;     // weight bytes per lane and step
   extern __shared__ __align__(16) uint8_t smem[];
 
   const int lane = threadIdx.x & 63;
@@ -108,10 +111,10 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
   const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc((void*)p.w, (short)0, p.w_bytes, 0x00020000);
   int xo[TM];
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) xo[tm] = (m0 + 16 * tm + r16) * p.lda * 2 + (I4 ? 64 : 32) * q;
+  for (int tm = 0; tm < TM; ++tm) xo[tm] = (m0 + 16 * tm + r16) * p.lda * 2 + XP * 16 * q;
   int wo[TN];
 #pragma unroll
-  for (int tn = 0; tn < TN; ++tn) wo[tn] = (n0 + 16 * tn + r16) * p.ldw + 16 * q;
+  for (int tn = 0; tn < TN; ++tn) wo[tn] = (n0 + 16 * tn + r16) * p.ldw + WB * q;
 
   struct Slot {
     uint4 x[TM][XP];
@@ -119,13 +122,20 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
   };
   auto load = [&](Slot& sl, int st) __attribute__((always_inline)) {
     const int live = st < s_hi;
-    const int sx = live ? st * KS * 2 : kPastEnd, sw = live ? st * 64 : kPastEnd;
+    const int sx = live ? st * KS * 2 : kPastEnd, sw = live ? st * 4 * WB : kPastEnd;
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
       for (int h = 0; h < XP; ++h) sl.x[tm][h] = ld16(rsa, xo[tm] + 16 * h, sx);
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) sl.w[tn] = ld16_nt(rsw, wo[tn], sw);
+    for (int tn = 0; tn < TN; ++tn) {
+      if constexpr (WB == 8) {
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rsw, wo[tn], sw, 2));
+        sl.w[tn] = make_uint4(v.x, v.y, 0u, 0u);
+      } else {
+        sl.w[tn] = ld16_nt(rsw, wo[tn], sw);
+      }
+    }
   };
   Slot sl[D];
 #pragma unroll
@@ -165,15 +175,16 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
 
   auto compute = [&](const Slot& sl, int st) __attribute__((always_inline)) {
     if constexpr (I4) {
-      uint4 xpm[TM][4];
+      constexpr int NJ = XP;  // weight dwords (8 nibbles each) per lane and step
+      uint4 xpm[TM][NJ];
       f32x4 xs[TM];
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xpm[tm][j] = perm_x(sl.x[tm][j]);
+        for (int j = 0; j < NJ; ++j) xpm[tm][j] = perm_x(sl.x[tm][j]);
         xs[tm] = zero;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) xs[tm] = MM::mma(ones, xpm[tm][j], xs[tm]);
+        for (int j = 0; j < NJ; ++j) xs[tm] = MM::mma(ones, xpm[tm][j], xs[tm]);
       }
       // scales of rows n = n0 + 16 tn + 4 q + i for this step's group (clamped past K)
       const int g = min(st * KS / p.group, p.G - 1);
@@ -181,9 +192,9 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
         const uint32_t d[4] = {sl.w[tn].x, sl.w[tn].y, sl.w[tn].z, sl.w[tn].w};
-        uint4 wop[4];
+        uint4 wop[NJ];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
           wop[j] = make_uint4(andor(d[j], nmask, magic), andor(d[j] >> 4, nmask, magic),
                               andor(d[j] >> 8, nmask, magic), andor(d[j] >> 12, nmask, magic));
         float sc[4];
@@ -193,7 +204,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
         for (int tm = 0; tm < TM; ++tm) {
           f32x4 pp = zero;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) pp = MM::mma(wop[j], xpm[tm][j], pp);
+          for (int j = 0; j < NJ; ++j) pp = MM::mma(wop[j], xpm[tm][j], pp);
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[tn][tm][i] = fmaf(sc[i], fmaf(-Nib<AT>::OFF, xs[tm][i], pp[i]), acc[tn][tm][i]);
         }
@@ -253,14 +264,14 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
   }
 }
 
-template <int WBITS, typename AT, typename ST, int TM, int TN, int D>
+template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64>
 int launch_small(SmallArgs a, hipStream_t st) {
   a.m_tiles = (int)cdiv(a.M, 16 * TM);
   const int64_t nt = cdiv(cdiv(a.N, 16 * TN), 8) * 8;
   const int red = 4 * TN * TM * 64 * 16;
   const int sc = WBITS == 4 ? 16 * TN * a.G * (int)sizeof(ST) + 256 * 4 : 0;  // + padding of the last dword load
   if (a.m_tiles > 65535) return MLS_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((gemm_small_kernel<WBITS, AT, ST, TM, TN, D>), dim3((unsigned)nt, (unsigned)a.m_tiles), dim3(256),
+  hipLaunchKernelGGL((gemm_small_kernel<WBITS, AT, ST, TM, TN, D, S64>), dim3((unsigned)nt, (unsigned)a.m_tiles), dim3(256),
                      red > sc ? red : sc, st, a);
   return MLS_OK;
 }
@@ -275,7 +286,7 @@ double small_cost(int64_t M, int64_t N, int64_t K, int wbits, int tm, int tn) {
   return (double)cdiv(blocks, 256) * per_block;
 }
 
-template <int WBITS, typename AT, typename ST>
+template <int WBITS, typename AT, typename ST, bool S64 = false>
 int dispatch_small(SmallArgs a, hipStream_t st) {
   static const int force = env_int("MLS_SMALL_TILE", 0);  // TM * 10 + TN (sweeps)
   int best_tm = 1, best_tn = 1;
@@ -297,7 +308,7 @@ int dispatch_small(SmallArgs a, hipStream_t st) {
   }
   // ring depth 2: deeper rings (up to 8 steps in flight) measured slower at M = 4..128
 #define MLS_SMALL(TM_, TN_) \
-  if (best_tm == TM_ && best_tn == TN_) return launch_small<WBITS, AT, ST, TM_, TN_, 2>(a, st)
+  if (best_tm == TM_ && best_tn == TN_) return launch_small<WBITS, AT, ST, TM_, TN_, 2, S64>(a, st)
   MLS_SMALL(1, 1); MLS_SMALL(1, 2); MLS_SMALL(1, 4);
   MLS_SMALL(2, 1); MLS_SMALL(2, 2); MLS_SMALL(2, 4);
   MLS_SMALL(4, 1); MLS_SMALL(4, 2);
@@ -310,9 +321,11 @@ int dispatch_small(SmallArgs a, hipStream_t st) {
 
 int launch_gemm_small(int wbits, const WqArgs& p) {
   if (p.a_dt != MLS_BF16 && p.a_dt != MLS_F16) return MLS_ERR_UNSUPPORTED;
-  const int KS = wbits == 4 ? 128 : 64;
+  // INT4 steps of 128 k (groups a multiple of 128) or of 64 k (groups of 64)
+  const bool s64 = wbits == 4 && p.group % 128 != 0;
+  const int KS = wbits == 4 && !s64 ? 128 : 64;
   if (p.K % KS != 0 || p.K < KS) return MLS_ERR_UNSUPPORTED;
-  if (wbits == 4 && p.group % 128 != 0) return MLS_ERR_UNSUPPORTED;
+  if (wbits == 4 && p.group % 64 != 0) return MLS_ERR_UNSUPPORTED;
   if (!aligned(p.a, 16) || p.lda % 8 != 0 || !aligned(p.w, 16) || p.ldw % 16 != 0) return MLS_ERR_UNSUPPORTED;
   // 32-bit buffer offsets below the past-the-end soffset
   if (p.M * p.lda * 2 >= kPastEnd / 2 || (p.N + 64) * p.ldw >= kPastEnd / 2) return MLS_ERR_UNSUPPORTED;
@@ -330,6 +343,12 @@ int launch_gemm_small(int wbits, const WqArgs& p) {
       return MLS_ERR_UNSUPPORTED;
     if (64 * a.G * ssz + 1024 > 65536 || p.N * p.ld_sn * ssz >= kPastEnd / 2) return MLS_ERR_UNSUPPORTED;
     a.s_bytes = (int)(p.N * p.ld_sn * ssz);
+  }
+  if (wbits == 4 && s64) {
+    if (p.a_dt == MLS_BF16) return p.s_dt == MLS_F16 ? dispatch_small<4, __bf16, _Float16, true>(a, p.stream)
+                                                     : dispatch_small<4, __bf16, float, true>(a, p.stream);
+    return p.s_dt == MLS_F16 ? dispatch_small<4, _Float16, _Float16, true>(a, p.stream)
+                             : dispatch_small<4, _Float16, float, true>(a, p.stream);
   }
   if (wbits == 4) {
     if (p.a_dt == MLS_BF16) return p.s_dt == MLS_F16 ? dispatch_small<4, __bf16, _Float16>(a, p.stream)

@@ -235,7 +235,9 @@ def test_medium_int8(dev, M, N, K, dtype):
     (40, 1000, 1152, 128, torch.bfloat16),   # 9 steps: wavefronts of 2 and 3 steps
     (200, 520, 768, 256, torch.float16),     # a group spans two steps
     (33, 4096, 4096, 128, torch.bfloat16),
-    (128, 2048, 2048, 64, torch.float16),    # group 64: not this path (engine), same answer
+    (128, 2048, 2048, 64, torch.float16),    # group 64: steps of 64 k (the reference's bench shape)
+    (40, 1000, 1088, 64, torch.bfloat16),    # group 64, 17 steps: wavefronts of 4 and 5 steps
+    (130, 520, 576, 192, torch.float16),     # group 192: 64-k steps, a group spans three
 ])
 def test_medium_int4(dev, M, N, K, gs, dtype):
     a, p, s, want = _int4_setup(dev, M, N, K, gs, 900 + M, dtype)
