@@ -15,7 +15,8 @@
 // the exact integer q + 128. The offset is removed with the per-row sums of x, which
 // one more MFMA against an all-ones operand produces in the same accumulator layout:
 //   sum_k x (v - 8) = sum_k x (128 + v) - 136 sum_k x          (bf16; fp16: 1024, 1032).
-// INT4 group scales multiply each step's partial sums (groups are multiples of 128);
+// INT4 group scales multiply each step's partial sums (groups are multiples of 128; groups
+// of 64 take steps of 64 k, a lane's 8 weight bytes per tile k [16q, 16q + 16));
 // the INT8 row scale multiplies the reduced total.
 //
 // MFMA operands: weights are the "A" operand (rows n), x the "B" operand (columns m),
@@ -123,15 +124,16 @@ constexpr int SLG = 16;
 // address units (not HBM) bounded the kernel. The 16-byte chunk index of row r is XOR-ed
 // with r & (CH - 1) (conflict-free 16-row reads). Rows of the slice at or past M hold
 // zeros or stale data; they feed only output columns m >= M, which are never stored.
-template <int WBITS, typename AT, typename ST, int R, int WAVES, int U, bool SL, bool XL>
+template <int WBITS, typename AT, typename ST, int R, int WAVES, int U, bool SL, bool XL, bool S64>
 // One wavefront per SIMD is the design point (a grid of N / 16 blocks of WAVES
 // wavefronts), so the compiler may spend registers on keeping a chunk's loads in flight.
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemv_mfma_kernel(
     const AT* __restrict__ a, int64_t lda, const uint8_t* __restrict__ w, int64_t ldw,
     const ST* __restrict__ s, int64_t ld_sn, int64_t ld_sg, int group, AT* __restrict__ c,
     int64_t ldc, int M, int N, int K) {
-  constexpr int KB = WBITS == 4 ? 128 : 64;  // k per step
-  constexpr int NMF = WBITS == 4 ? 4 : 2;    // MFMAs per step and 16-row tile
+  constexpr bool W16 = WBITS == 8 || !S64;    // 16 weight bytes per lane and step (else 8)
+  constexpr int KB = WBITS == 4 && W16 ? 128 : 64;  // k per step
+  constexpr int NMF = WBITS == 4 && W16 ? 4 : 2;    // MFMAs per step and 16-row tile
   __shared__ f32x4 red[WAVES][R][64];
   // one dword per scale: an LDS-direct load of 2 bytes still advances 4 bytes per lane
   __shared__ __align__(16) uint32_t sls[SL ? WAVES : 1][SL ? SLG * 16 * R : 1];
@@ -178,10 +180,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
   const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(w + (int64_t)n_base * ldw), (short)0, (int)(rows_w * ldw), 0x00020000);
   // this lane's byte offsets inside a step (x row m = r)
-  const int x_off = r * (int)lda * (int)sizeof(AT) + (WBITS == 4 ? 64 * q : 32 * q);
+  const int x_off = r * (int)lda * (int)sizeof(AT) + NMF * 16 * q;
   int w_off[R];
 #pragma unroll
-  for (int t = 0; t < R; ++t) w_off[t] = (16 * t + r) * (int)ldw + 16 * q;
+  for (int t = 0; t < R; ++t) w_off[t] = (16 * t + r) * (int)ldw + (W16 ? 16 : 8) * q;
   // scale rows of this lane's accumulators: n = n_base + 16 t + 4 q + i
   int64_t s_row[R][4];
 #pragma unroll
@@ -224,7 +226,12 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
       const int xs_off = live ? st * KB * (int)sizeof(AT) : 0x7FFFFFF0;
 #pragma unroll
       for (int t = 0; t < R; ++t)
-        wv[u][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, w_off[t], st * 64, kNonTemporal));
+        if constexpr (W16) {
+          wv[u][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, w_off[t], st * 64, kNonTemporal));
+        } else {
+          const uint2 v2 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rsw, w_off[t], st * 32, kNonTemporal));
+          wv[u][t] = make_uint4(v2.x, v2.y, 0u, 0u);
+        }
       if constexpr (!XL) {
 #pragma unroll
         for (int j = 0; j < NMF; ++j)
@@ -345,23 +352,24 @@ int env_pair(int& r, int& waves) {
   return sscanf(v, "%d,%d", &r, &waves) == 2;
 }
 
-template <int WBITS, typename AT, typename ST, int R, int WAVES>
+template <int WBITS, typename AT, typename ST, int R, int WAVES, bool S64>
 int launch_one(const WqArgs& p) {
   constexpr int U = 8;
+  constexpr int KB = WBITS == 4 && !S64 ? 128 : 64;
   const int64_t blocks = cdiv(p.N, 16 * R);
   // the LDS scale slice: every wavefront's steps span at most SLG groups, and the slice's
   // global offsets stay in 32 bits
   static const bool sl_env = env_int("MLS_GEMV_MFMA_SL", 1) != 0;
-  const int64_t nsteps = p.K / (WBITS == 4 ? 128 : 64), per_wave = cdiv(nsteps, WAVES);
-  const int64_t spg = WBITS == 4 ? p.group / 128 : 1;
+  const int64_t nsteps = p.K / KB, per_wave = cdiv(nsteps, WAVES);
+  const int64_t spg = WBITS == 4 ? p.group / KB : 1;
   const bool sl = WBITS == 4 && sl_env && cdiv(per_wave + spg - 1, spg) + 1 <= SLG &&
                   16 * R * p.ld_sn * (int64_t)sizeof(ST) < (1ll << 30) && (int64_t)(p.K / p.group) * p.ld_sg * (int64_t)sizeof(ST) < (1ll << 30);
   // x through LDS: one chunk per wavefront, and the wavefronts' slices within 128 KiB
   static const bool xl_env = env_int("MLS_GEMV_MFMA_XL", 1) != 0;
-  constexpr bool XL_FITS = WAVES * U * 16 * (WBITS == 4 ? 256 : 128) <= 128 * 1024;
+  constexpr bool XL_FITS = WAVES * U * 16 * KB * 2 <= 128 * 1024;
   const bool xl = XL_FITS && xl_env && per_wave <= U;
   auto go = [&](auto slc, auto xlc) {
-    hipLaunchKernelGGL((gemv_mfma_kernel<WBITS, AT, ST, R, WAVES, U, decltype(slc)::value, decltype(xlc)::value>),
+    hipLaunchKernelGGL((gemv_mfma_kernel<WBITS, AT, ST, R, WAVES, U, decltype(slc)::value, decltype(xlc)::value, S64>),
                        dim3((unsigned)blocks), dim3(64 * WAVES), 0, p.stream, static_cast<const AT*>(p.a), p.lda, p.w,
                        p.ldw, static_cast<const ST*>(p.s), p.ld_sn, p.ld_sg, p.group, static_cast<AT*>(p.c), p.ldc,
                        (int)p.M, (int)p.N, (int)p.K);
@@ -380,26 +388,26 @@ int launch_one(const WqArgs& p) {
   return MLS_OK;
 }
 
-template <int WBITS, typename AT, typename ST>
+template <int WBITS, typename AT, typename ST, bool S64>
 int launch_shape(const WqArgs& p) {
-  constexpr int KB = WBITS == 4 ? 128 : 64;
+  constexpr int KB = WBITS == 4 && !S64 ? 128 : 64;
   const int64_t nsteps = p.K / KB;
   int r = 1, waves = nsteps >= 64 ? 8 : 4;  // about 8 steps (one chunk) per wavefront
   if (nsteps >= 128) waves = 16;
   // (twice the wavefronts with at most 4 steps each measured slower: M=16 6.05 -> 6.50 us)
   env_pair(r, waves);
   if (r == 2) {  // two tiles per wavefront: at most 8 wavefronts (16 spill)
-    if (waves >= 8) return launch_one<WBITS, AT, ST, 2, 8>(p);
-    return launch_one<WBITS, AT, ST, 2, 4>(p);
+    if (waves >= 8) return launch_one<WBITS, AT, ST, 2, 8, S64>(p);
+    return launch_one<WBITS, AT, ST, 2, 4, S64>(p);
   }
-  if (waves == 16) return launch_one<WBITS, AT, ST, 1, 16>(p);
-  if (waves == 8) return launch_one<WBITS, AT, ST, 1, 8>(p);
-  return launch_one<WBITS, AT, ST, 1, 4>(p);
+  if (waves == 16) return launch_one<WBITS, AT, ST, 1, 16, S64>(p);
+  if (waves == 8) return launch_one<WBITS, AT, ST, 1, 8, S64>(p);
+  return launch_one<WBITS, AT, ST, 1, 4, S64>(p);
 }
 
-template <int WBITS, typename AT>
+template <int WBITS, typename AT, bool S64 = false>
 int launch_st(const WqArgs& p) {
-  return p.s_dt == MLS_F16 ? launch_shape<WBITS, AT, _Float16>(p) : launch_shape<WBITS, AT, float>(p);
+  return p.s_dt == MLS_F16 ? launch_shape<WBITS, AT, _Float16, S64>(p) : launch_shape<WBITS, AT, float, S64>(p);
 }
 
 }  // namespace
@@ -412,15 +420,18 @@ int launch_gemv_mfma(int wbits, const WqArgs& p) {
   if (!enabled) return MLS_ERR_UNSUPPORTED;
   if (p.a_dt != MLS_BF16 && p.a_dt != MLS_F16) return MLS_ERR_UNSUPPORTED;
   if (p.M < 1 || p.M > 16) return MLS_ERR_UNSUPPORTED;
-  const int KB = wbits == 4 ? 128 : 64;
+  // INT4 steps of 128 k (groups a multiple of 128) or of 64 k (other multiples of 64)
+  const bool s64 = wbits == 4 && p.group % 128 != 0;
+  const int KB = wbits == 4 && !s64 ? 128 : 64;
   if (p.K % KB != 0) return MLS_ERR_UNSUPPORTED;
-  if (wbits == 4 && p.group % 128 != 0) return MLS_ERR_UNSUPPORTED;
+  if (wbits == 4 && p.group % 64 != 0) return MLS_ERR_UNSUPPORTED;
   if (!aligned(p.a, 16) || (p.lda * 2) % 16 != 0) return MLS_ERR_UNSUPPORTED;
   if (!aligned(p.w, 16) || p.ldw % 16 != 0) return MLS_ERR_UNSUPPORTED;
   // 32-bit buffer offsets: 16 rows of x and a 32-row weight tile
   // (and the past-the-end x offset 0x7FFFFFF0 added to an x offset must not wrap)
   if (16 * p.lda * 2 >= (1ll << 31) || 32 * p.ldw >= (1ll << 31)) return MLS_ERR_UNSUPPORTED;
   if (p.N > 0x7FFFFFFF - 32 || p.K > 0x3FFFFFFF) return MLS_ERR_UNSUPPORTED;
+  if (wbits == 4 && s64) return p.a_dt == MLS_BF16 ? launch_st<4, __bf16, true>(p) : launch_st<4, _Float16, true>(p);
   if (wbits == 4) return p.a_dt == MLS_BF16 ? launch_st<4, __bf16>(p) : launch_st<4, _Float16>(p);
   return p.a_dt == MLS_BF16 ? launch_st<8, __bf16>(p) : launch_st<8, _Float16>(p);
 }

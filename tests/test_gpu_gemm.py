@@ -179,6 +179,9 @@ def test_gemv_long_k(dev):
     (7, 333, 768, 256, torch.float16),        # group of two steps, odd M, ragged N
     (16, 4096, 14336, 128, torch.bfloat16),   # 112 steps: 16 wavefronts, chunks with tails
     (3, 48, 128, 128, torch.bfloat16),        # a single step: three wavefronts have none
+    (16, 2048, 2048, 64, torch.float16),      # group 64: steps of 64 k (the reference's bench shape)
+    (5, 1000, 1088, 64, torch.bfloat16),      # group 64, 17 steps, ragged N
+    (9, 520, 576, 192, torch.float16),        # group 192: 64-k steps, a group spans three
 ])
 def test_skinny_int4(dev, M, N, K, gs, dtype):
     a, p, s, want = _int4_setup(dev, M, N, K, gs, 500 + M, dtype)
