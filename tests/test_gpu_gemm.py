@@ -274,6 +274,21 @@ def test_mfma_int8(dev, M, N, K, dtype):
     _check(out, ref.int8_matmul(a.float().numpy(), q.cpu().numpy(), s.cpu().numpy()), f"int8 {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K", [
+    (1000, 11000, 512),   # 256 x 192 tiles, M and N ragged
+    (4000, 4000, 256),    # 256 x 256 tiles (two rounds of 192-wide ones would be slower), ragged
+])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mfma_int8_256_row_tiles(dev, M, N, K, dtype):
+    """Shapes that take the 256-row INT8 kernel (widening interleaved with the MFMAs), with
+    partial row and column tiles."""
+    a, w = _data(M, N, K, M + N + K + 7, 0.02)
+    q, s = quantize_int8(w.to(dev))
+    a = a.to(dtype)
+    out = int8_matmul(a.to(dev), q, s)
+    _check(out, ref.int8_matmul(a.float().numpy(), q.cpu().numpy(), s.cpu().numpy()), f"int8 {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("M,N,K,gs", [(17, 256, 256, 128), (64, 512, 512, 32), (100, 300, 320, 64),
                                       (256, 1024, 1024, 128), (513, 768, 640, 128)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
