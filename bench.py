@@ -270,7 +270,9 @@ def floor_rows(dev, steps: int, warmup: int, nbytes=8_667_136, copies=125, block
 
     ms_empty = time_steps([lambda: call(lib.mlsf_empty(blocks, st()))], warmup, steps)
     best = None
-    for nb in (256, 512, 1024):  # blocks of 4 wavefronts (the GEMV: 256)
+    for nb in (256, 512, 1024):  # blocks of 4 wavefronts (the INT4 GEMV: 256, INT8: 512)
+        if nbytes // 16 > nb * 4 * 64 * 16:  # the stream kernel issues at most 16 loads per lane
+            continue
         fns = [lambda b=b, nb=nb: call(lib.mlsf_stream(b.data_ptr(), nbytes, nb, sink.data_ptr(), st()))
                for b in bufs]
         ms = time_steps(fns, warmup, steps)
@@ -852,7 +854,9 @@ def main(argv=None) -> int:
         "quantize_int4": lambda: _hbm_row("quantize_int4_14336x4096_g128", quantize_int4_load(dev, small, 4)),
         "ref_shapes": lambda: ref_shape_rows(dev, max(64, args.steps // 4), 16),
         "copy": lambda: _hbm_row("copy_256MiB", copy_calibration(dev, small, 4)),
-        "floor": lambda: floor_rows(dev, args.steps, args.warmup),
+        "floor": lambda: (floor_rows(dev, args.steps, args.warmup)
+                          + floor_rows(dev, args.steps, args.warmup, nbytes=16_801_792, copies=64,
+                                       blocks=512)[1:]),
         "cpu": lambda: cpu_baseline(),
     }
     for kind, peak in (("fp8_rowwise", FP8_PEAK_TFLOPS), ("fp8_tensorwise", FP8_PEAK_TFLOPS),
