@@ -184,7 +184,8 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_bytes_kernel(const Mfma16Par
   const uint32_t lds0 = lds_addr(smem);
 
   const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int nt = L / p.m_tiles, mt = L % p.m_tiles;
+  int nt, mt;
+  tile_order(L, p.m_tiles, p.n_tiles, p.tile_gm, mt, nt);
   const int m0 = mt * BM, n0 = nt * BN;
   const int M = p.M, N = p.N;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -338,6 +339,8 @@ template <int AKIND, int BKIND, typename MT, typename OT, int BM, int BN, int WM
 int launch_bytes(Mfma16Params p, hipStream_t st) {
   p.n_tiles = (int)cdiv(p.N, BN);
   p.m_tiles = (int)cdiv(p.M, BM);
+  static const int gm = env_int("MLS_TILE_GM", 4);  // row tiles per run of the tile order (0: column-major)
+  p.tile_gm = gm;
   constexpr size_t lds = (size_t)3 * (BM * RowFmt<AKIND != A_RAW16>::BYTES_PER_ROW + BN * 64);
   auto kern = gemm_bytes_kernel<AKIND, BKIND, MT, OT, BM, BN, WM, WN>;
   static bool attr_set = false;  // raise the dynamic LDS limit once per instantiation

@@ -596,7 +596,8 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_w8_kernel(const Mfma16Par
   __shared__ __align__(16) uint4 Bs[2][BN * 8];
 
   const int L = xcd_remap(blockIdx.x, gridDim.x);
-  const int nt = L / p.m_tiles, mt = L % p.m_tiles;
+  int nt, mt;
+  tile_order(L, p.m_tiles, p.n_tiles, p.tile_gm, mt, nt);
   const int m0 = mt * BM, n0 = nt * BN;
   const int M = p.M, N = p.N;
 
@@ -743,6 +744,8 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_w8_kernel(const Mfma16Par
 template <typename MT, typename OT, int BN>
 static int launch_w8(Mfma16Params p, hipStream_t st) {
   p.n_tiles = (int)cdiv(p.N, BN);
+  static const int gm = env_int("MLS_TILE_GM", 4);  // row tiles per run of the tile order (0: column-major)
+  p.tile_gm = gm;
   const int64_t blocks = (int64_t)p.n_tiles * p.m_tiles;
   hipLaunchKernelGGL((mfma16_w8_kernel<MT, OT, 256, BN, 2, 4>), dim3((unsigned)blocks), dim3(512), 0, st, p);
   return check_launch("INT8 GEMM");

@@ -36,6 +36,7 @@ struct Mfma16Params {
   int64_t c_sstride;              // grouped split: elements between the partial outputs
   const int32_t* a_rows;          // grouped: sorted row m is row a_rows[m] of a (null: row m)
   int a_src_rows;                 // grouped: rows of a when a_rows is set
+  int tile_gm;                    // dense: row tiles per run of the tile order (0: column-major)
 };
 
 template <typename T> struct Mfma16;
@@ -65,6 +66,20 @@ template <> struct Mfma16<_Float16> {
 };
 
 __device__ __forceinline__ int swz(int row) { return row & 7; }
+
+// Logical tile L (consecutive on one XCD after xcd_remap) -> (row tile, column tile). gm = 0:
+// every row tile of a column tile in turn. gm > 0: runs of gm row tiles sweep all column
+// tiles, so an XCD's 32 concurrent blocks share ~gm row tiles and ~32 / gm column tiles.
+__device__ __forceinline__ void tile_order(int L, int m_tiles, int n_tiles, int gm, int& mt, int& nt) {
+  if (gm <= 0) {
+    nt = L / m_tiles;
+    mt = L % m_tiles;
+    return;
+  }
+  const int per = gm * n_tiles, first = (L / per) * gm, gsz = min(m_tiles - first, gm), r = L % per;
+  mt = first + r % gsz;
+  nt = r / gsz;
+}
 
 __device__ __forceinline__ float scale_at(const void* s, int s_dt, int64_t i) {
   return s_dt == MLS_F16 ? (float)((const _Float16*)s)[i] : ((const float*)s)[i];
