@@ -83,11 +83,12 @@ __global__ __launch_bounds__(256) void dgrad_scale_kernel(const T* __restrict__ 
                                                           const void* __restrict__ s, int s_dt,
                                                           T* __restrict__ ys, int64_t Np, float* __restrict__ ones,
                                                           int M, int N, int K) {
-  // 2-D grid: x over a row's 8-element pieces (and, in the first row of blocks, the K
-  // ones), y over rows (grid-stride)
+  // 2-D grid: x over a row's 8-element pieces (the first row of blocks also writes the K
+  // ones, grid-stride), y over rows (grid-stride)
   const int64_t per_row = Np / 8;
   const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (blockIdx.y == 0 && c < K) ones[c] = 1.0f;
+  if (blockIdx.y == 0)
+    for (int64_t i = c; i < K; i += (int64_t)gridDim.x * 256) ones[i] = 1.0f;
   if (c >= per_row) return;
   const int n0 = (int)c * 8;
   // this thread's 8 scales (0 past N), once for all its rows
@@ -109,7 +110,28 @@ __global__ __launch_bounds__(256) void dgrad_scale_kernel(const T* __restrict__ 
     for (int e = 0; e < 8; ++e)
       sv[e] = n0 + e < N ? (s_dt == MLS_F16 ? (float)((const _Float16*)s)[n0 + e] : ((const float*)s)[n0 + e]) : 0.0f;
   }
-  for (int64_t m = blockIdx.y; m < M; m += gridDim.y) {
+  const int64_t ystep = gridDim.y;
+  int64_t m = blockIdx.y;
+  if (VEC && n0 + 8 <= N) {
+    // RB rows at a time, every load issued before the first use: RB 16-byte loads in
+    // flight per thread instead of one
+    constexpr int RB = 4;
+    for (; m + (RB - 1) * ystep < M; m += RB * ystep) {
+      uint4 d[RB];
+#pragma unroll
+      for (int r = 0; r < RB; ++r) d[r] = *reinterpret_cast<const uint4*>(dy + (m + r * ystep) * lddy + n0);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const T* dv = reinterpret_cast<const T*>(&d[r]);
+        uint32_t o[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          o[h] = pack2_bits(from_f32<T>(to_f32(dv[2 * h]) * sv[2 * h]), from_f32<T>(to_f32(dv[2 * h + 1]) * sv[2 * h + 1]));
+        *reinterpret_cast<uint4*>(ys + (m + r * ystep) * Np + n0) = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+  for (; m < M; m += ystep) {
     float v[8];
     if (VEC && n0 + 8 <= N) {  // one 16-byte load (rows 16-byte aligned: checked on the host)
       const uint4 d = *reinterpret_cast<const uint4*>(dy + m * lddy + n0);
@@ -208,7 +230,7 @@ extern "C" int mls_int8_dgrad_ws(const void* dy, int dy_dt, int64_t lddy, const 
   uint8_t* wt = ws + L.wt_off;
   float* ones = reinterpret_cast<float*>(ws + L.ones_off);
   hipStream_t st = (hipStream_t)stream;
-  const int64_t gx = cdiv(std::max<int64_t>(L.Np / 8, K), 256);
+  const int64_t gx = cdiv(L.Np / 8, 256);
   if (gx > 0x7FFFFFFF) return fail(MLS_ERR_UNSUPPORTED, "mls_int8_dgrad_ws: shape too large");
   // about 8 rows per thread: the scales are loaded once for all of them
   const dim3 grid((unsigned)gx, (unsigned)std::min<int64_t>(cdiv(M, 8), 65535));

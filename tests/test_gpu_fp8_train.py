@@ -55,7 +55,7 @@ def test_quantize_e5m2_strided_rows(dev):
 
 
 @pytest.mark.parametrize("R,C,off", [(1, 1, 0), (64, 64, 0), (63, 65, 0), (1000, 37, 0),
-                                     (4096, 512, 0), (130, 300, 5)])
+                                     (4096, 512, 0), (384, 256, 0), (300, 4096, 16), (130, 300, 5)])
 def test_transpose_u8(dev, R, C, off):
     g = torch.Generator().manual_seed(R * C)
     full = torch.randint(0, 256, (R, C + off), generator=g, dtype=torch.uint8)
