@@ -14,6 +14,8 @@
 // v_and_or per two weights and one v_dot2 per two products. fp32 activations use
 // exact byte->float converts and FMAs. INT8 uses u = q ^ 0x80 = q + 128 bytes.
 // Each lane's partial sums are reduced across the wavefront at the end.
+#include <type_traits>
+
 #include "wq.h"
 
 namespace mls {
@@ -203,6 +205,44 @@ __device__ __forceinline__ float chunk_dot(const uint4 wq, const uint32_t* xr, u
   return acc;
 }
 
+// The 16-bit operand pairs of one weight chunk, as chunk_dot forms them (INT4: 16 dwords
+// of biased nibble pairs in k order (0,4)(1,5)(2,6)(3,7) per 8 k; INT8: 8 dwords of q + 128),
+// for reuse across several rows of x (16-bit activations only).
+template <int WBITS, typename AT>
+struct WPairs {
+  static constexpr int NW = WBITS == 4 ? 16 : 8;
+  uint32_t v[NW];
+};
+
+template <int WBITS, typename AT>
+__device__ __forceinline__ void chunk_widen(const uint4 wq, uint32_t nib_mask, uint32_t magic, WPairs<WBITS, AT>& w) {
+  using H = Half16<AT>;
+  const uint32_t q[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    if constexpr (WBITS == 4) {
+      w.v[4 * b + 0] = and_or(q[b], nib_mask, magic);
+      w.v[4 * b + 1] = and_or(q[b] >> 4, nib_mask, magic);
+      w.v[4 * b + 2] = and_or(q[b] >> 8, nib_mask, magic);
+      w.v[4 * b + 3] = and_or(q[b] >> 12, nib_mask, magic);
+    } else {
+      const uint32_t u = q[b] ^ 0x80808080u;
+      w.v[2 * b + 0] = H::pack2(ub0(u), ub1(u));
+      w.v[2 * b + 1] = H::pack2(ub2(u), ub3(u));
+    }
+  }
+}
+
+// the same sum as chunk_dot, from widened pairs
+template <int WBITS, typename AT>
+__device__ __forceinline__ float pairs_dot(const WPairs<WBITS, AT>& w, const uint32_t* xr) {
+  using H = Half16<AT>;
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < WPairs<WBITS, AT>::NW; ++i) acc = H::dot2(w.v[i], xr[i], acc);
+  return acc;
+}
+
 template <int WBITS, typename AT>
 constexpr float code_offset() {
   if constexpr (WBITS == 8) return 128.0f;
@@ -355,16 +395,17 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x70 | 0xF00);
 }
 
-template <int WBITS, typename AT, typename ST, int CPL, int R, int XI, int SI>
+template <int WBITS, typename AT, typename ST, int CPL, int R, int XI, int SI, int MX>
 __global__ __launch_bounds__(256) void gemv1_kernel(const AT* __restrict__ x, const uint8_t* __restrict__ w,
                                                     int ldw, int w_bytes, const ST* __restrict__ s, int s_row_bytes,
                                                     int s_bytes, int group, AT* __restrict__ y, int N, int K,
-                                                    int s_dw) {
+                                                    int s_dw, int lda_b, int M, int ldy) {
   using S = XSlot<WBITS, AT>;
   constexpr int KC = S::KC, NV = S::NV;
   constexpr float OFF = code_offset<WBITS, AT>();
   constexpr int S_SLICE = 64 * SI;  // scale dwords per wavefront slice
-  __shared__ __attribute__((aligned(16))) uint8_t smem[XI * 4096 + (WBITS == 4 ? 4 * S_SLICE * 4 : 16)];
+  constexpr int XB = XI * 4096;     // LDS bytes per row of x
+  __shared__ __attribute__((aligned(16))) uint8_t smem[MX * XB + (WBITS == 4 ? 4 * S_SLICE * 4 : 16)];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nchunks = K / KC;
@@ -376,10 +417,18 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const AT* __restrict__ x, co
   //    per operand from the kernel arguments, row offsets in SGPRs, no per-lane clamps):
   //    each one delays the weight stream. XI instructions per wavefront cover XI * 4 KiB
   //    >= 2K bytes; those past x read zeros into LDS padding.
-  const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc((void*)x, (short)0, K * (int)sizeof(AT), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)x, (short)0, (MX == 1 ? 0 : (M - 1) * lda_b) + K * (int)sizeof(AT), 0x00020000);
 #pragma unroll
-  for (int i = 0; i < XI; ++i) lds_direct16(rsx, smem + wave * 1024 + i * 4096, lane * 16, wave * 1024 + i * 4096);
-  uint8_t* sl = smem + XI * 4096 + wave * (S_SLICE * 4);
+  for (int mi = 0; mi < MX; ++mi) {
+    // rows past M repeat row M - 1 (computed, never stored); bytes past a row's K are
+    // the next row's or zeros, and feed only chunks past K, whose terms are dropped
+    const int xo = MX == 1 ? 0 : min(mi, M - 1) * lda_b;
+#pragma unroll
+    for (int i = 0; i < XI; ++i)
+      lds_direct16(rsx, smem + mi * XB + wave * 1024 + i * 4096, lane * 16, xo + wave * 1024 + i * 4096);
+  }
+  uint8_t* sl = smem + MX * XB + wave * (S_SLICE * 4);
   float srow[R];
   if constexpr (WBITS == 4) {
     // slice = the R rows' s_dw scale dwords back to back (rows past N read zeros); lane q of
@@ -424,61 +473,147 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const AT* __restrict__ x, co
 #pragma unroll
       for (int j = 0; j < CPL; ++j) sc[r][j] = to_f32(st[min(r * P + ((lane + 64 * j) * KC) / group, S_SLICE * 4 / (int)sizeof(ST) - 1)]);
   }
-  XRaw<WBITS, AT> xraw[CPL];
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const uint4* xl = reinterpret_cast<const uint4*>(smem + (lane + 64 * j) * KC * (int)sizeof(AT));
-#pragma unroll
-    for (int q = 0; q < XRaw<WBITS, AT>::XQ; ++q) xraw[j].v[q] = xl[q];
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // 4. dot products (as gemv_wq_kernel); a chunk past K adds nothing (its scale may be
-  //    any bits, so the whole term is dropped, not multiplied by zero)
-  uint32_t xr[CPL][NV];
-  float osx[CPL];
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) osx[j] = OFF * x_from_raw<WBITS, AT>(xraw[j], xr[j]);
-  uint32_t nib_mask = 0x000F000Fu, magic = 0;
-  if constexpr (WBITS == 4) magic = Half16<AT>::MAGIC4;
-  asm volatile("" : "+v"(nib_mask), "+v"(magic));
-  float part[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) {
-    float acc = 0.0f;
+  if constexpr (MX == 1) {
+    // one row of x (the M = 1 GEMV)
+    XRaw<WBITS, AT> xraw[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const float d = chunk_dot<WBITS, AT>(wv[r][j], xr[j], nib_mask, magic) - osx[j];
-      const float t = WBITS == 4 ? fmaf(sc[r][j], d, acc) : acc + d;
-      acc = (64 * (j + 1) > nchunks && lane + 64 * j >= nchunks) ? acc : t;
+      const uint4* xl = reinterpret_cast<const uint4*>(smem + (lane + 64 * j) * KC * (int)sizeof(AT));
+#pragma unroll
+      for (int q = 0; q < XRaw<WBITS, AT>::XQ; ++q) xraw[j].v[q] = xl[q];
     }
-    part[r] = acc;
-  }
+    __builtin_amdgcn_sched_barrier(0);
 
-  // 5. wave totals by DPP; lane 63 holds every row's and writes them
+    // 4. dot products (as gemv_wq_kernel); a chunk past K adds nothing (its scale may be
+    //    any bits, so the whole term is dropped, not multiplied by zero)
+    uint32_t xr[CPL][NV];
+    float osx[CPL];
 #pragma unroll
-  for (int r = 0; r < R; ++r) part[r] = wave_total_dpp(part[r]);
-  const int rows = min(R, N - n0);
-  if (lane == 63 && rows > 0) {
-    float v[R];
+    for (int j = 0; j < CPL; ++j) osx[j] = OFF * x_from_raw<WBITS, AT>(xraw[j], xr[j]);
+    uint32_t nib_mask = 0x000F000Fu, magic = 0;
+    if constexpr (WBITS == 4) magic = Half16<AT>::MAGIC4;
+    asm volatile("" : "+v"(nib_mask), "+v"(magic));
+    float part[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) v[r] = WBITS == 8 ? part[r] * srow[r] : part[r];
-    AT* dst = y + n0;
-    if constexpr (R == 4) {
-      if (rows == 4 && ((uintptr_t)dst & 7) == 0) {
-        *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_bits(from_f32<AT>(v[0]), from_f32<AT>(v[1])),
-                                                    pack2_bits(from_f32<AT>(v[2]), from_f32<AT>(v[3])));
-        return;
+    for (int r = 0; r < R; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const float d = chunk_dot<WBITS, AT>(wv[r][j], xr[j], nib_mask, magic) - osx[j];
+        const float t = WBITS == 4 ? fmaf(sc[r][j], d, acc) : acc + d;
+        acc = (64 * (j + 1) > nchunks && lane + 64 * j >= nchunks) ? acc : t;
       }
-    } else if constexpr (R == 2) {
-      if (rows == 2 && ((uintptr_t)dst & 3) == 0) {
-        *reinterpret_cast<uint32_t*>(dst) = pack2_bits(from_f32<AT>(v[0]), from_f32<AT>(v[1]));
-        return;
-      }
+      part[r] = acc;
     }
+
+    // 5. wave totals by DPP; lane 63 holds every row's and writes them
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (r < rows) dst[r] = from_f32<AT>(v[r]);
+    for (int r = 0; r < R; ++r) part[r] = wave_total_dpp(part[r]);
+    const int rows = min(R, N - n0);
+    if (lane == 63 && rows > 0) {
+      float v[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[r] = WBITS == 8 ? part[r] * srow[r] : part[r];
+      AT* dst = y + n0;
+      if constexpr (R == 4) {
+        if (rows == 4 && ((uintptr_t)dst & 7) == 0) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_bits(from_f32<AT>(v[0]), from_f32<AT>(v[1])),
+                                                      pack2_bits(from_f32<AT>(v[2]), from_f32<AT>(v[3])));
+          return;
+        }
+      } else if constexpr (R == 2) {
+        if (rows == 2 && ((uintptr_t)dst & 3) == 0) {
+          *reinterpret_cast<uint32_t*>(dst) = pack2_bits(from_f32<AT>(v[0]), from_f32<AT>(v[1]));
+          return;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (r < rows) dst[r] = from_f32<AT>(v[r]);
+    }
+  } else {
+    // MX rows of x: each weight chunk is widened once and dotted with every row
+    XRaw<WBITS, AT> xraw[MX][CPL];
+#pragma unroll
+    for (int mi = 0; mi < MX; ++mi)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const uint4* xl = reinterpret_cast<const uint4*>(smem + mi * XB + (lane + 64 * j) * KC * (int)sizeof(AT));
+#pragma unroll
+        for (int q = 0; q < XRaw<WBITS, AT>::XQ; ++q) xraw[mi][j].v[q] = xl[q];
+      }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 4. dot products (as gemv_wq_kernel); a chunk past K adds nothing (its scale may be
+    //    any bits, so the whole term is dropped, not multiplied by zero)
+    uint32_t xr[MX][CPL][NV];
+    float osx[MX][CPL];
+#pragma unroll
+    for (int mi = 0; mi < MX; ++mi)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) osx[mi][j] = OFF * x_from_raw<WBITS, AT>(xraw[mi][j], xr[mi][j]);
+    uint32_t nib_mask = 0x000F000Fu, magic = 0;
+    if constexpr (WBITS == 4) magic = Half16<AT>::MAGIC4;
+    asm volatile("" : "+v"(nib_mask), "+v"(magic));
+    float part[MX][R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float acc[MX];
+#pragma unroll
+      for (int mi = 0; mi < MX; ++mi) acc[mi] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const bool past_k = 64 * (j + 1) > nchunks && lane + 64 * j >= nchunks;
+        if constexpr (MX == 1) {
+          const float d = chunk_dot<WBITS, AT>(wv[r][j], xr[0][j], nib_mask, magic) - osx[0][j];
+          const float t = WBITS == 4 ? fmaf(sc[r][j], d, acc[0]) : acc[0] + d;
+          acc[0] = past_k ? acc[0] : t;
+        } else {
+          // several rows of x: the chunk is widened once and dotted with each row
+          WPairs<WBITS, AT> wp;
+          chunk_widen<WBITS, AT>(wv[r][j], nib_mask, magic, wp);
+#pragma unroll
+          for (int mi = 0; mi < MX; ++mi) {
+            const float d = pairs_dot<WBITS, AT>(wp, xr[mi][j]) - osx[mi][j];
+            const float t = WBITS == 4 ? fmaf(sc[r][j], d, acc[mi]) : acc[mi] + d;
+            acc[mi] = past_k ? acc[mi] : t;
+          }
+        }
+      }
+#pragma unroll
+      for (int mi = 0; mi < MX; ++mi) part[mi][r] = acc[mi];
+    }
+
+    // 5. wave totals by DPP; lane 63 holds every row's and writes them
+#pragma unroll
+    for (int mi = 0; mi < MX; ++mi)
+#pragma unroll
+      for (int r = 0; r < R; ++r) part[mi][r] = wave_total_dpp(part[mi][r]);
+    const int rows = min(R, N - n0);
+    if (lane != 63 || rows <= 0) return;
+#pragma unroll
+    for (int mi = 0; mi < MX; ++mi) {
+      if (MX > 1 && mi >= M) break;  // (a row of x past M: never stored)
+      float v[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[r] = WBITS == 8 ? part[mi][r] * srow[r] : part[mi][r];
+      AT* dst = y + (int64_t)mi * ldy + n0;
+      if constexpr (R == 4) {
+        if (rows == 4 && ((uintptr_t)dst & 7) == 0) {
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_bits(from_f32<AT>(v[0]), from_f32<AT>(v[1])),
+                                                      pack2_bits(from_f32<AT>(v[2]), from_f32<AT>(v[3])));
+          continue;
+        }
+      } else if constexpr (R == 2) {
+        if (rows == 2 && ((uintptr_t)dst & 3) == 0) {
+          *reinterpret_cast<uint32_t*>(dst) = pack2_bits(from_f32<AT>(v[0]), from_f32<AT>(v[1]));
+          continue;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (r < rows) dst[r] = from_f32<AT>(v[r]);
+    }
   }
 }
 
@@ -491,10 +626,24 @@ static int launch_gemv1_si(const WqArgs& p, int s_dw) {
   if (p.K * 2 > XI * 4096) return MLS_ERR_UNSUPPORTED;
   const int s_row_bytes = (int)(p.ld_sn * (int64_t)sizeof(ST));
   const int s_bytes = WBITS == 4 ? (int)(p.N * p.ld_sn * (int64_t)sizeof(ST)) : 0;
-  hipLaunchKernelGGL((gemv1_kernel<WBITS, AT, ST, CPL, R, XI, SI>), dim3((unsigned)cdiv(p.N, 4 * R)), dim3(256), 0,
-                     p.stream, (const AT*)p.a, p.w, (int)p.ldw, (int)(p.N * p.ldw), (const ST*)p.s, s_row_bytes,
-                     s_bytes, p.group, (AT*)p.c, (int)p.N, (int)p.K, s_dw);
-  return MLS_OK;
+  // rows of x: 1 or 2 (3 and 4 rows measured slower than the MFMA skinny kernel: the dot
+  // products grow with M while the widening is shared); x of both rows in LDS within 32 KiB
+  if (p.M > 2) return MLS_ERR_UNSUPPORTED;
+  const int mx = (int)p.M;
+  const int64_t lda_b = p.lda * (int64_t)sizeof(AT);
+  if (mx > 1 && (mx * XI > 8 || (p.M - 1) * lda_b + p.K * (int64_t)sizeof(AT) > 0x7FFFFFFF))
+    return MLS_ERR_UNSUPPORTED;
+  auto go = [&](auto mxc) {
+    constexpr int MX = decltype(mxc)::value;
+    hipLaunchKernelGGL((gemv1_kernel<WBITS, AT, ST, CPL, R, XI, SI, MX>), dim3((unsigned)cdiv(p.N, 4 * R)), dim3(256),
+                       0, p.stream, (const AT*)p.a, p.w, (int)p.ldw, (int)(p.N * p.ldw), (const ST*)p.s, s_row_bytes,
+                       s_bytes, p.group, (AT*)p.c, (int)p.N, (int)p.K, s_dw, (int)(mx > 1 ? lda_b : 0), (int)p.M,
+                       (int)(mx > 1 ? p.ldc : 0));
+    return MLS_OK;
+  };
+  if (mx == 1) return go(std::integral_constant<int, 1>{});
+  if constexpr (XI <= 4) return go(std::integral_constant<int, 2>{});
+  return MLS_ERR_UNSUPPORTED;
 }
 
 template <int WBITS, typename AT, typename ST, int CPL>
@@ -531,11 +680,12 @@ static int launch_gemv1_st(const WqArgs& p) {
   return MLS_ERR_UNSUPPORTED;
 }
 
-// M = 1 with 16-bit activations; MLS_ERR_UNSUPPORTED sends the call to gemv_wq_kernel.
-// MLS_GEMV1=0 disables this path (A/B sweeps).
+// M = 1 (and, through launch_gemv_rows, M = 2) with 16-bit activations;
+// MLS_ERR_UNSUPPORTED sends the call to gemv_wq_kernel. MLS_GEMV1=0 disables this path
+// (A/B sweeps).
 static int launch_gemv1(int wbits, const WqArgs& p) {
   static const int enabled = env_int("MLS_GEMV1", 1);
-  if (!enabled || p.M != 1 || p.a_dt == MLS_F32) return MLS_ERR_UNSUPPORTED;
+  if (!enabled || p.M < 1 || p.M > 2 || p.a_dt == MLS_F32) return MLS_ERR_UNSUPPORTED;
   // x in LDS (at most 32 KiB); 32-bit buffer offsets into the whole weight matrix
   if (p.K * 2 > 32768 || (p.N + 4) * p.ldw >= (1ll << 31)) return MLS_ERR_UNSUPPORTED;
   if (wbits == 4) {
@@ -630,7 +780,7 @@ int launch_gemv_wq(int wbits, const WqArgs& p) {
   if (!aligned(p.w, 16) || p.ldw % 16 != 0) return MLS_ERR_UNSUPPORTED;
   if (!aligned(p.a, 16) || (p.lda * esz) % 16 != 0) return MLS_ERR_UNSUPPORTED;
   if (p.N > 0x7FFFFFFF / 2 || p.M > 4 * 65535) return MLS_ERR_UNSUPPORTED;  // grid.y = M / MT
-  const int rc = launch_gemv1(wbits, p);
+  const int rc = p.M == 1 ? launch_gemv1(wbits, p) : MLS_ERR_UNSUPPORTED;
   if (rc != MLS_ERR_UNSUPPORTED) return rc;
   if (wbits == 4) {
     if (p.a_dt == MLS_F32) return dispatch_st<4, float>(p);
@@ -640,6 +790,17 @@ int launch_gemv_wq(int wbits, const WqArgs& p) {
   if (p.a_dt == MLS_F32) return dispatch_st<8, float>(p);
   if (p.a_dt == MLS_F16) return dispatch_st<8, _Float16>(p);
   return dispatch_st<8, __bf16>(p);
+}
+
+// M = 2 on the M = 1 kernel's layout (every weight chunk widened once, dotted with
+// each row of x); MLS_ERR_UNSUPPORTED when the shape or alignment does not fit it.
+int launch_gemv_rows(int wbits, const WqArgs& p) {
+  const int KC = wbits == 4 ? 32 : 16;
+  if (p.M != 2 || p.a_dt == MLS_F32 || p.K % KC != 0) return MLS_ERR_UNSUPPORTED;
+  if (wbits == 4 && (p.group % KC != 0)) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(p.w, 16) || p.ldw % 16 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(p.a, 16) || (p.lda * 2) % 16 != 0 || p.N > 0x7FFFFFFF / 2) return MLS_ERR_UNSUPPORTED;
+  return launch_gemv1(wbits, p);
 }
 
 // ------------------------------------------------------------------ generic path

@@ -26,6 +26,10 @@ struct WqArgs {
 // when the shape or alignment is outside its fast path.
 int launch_gemv_wq(int wbits, const WqArgs& p);
 
+// M = 2 with 16-bit activations on the M = 1 GEMV's layout (x of both rows in LDS, each
+// weight chunk widened once for both). MLS_ERR_UNSUPPORTED outside its fast path.
+int launch_gemv_rows(int wbits, const WqArgs& p);
+
 // MFMA skinny GEMM for M <= 16 and 16-bit activations (weights read once for all M).
 // MLS_ERR_UNSUPPORTED outside its fast path.
 int launch_gemv_mfma(int wbits, const WqArgs& p);
