@@ -22,7 +22,8 @@ rule (its accumulation truncates); its rows are timed and marked
 within_config_tolerance = false.
 
 The other BASELINE configs (INT4 M = 4 / 16, the INT8 GEMV target, INT8 prefill,
-FP8 e4m3 GEMM, INT4 MoE grouped GEMM), the whole INT4 SwiGLU expert MLP of a
+FP8 e4m3 GEMM, INT4 MoE grouped GEMM), INT4 and INT8 at M = 2 (a speculative
+decoding verify step with one draft token), the whole INT4 SwiGLU expert MLP of a
 routed MoE layer, FP8Linear's backward at config D's shape, paged-attention
 decode, the load-time INT4 quantizer and the reference's own published
 bench_quantize shapes (N = K = 2048, fp16, M in {1, 16, 128}) are reported under
@@ -813,9 +814,11 @@ def main(argv=None) -> int:
     small = max(8, args.steps // 8)
     runners = {
         "int4_gemv": lambda: _hbm_row("int4_gemv_m1", int4_gemv(dev, 1, args.steps, args.warmup)),
+        "int4_m2": lambda: _hbm_row("int4_gemv_m2", int4_gemv(dev, 2, args.steps, args.warmup)),
         "int4_m4": lambda: _hbm_row("int4_gemv_m4", int4_gemv(dev, 4, args.steps, args.warmup)),
         "int4_m16": lambda: _hbm_row("int4_gemv_m16", int4_gemv(dev, 16, args.steps, args.warmup)),
         "int8_gemv": lambda: _hbm_row("int8_gemv_m1", int8_gemv(dev, 1, args.steps, args.warmup)),
+        "int8_m2": lambda: _hbm_row("int8_gemv_m2", int8_gemv(dev, 2, args.steps, args.warmup)),
         "int8_prefill": lambda: _mfma_row("int8_prefill_2048x11008x4096",
                                           int8_prefill(dev, small, 4), BF16_PEAK_TFLOPS),
         "int8_dgrad": lambda: _mfma_row("int8_dgrad_4096x11008x4096_bf16", int8_dgrad_row(dev, small, 4),
@@ -882,7 +885,7 @@ def main(argv=None) -> int:
         return 1
     extra = []
     if not args.no_extra:
-        for k in ("int4_m4", "int4_m16", "int8_gemv", "int8_prefill", "int8_dgrad", "fp8_gemm", "fp8_native",
+        for k in ("int4_m2", "int4_m4", "int4_m16", "int8_gemv", "int8_m2", "int8_prefill", "int8_dgrad", "fp8_gemm", "fp8_native",
                   "fp8_bwd", "fp8_bwd_native", "moe_int4", "moe_mlp_int4", "paged_attn", "quantize_int4",
                   "ref_shapes", "copy", "floor", "vendor_fp8_rowwise", "vendor_fp8_tensorwise", "vendor_bf16"):
             log(f"{k} ...")
