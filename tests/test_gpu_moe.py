@@ -63,6 +63,23 @@ def test_grouped_group_sizes(dev, gs, dtype):
     assert ok, f"worst {worst:.3g}"
 
 
+@pytest.mark.parametrize("K,gs", [(8192, 128), (14336, 128), (4096, 64)])
+def test_grouped_many_groups(dev, K, gs):
+    """More than 32 groups per row: the 128-group scale table (64 and 112 groups; the
+    expert MLP's unsplit down projection at H = 14336)."""
+    counts = [40, 0, 130, 7]
+    E, N = len(counts), 256
+    P, S = _experts(dev, E, N, K, gs, K + gs)
+    M = sum(counts)
+    g = torch.Generator().manual_seed(K)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    out = int4_grouped_matmul(a.to(dev), P, S, torch.tensor(counts, device=dev), gs)
+    off = np.concatenate([[0], np.cumsum(counts)])
+    want = ref.grouped_int4_matmul(a.float().numpy(), P.cpu().numpy(), S.float().cpu().numpy(), off, gs)
+    ok, worst = ref.close_bf16(out.float().cpu().numpy(), want)
+    assert ok, f"K={K} gs={gs}: worst {worst:.3g}"
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_grouped_fused_gather(dev, dtype):
     """a_rows: the dispatch gather inside the activation load gives the same bits as the
