@@ -564,20 +564,13 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const AT* __restrict__ x, co
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
         const bool past_k = 64 * (j + 1) > nchunks && lane + 64 * j >= nchunks;
-        if constexpr (MX == 1) {
-          const float d = chunk_dot<WBITS, AT>(wv[r][j], xr[0][j], nib_mask, magic) - osx[0][j];
-          const float t = WBITS == 4 ? fmaf(sc[r][j], d, acc[0]) : acc[0] + d;
-          acc[0] = past_k ? acc[0] : t;
-        } else {
-          // several rows of x: the chunk is widened once and dotted with each row
-          WPairs<WBITS, AT> wp;
-          chunk_widen<WBITS, AT>(wv[r][j], nib_mask, magic, wp);
+        WPairs<WBITS, AT> wp;
+        chunk_widen<WBITS, AT>(wv[r][j], nib_mask, magic, wp);
 #pragma unroll
-          for (int mi = 0; mi < MX; ++mi) {
-            const float d = pairs_dot<WBITS, AT>(wp, xr[mi][j]) - osx[mi][j];
-            const float t = WBITS == 4 ? fmaf(sc[r][j], d, acc[mi]) : acc[mi] + d;
-            acc[mi] = past_k ? acc[mi] : t;
-          }
+        for (int mi = 0; mi < MX; ++mi) {
+          const float d = pairs_dot<WBITS, AT>(wp, xr[mi][j]) - osx[mi][j];
+          const float t = WBITS == 4 ? fmaf(sc[r][j], d, acc[mi]) : acc[mi] + d;
+          acc[mi] = past_k ? acc[mi] : t;
         }
       }
 #pragma unroll
@@ -593,7 +586,7 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const AT* __restrict__ x, co
     if (lane != 63 || rows <= 0) return;
 #pragma unroll
     for (int mi = 0; mi < MX; ++mi) {
-      if (MX > 1 && mi >= M) break;  // (a row of x past M: never stored)
+      if (mi >= M) break;  // (a row of x past M: never stored)
       float v[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) v[r] = WBITS == 8 ? part[mi][r] * srow[r] : part[mi][r];
