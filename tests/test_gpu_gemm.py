@@ -94,6 +94,65 @@ def test_config_b_int4_gemv(dev, M):
     _check(out, want, f"config B M={M}")
 
 
+@pytest.mark.parametrize("bits,N,K,dtype,sdt,pad", [
+    (4, 1000, 4096, torch.bfloat16, torch.float16, 64),   # ragged N, x rows 64 elements apart
+    (4, 4096, 2048, torch.float16, torch.float32, 0),     # fp16 x, fp32 scales
+    (4, 512, 8192, torch.bfloat16, torch.float16, 0),     # 4 chunks per lane
+    (4, 256, 16384, torch.bfloat16, torch.float16, 0),    # x too long for LDS: skinny kernel
+    (8, 4095, 4096, torch.bfloat16, torch.float16, 128),  # INT8, ragged N, strided x
+    (8, 2048, 8192, torch.float16, torch.float32, 0),     # INT8, 8 chunks per lane
+])
+def test_gemv_two_rows(dev, bits, N, K, dtype, sdt, pad):
+    """M = 2 on the M = 1 GEMV's layout: both rows of x in LDS (row stride from the view),
+    each weight chunk widened once for both rows; shapes it does not take fall back."""
+    a, w = _data(2, N, K + pad, 300 + bits + N, 0.02)
+    a = a.to(dtype)
+    ax = a.to(dev)[:, :K] if pad else a.to(dev)
+    w = w[:, :K].contiguous()
+    if bits == 4:
+        p, s = quantize_int4(w.to(dev), 128)
+        s = s.to(sdt)
+        out = int4_matmul(ax, p, s, 128)
+        want = ref.int4_matmul(a[:, :K].float().numpy(), p.cpu().numpy(), s.float().cpu().numpy(), 128)
+    else:
+        q, s = quantize_int8(w.to(dev))
+        s = s.to(sdt)
+        out = int8_matmul(ax, q, s)
+        want = ref.int8_matmul(a[:, :K].float().numpy(), q.cpu().numpy(), s.float().cpu().numpy())
+    assert out.dtype == dtype and out.shape == (2, N)
+    _check(out, want, f"two rows int{bits} N={N} K={K}")
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_gemv_two_rows_output_stride(dev, bits):
+    """M = 2 through the C ABI into a wider output buffer: row 1 lands ldc elements after
+    row 0, and the columns past N stay untouched."""
+    import kernels
+    from kernels._hip import stream
+    M, N, K, pad = 2, 1000, 4096, 40
+    a, w = _data(M, N, K, 400 + bits, 0.02)
+    ab = a.to(torch.bfloat16).to(dev)
+    c = torch.full((M, N + pad), 7.0, dtype=torch.bfloat16, device=dev)
+    L = kernels.lib()
+    if bits == 4:
+        p, s = quantize_int4(w.to(dev), 128)
+        s = s.to(torch.float16).contiguous()
+        rc = L.mls_int4_gemm(ab.data_ptr(), kernels.MLS_BF16, K, p.data_ptr(), p.stride(0), s.data_ptr(),
+                             kernels.MLS_F16, s.stride(0), 1, 128, c.data_ptr(), kernels.MLS_BF16, N + pad,
+                             M, N, K, stream(dev))
+        want = ref.int4_matmul(ab.float().cpu().numpy(), p.cpu().numpy(), s.float().cpu().numpy(), 128)
+    else:
+        q, s = quantize_int8(w.to(dev))
+        s = s.to(torch.float16).contiguous()
+        rc = L.mls_int8_gemm(ab.data_ptr(), kernels.MLS_BF16, K, q.data_ptr(), q.stride(0), s.data_ptr(),
+                             kernels.MLS_F16, c.data_ptr(), kernels.MLS_BF16, N + pad, M, N, K, stream(dev))
+        want = ref.int8_matmul(ab.float().cpu().numpy(), q.cpu().numpy(), s.float().cpu().numpy())
+    torch.cuda.synchronize(dev)
+    assert rc == 0
+    _check(c[:, :N], want, f"two rows int{bits}, ldc = N + {pad}")
+    assert torch.all(c[:, N:] == 7.0)
+
+
 @pytest.mark.parametrize("M", [1, 4, 16])
 def test_int8_gemv_target(dev, M):
     """North-star INT8 GEMV: M=1, K = N = 4096, bf16 x, fp16 per-row scales."""
