@@ -69,6 +69,15 @@ def test_mfma_paths(dev, M, N, K, out_dtype, native):
     _check(out, ref.fp8_matmul(ab.numpy(), bb.numpy(), sa, sb), f"fp8 {M}x{N}x{K} native={native}")
 
 
+def test_exact_partial_tile_run(dev):
+    """The exact e4m3 kernel on 256-row tiles with 11 row tiles: in the tile order, runs of
+    4, 4 and 3 row tiles sweep the column tiles."""
+    M, N, K = 2800, 8192, 256
+    ab, bb, sa, sb = _operands(M, N, K, 11, per_row=False)
+    out = fp8_matmul(ab.to(dev), bb.to(dev), sa, sb, out_dtype=torch.float32)
+    _check(out, ref.fp8_matmul(ab.numpy(), bb.numpy(), sa, sb), f"fp8 {M}x{N}x{K} exact")
+
+
 @pytest.mark.parametrize("M,N,K", [(64, 96, 128), (300, 200, 384), (5, 7, 48)])
 def test_per_row_scales_with_outliers(dev, M, N, K):
     ab, bb, sa, sb = _operands(M, N, K, 3 * M + N, per_row=True, outliers=True)

@@ -336,6 +336,7 @@ def test_mfma_int8(dev, M, N, K, dtype):
 @pytest.mark.parametrize("M,N,K", [
     (1000, 11000, 512),   # 256 x 192 tiles, M and N ragged
     (4000, 4000, 256),    # 256 x 256 tiles (two rounds of 192-wide ones would be slower), ragged
+    (2800, 8192, 256),    # 11 row tiles: runs of 4, 4 and 3 in the tile order
 ])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_mfma_int8_256_row_tiles(dev, M, N, K, dtype):
