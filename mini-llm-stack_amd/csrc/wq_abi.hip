@@ -58,8 +58,8 @@ int run(const char* fn, int wbits, const WqArgs& p) {
     if (rc != MLS_ERR_UNSUPPORTED) {
     } else if (small_m) {
       // M = 2 on the M = 1 GEMV's layout (INT4 -4%, INT8 -18% against the MFMA skinny kernel
-      // at K = N = 4096); MLS_GEMV_ROWS_X=0 keeps M = 2 on the skinny kernel (A/B sweeps)
-      static const bool rows_env = env_int("MLS_GEMV_ROWS_X", 1) != 0;
+      // at K = N = 4096); MLS_GEMV_M2=0 keeps M = 2 on the skinny kernel (A/B sweeps)
+      static const bool rows_env = env_int("MLS_GEMV_M2", 1) != 0;
       if (rows_env && p.M == 2) rc = launch_gemv_rows(wbits, p);
       if (rc == MLS_ERR_UNSUPPORTED && p.M >= 2 && p.a_dt != MLS_F32) rc = launch_gemv_mfma(wbits, p);
       if (rc == MLS_ERR_UNSUPPORTED) rc = launch_gemv_wq(wbits, p);
