@@ -804,8 +804,7 @@ def main(argv=None) -> int:
     EAGER = args.eager
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build runs on a single MI355X and has no "
-              "multi-GPU path (see DESIGN.md for how the path would shard); use --gpus 1",
-              file=sys.stderr)
+              "multi-GPU path; use --gpus 1", file=sys.stderr)
         return 2
 
     import torch
