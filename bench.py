@@ -6,10 +6,13 @@ Headline: INT4 g128 decode GEMV, M = 1, K = N = 4096,
 bf16 activations, fp16 group scales, bf16 output. A step is one launch over one
 batch; consecutive steps read distinct copies of the packed weights (>= 1 GiB of
 copies in total), so the 256 MB Infinity Cache cannot serve them and the data
-really streams from HBM. The W warmup steps and the K timed steps are each one
-HIP graph of back-to-back launches, replayed on the launching stream between
-HIP events; the timed steps start at the copy after the last warmup one, so no
-timed step re-reads what warmup just read. value = algorithmic bytes x K / elapsed.
+really streams from HBM. The W warmup steps and the K timed steps are captured
+back to back as one HIP graph, with a one-thread kernel that reads the GPU's
+constant-rate realtime counter just before and just after the K timed steps; the
+graph is replayed once and the elapsed time is the counter difference, so the
+graph's own launch cost (~11.6 us per replay) stays outside it. The timed steps
+start at the copy after the last warmup one, so no timed step re-reads what
+warmup just read. value = algorithmic bytes x K / elapsed.
 
 Parity gate (the reference refuses to benchmark when an on-device check fails,
 kaggle/kaggle_bench.py:46-54): before a workload is timed, one of its outputs is
@@ -73,10 +76,33 @@ def log(msg: str) -> None:
 EAGER = False  # --eager: plain launches instead of graph replay (for counter collection)
 
 
+_FLOOR_LIB = None
+
+
+def _floor_lib():
+    """libmls_floor.so: bench.py's calibration kernels (csrc/floor.hip), not the product."""
+    global _FLOOR_LIB
+    if _FLOOR_LIB is None:
+        import ctypes
+        lib = ctypes.CDLL(str(ROOT / "mini-llm-stack_amd" / "libmls_floor.so"))
+        lib.mlsf_stamp.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        lib.mlsf_wallclock_khz.argtypes = [ctypes.POINTER(ctypes.c_int)]
+        _FLOOR_LIB = lib
+    return _FLOOR_LIB
+
+
 def time_steps(fns, warmup: int, steps: int) -> float:
     """ms per step: `warmup` then `steps` launches, fns[i % len(fns)] for step i
-    (the timed steps continue the rotation where warmup stopped), each batch
-    captured as one HIP graph and replayed between events."""
+    (the timed steps continue the rotation where warmup stopped).
+
+    The warmup and timed steps are captured as one HIP graph with a timestamp kernel
+    (the GPU's constant-rate realtime counter, libmls_floor.so's mlsf_stamp) before and
+    after the timed steps, and replayed once; the interval between the stamps holds
+    exactly the timed steps (plus one one-thread launch, ~1.5 us). Timing the replay
+    with events instead would add the graph's own launch cost, ~11.6 us per replay on
+    the GPU (the headline GEMV: 3.68 + 11.6 / K us per step), 0.6 us per step at K = 20.
+    Events around the whole replay check the stamps."""
+    import ctypes
     import torch
     n = len(fns)
     for f in fns:  # first calls: library load, LDS attributes, output pools
@@ -94,25 +120,34 @@ def time_steps(fns, warmup: int, steps: int) -> float:
         torch.cuda.synchronize()
         return start.elapsed_time(end) / steps
 
-    def capture(first, count):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for i in range(count):
-                fns[(first + i) % n]()
-        return g
-
-    gw = capture(0, warmup) if warmup > 0 else None
-    gt = capture(warmup, steps)
-    torch.cuda.synchronize()
-    if gw is not None:
-        gw.replay()
+    lib = _floor_lib()
+    khz = ctypes.c_int(0)
+    if lib.mlsf_wallclock_khz(ctypes.byref(khz)) != 0 or khz.value <= 0:
+        raise RuntimeError("bench: cannot read the GPU's realtime counter rate")
+    stamps = torch.zeros(2, dtype=torch.int64, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(warmup):
+            fns[i % n]()
+        if lib.mlsf_stamp(ctypes.c_void_p(stamps.data_ptr()), ctypes.c_void_p(st)) != 0:
+            raise RuntimeError("bench: timestamp launch failed")
+        for i in range(steps):
+            fns[(warmup + i) % n]()
+        if lib.mlsf_stamp(ctypes.c_void_p(stamps.data_ptr() + 8), ctypes.c_void_p(st)) != 0:
+            raise RuntimeError("bench: timestamp launch failed")
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
-    gt.replay()
+    g.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    t0, t1 = (int(v) for v in stamps.cpu())
+    ms = (t1 - t0) / khz.value
+    whole = start.elapsed_time(end)
+    if not 0 < ms <= whole * 1.001 + 0.01:
+        raise RuntimeError(f"bench: timestamps {ms:.4f} ms outside the replay's {whole:.4f} ms")
+    return ms / steps
 
 
 def wall_median_ms(fn, warmup: int = 3, iters: int = 30) -> float:
