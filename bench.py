@@ -74,6 +74,8 @@ def log(msg: str) -> None:
 # ----------------------------------------------------------------------------- timing
 
 
+EAGER_TOO_MS = 0.05  # steps at least this long are also timed as eager launches
+LAST_EAGER_MS = None  # that time for the last workload timed, ms per step
 STAMP_GAPS = 5  # stamp-to-stamp gaps measured per timing, median subtracted
 STAMP_GAP_US: list = []  # the stamp launch cost measured by each graph-timed workload
 EAGER = False  # --eager: plain launches instead of graph replay (for counter collection)
@@ -109,10 +111,11 @@ def time_steps(fns, warmup: int, steps: int) -> float:
     Events around the whole replay check the stamps.
 
     The graph is replayed once untimed first, then every copy is read once more (1 GiB
-    or more, so the 256 MB MALL no longer holds what the timed steps read), then timed:
-    a graph's first replay ran every step slower (headline, fresh processes on one box:
-    3.91-3.94 us at K = 20 and 3.78 us at K = 512 on a first replay, 3.64-3.79 and
-    3.65 us on a second), a one-time cost of the runtime, not of the steps."""
+    or more for the GEMVs, so the 256 MB MALL no longer holds what the timed steps
+    read), then timed: the first ~10 ms of work of a fresh process ran this library's
+    kernels slower, whether launched eagerly or as a graph's first replay (headline at
+    K = 20: 3.91-3.94 us against 3.64-3.79 us; INT8 prefill 0.200 against 0.176 ms on
+    one box), while the same launches after that ran at the steady rate either way."""
     import ctypes
     import torch
     n = len(fns)
@@ -170,6 +173,18 @@ def time_steps(fns, warmup: int, steps: int) -> float:
         raise RuntimeError(f"bench: timestamps {raw:.4f} ms (stamp gap {gap / khz.value:.4f} ms) "
                            f"inconsistent with the replay's {whole:.4f} ms")
     STAMP_GAP_US.append(gap / khz.value * 1e3)
+    global LAST_EAGER_MS
+    LAST_EAGER_MS = None
+    if ms / steps >= EAGER_TOO_MS:  # long steps: also the same steps launched one by one
+        for i in range(warmup):
+            fns[i % n]()
+        torch.cuda.synchronize()
+        start.record()
+        for i in range(steps):
+            fns[(warmup + i) % n]()
+        end.record()
+        torch.cuda.synchronize()
+        LAST_EAGER_MS = start.elapsed_time(end) / steps
     return ms / steps
 
 
@@ -791,10 +806,21 @@ def _mfma_row(name, r, peak, extra=None):
                         "frac": round(tf / peak, 4)},
            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "flops_per_step": r["flops"],
            "copies": r["copies"]}
+    _eager_field(row)
     if "parity" in r:
         row["parity"] = r["parity"]
     row.update(extra or {})
     return row
+
+
+def _eager_field(row):
+    """The same steps launched one by one right after the graph timing (events around
+    them): the graph replay does not flatter the long steps; eager launches at the same
+    point give the same time per step."""
+    global LAST_EAGER_MS
+    if LAST_EAGER_MS is not None:
+        row["eager_ms_per_step"] = round(LAST_EAGER_MS, 6)
+        LAST_EAGER_MS = None
 
 
 def _native_row(name, r, extra):
