@@ -788,6 +788,7 @@ def _hbm_row(name, r, extra=None):
            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)},
            "bytes_per_step": r["bytes"], "weight_copies": r["copies"]}
+    _eager_field(row)
     if "parity" in r:
         row["parity"] = r["parity"]
     row.update(extra or {})
