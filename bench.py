@@ -74,6 +74,7 @@ def log(msg: str) -> None:
 # ----------------------------------------------------------------------------- timing
 
 
+WARM_MS = 50.0  # eager launches of each workload's steps ahead of its timed replay, ms
 EAGER_TOO_MS = 0.05  # steps at least this long are also timed as eager launches
 LAST_EAGER_MS = None  # that time for the last workload timed, ms per step
 STAMP_GAPS = 5  # stamp-to-stamp gaps measured per timing, median subtracted
@@ -110,12 +111,15 @@ def time_steps(fns, warmup: int, steps: int) -> float:
     ~11.6 us per replay on the GPU (the headline GEMV: 3.68 + 11.6 / K us per step).
     Events around the whole replay check the stamps.
 
-    The graph is replayed once untimed first, then every copy is read once more (1 GiB
-    or more for the GEMVs, so the 256 MB MALL no longer holds what the timed steps
-    read), then timed: the first ~10 ms of work of a fresh process ran this library's
-    kernels slower, whether launched eagerly or as a graph's first replay (headline at
-    K = 20: 3.91-3.94 us against 3.64-3.79 us; INT8 prefill 0.200 against 0.176 ms on
-    one box), while the same launches after that ran at the steady rate either way."""
+    The graph is replayed once untimed, the steps are launched eagerly for WARM_MS of
+    wall time (many replays queued back to back made later replays of short-step
+    graphs slower: the empty kernel 1.5 -> 4.9 us per launch), then every copy is read
+    once more (1 GiB or more for the GEMVs, so the
+    256 MB MALL no longer holds what the timed steps read), then timed: this library's
+    kernels speed up over the first tens of milliseconds of sustained work, whether
+    launched eagerly or replayed (INT8 prefill launched eagerly on one box: 0.199-0.203
+    ms per step after 4 warmup steps, 0.177 ms after 64, 0.167-0.171 ms after 256), so
+    a short run would time the ramp rather than the kernels."""
     import ctypes
     import torch
     n = len(fns)
@@ -155,6 +159,13 @@ def time_steps(fns, warmup: int, steps: int) -> float:
             fns[(warmup + i) % n]()
         stamp(STAMP_GAPS + 1, st)
     g.replay()  # rehearsal (see above)
+    torch.cuda.synchronize()
+    deadline, i = time.perf_counter() + WARM_MS * 1e-3, 0
+    while time.perf_counter() < deadline:  # sustained work: eager launches, 16 at a time
+        fns[i % n]()
+        i += 1
+        if i % 16 == 0:
+            torch.cuda.synchronize()
     for f in fns:  # every copy once more, so the timed steps' copies have left the MALL
         f()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
