@@ -895,9 +895,12 @@ def main(argv=None) -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="launch steps one by one instead of replaying a HIP graph (profiling)")
+    ap.add_argument("--warm-ms", type=float, default=50.0,
+                    help="eager launches of each workload's steps ahead of its timed replay, ms")
     args = ap.parse_args(argv)
-    global EAGER
+    global EAGER, WARM_MS
     EAGER = args.eager
+    WARM_MS = max(0.0, args.warm_ms)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build runs on a single MI355X and has no "
               "multi-GPU path; use --gpus 1", file=sys.stderr)
@@ -1020,7 +1023,9 @@ def main(argv=None) -> int:
                    "scales": "fp16", "output": "bf16", "bytes_per_step": head["bytes_per_step"],
                    "weight_copies_rotated": head["weight_copies"], "launch": "HIP graph replay",
                    "timing": "realtime stamps in the graph around the K steps, less the median "
-                             "stamp-to-stamp launch gap",
+                             "stamp-to-stamp launch gap, after one untimed replay and warm_ms of "
+                             "eager launches",
+                   "warm_ms": WARM_MS,
                    "stamp_gap_us": round(statistics.median(STAMP_GAP_US), 3) if STAMP_GAP_US else None},
         "parity": head["parity"],
         "roofline": roof,
