@@ -612,7 +612,7 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const AT* __restrict__ x, co
 
 template <int WBITS, typename AT, typename ST, int CPL, int SI>
 static int launch_gemv1_si(const WqArgs& p, int s_dw) {
-  constexpr int R = CPL >= 8 ? 1 : 8 / CPL;
+  constexpr int R2 = CPL >= 8 ? 1 : 8 / CPL;  // rows per wavefront: 8 loads per lane
   // x instructions per wavefront: 4 wavefronts x 1 KiB cover 2K bytes (INT4: K <= 2048 CPL;
   // INT8: K <= 1024 CPL)
   constexpr int XI = WBITS == 4 ? CPL : (CPL >= 2 ? CPL / 2 : 1);
@@ -628,6 +628,9 @@ static int launch_gemv1_si(const WqArgs& p, int s_dw) {
     return MLS_ERR_UNSUPPORTED;
   auto go = [&](auto mxc) {
     constexpr int MX = decltype(mxc)::value;
+    // INT8 with one row of x: half the rows per wavefront, twice the wavefronts (K = 2048:
+    // 2.82 -> 2.72 us; K = 4096 the same; with two rows of x it measured 4% slower)
+    constexpr int R = (WBITS == 8 && MX == 1) ? (CPL >= 4 ? 1 : 4 / CPL) : R2;
     hipLaunchKernelGGL((gemv1_kernel<WBITS, AT, ST, CPL, R, XI, SI, MX>), dim3((unsigned)cdiv(p.N, 4 * R)), dim3(256),
                        0, p.stream, (const AT*)p.a, p.w, (int)p.ldw, (int)(p.N * p.ldw), (const ST*)p.s, s_row_bytes,
                        s_bytes, p.group, (AT*)p.c, (int)p.N, (int)p.K, s_dw, (int)(mx > 1 ? lda_b : 0), (int)p.M,
