@@ -626,19 +626,26 @@ static int launch_gemv1_si(const WqArgs& p, int s_dw) {
   const int64_t lda_b = p.lda * (int64_t)sizeof(AT);
   if (mx > 1 && (mx * XI > 8 || (p.M - 1) * lda_b + p.K * (int64_t)sizeof(AT) > 0x7FFFFFFF))
     return MLS_ERR_UNSUPPORTED;
-  auto go = [&](auto mxc) {
-    constexpr int MX = decltype(mxc)::value;
-    // INT8 with one row of x: half the rows per wavefront, twice the wavefronts (K = 2048:
-    // 2.82 -> 2.72 us; K = 4096 the same; with two rows of x it measured 4% slower)
-    constexpr int R = (WBITS == 8 && MX == 1) ? (CPL >= 4 ? 1 : 4 / CPL) : R2;
+  auto go = [&](auto mxc, auto rc) {
+    constexpr int MX = decltype(mxc)::value, R = decltype(rc)::value;
     hipLaunchKernelGGL((gemv1_kernel<WBITS, AT, ST, CPL, R, XI, SI, MX>), dim3((unsigned)cdiv(p.N, 4 * R)), dim3(256),
                        0, p.stream, (const AT*)p.a, p.w, (int)p.ldw, (int)(p.N * p.ldw), (const ST*)p.s, s_row_bytes,
                        s_bytes, p.group, (AT*)p.c, (int)p.N, (int)p.K, s_dw, (int)(mx > 1 ? lda_b : 0), (int)p.M,
                        (int)(mx > 1 ? p.ldc : 0));
     return MLS_OK;
   };
-  if (mx == 1) return go(std::integral_constant<int, 1>{});
-  if constexpr (XI <= 4) return go(std::integral_constant<int, 2>{});
+  using I1 = std::integral_constant<int, 1>;
+  if (mx == 1) {
+    // INT8 with one row of x: half the rows per wavefront, twice the wavefronts (K = 2048:
+    // 2.82 -> 2.72 us; K = 4096 the same; with two rows of x it measured 4% slower)
+    if constexpr (WBITS == 8) return go(I1{}, std::integral_constant<int, (CPL >= 4 ? 1 : 4 / CPL)>{});
+    // INT4 with K <= 2048 (8 rows per wavefront): 2 rows when 8 would leave CUs without a
+    // block (the reference's bench shape, N = K = 2048 g64: 64 -> 256 blocks, 3.54 -> 2.71 us)
+    if constexpr (WBITS == 4 && CPL == 1)
+      if (p.N < 4 * R2 * 256) return go(I1{}, std::integral_constant<int, 2>{});
+    return go(I1{}, std::integral_constant<int, R2>{});
+  }
+  if constexpr (XI <= 4) return go(std::integral_constant<int, 2>{}, std::integral_constant<int, R2>{});
   return MLS_ERR_UNSUPPORTED;
 }
 
