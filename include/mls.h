@@ -18,7 +18,7 @@
  *                (even k -> low nibble, value = nibble - 8)     strides ld_sn, ld_sg
  *   e4m3 bytes   OCP FP8 E4M3 ("fn": bias 7, no inf, max 448, NaN = S.1111.111)
  *
- * dtype codes: MLS_F32, MLS_F16, MLS_BF16.
+ * dtype codes: MLS_F32, MLS_F16, MLS_BF16 (MLS_F64 only where an entry point says so).
  */
 #ifndef MLS_H
 #define MLS_H
@@ -31,7 +31,8 @@ extern "C" {
 
 typedef struct ihipStream_t* mls_stream_t; /* identical to hipStream_t */
 
-enum { MLS_F32 = 0, MLS_F16 = 1, MLS_BF16 = 2 };
+enum { MLS_F32 = 0, MLS_F16 = 1, MLS_BF16 = 2,
+       MLS_F64 = 3 /* only where an entry point says so (mls_moe_combine) */ };
 enum {
   MLS_OK = 0,
   MLS_ERR_ARG = -1,         /* invalid argument (shape, stride, dtype, null, alignment) */
@@ -39,7 +40,7 @@ enum {
   MLS_ERR_HIP = -3          /* a HIP runtime call failed */
 };
 
-#define MLS_ABI_VERSION 6
+#define MLS_ABI_VERSION 7
 
 /* No reference counterpart: version of this ABI (MLS_ABI_VERSION). */
 int mls_abi_version(void);
@@ -246,7 +247,8 @@ int mls_int4_grouped_gate_up_rows(const void* a, int a_dt, int64_t lda,
 
 /* Replaces _combine_rows_kernel + combine_rows (kernels/moe_routing.py:52-76, 100-113):
  * out[t][d] = sum_{s<k} w[t][s] * X(pos[t][s], d), fp32 accumulation, one rounding; one block
- * per output row, no atomics. x: x_dt [x_rows][ldx]; X(r, d) = x[r][d], or with splits > 1
+ * per output row, no atomics. x_dt MLS_F64 (the reference's ACC64, moe_routing.py:58-72,
+ * 112): accumulated in fp64, and out_dt must be MLS_F64; w_dt may be any of the four. x: x_dt [x_rows][ldx]; X(r, d) = x[r][d], or with splits > 1
  * the sum of the `splits` partial products x[p * split_stride + r * ldx + d] of a K-split
  * GEMM (mls_int4_grouped_gemm_partial). out: out_dt [T][ldo]; w: w_dt [T][k]; pos: int64
  * [T][k]; a position outside [0, x_rows) contributes nothing. */

@@ -341,8 +341,10 @@ int launch_gemm_small(int wbits, const WqArgs& p) {
     // and a table of 64 rows that fits beside the reduction buffer
     if (p.ld_sg != 1 || (a.G * ssz) % 4 != 0 || (p.ld_sn * ssz) % 4 != 0 || !aligned(p.s, 4))
       return MLS_ERR_UNSUPPORTED;
-    if (64 * a.G * ssz + 1024 > 65536 || p.N * p.ld_sn * ssz >= kPastEnd / 2) return MLS_ERR_UNSUPPORTED;
-    a.s_bytes = (int)(p.N * p.ld_sn * ssz);
+    if (64 * a.G * ssz + 1024 > 65536 || (p.N * p.ld_sn + a.G) * ssz >= kPastEnd / 2) return MLS_ERR_UNSUPPORTED;
+    // the descriptor spans the scales that exist: row N - 1 starts at (N - 1) ld_sn and
+    // holds G groups (ld_sn may be below G, e.g. 0 for one row broadcast to every n)
+    a.s_bytes = (int)(((p.N - 1) * p.ld_sn + a.G) * ssz);
   }
   if (wbits == 4 && s64) {
     if (p.a_dt == MLS_BF16) return p.s_dt == MLS_F16 ? dispatch_small<4, __bf16, _Float16, true>(a, p.stream)

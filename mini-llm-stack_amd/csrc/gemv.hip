@@ -618,7 +618,10 @@ static int launch_gemv1_si(const WqArgs& p, int s_dw) {
   constexpr int XI = WBITS == 4 ? CPL : (CPL >= 2 ? CPL / 2 : 1);
   if (p.K * 2 > XI * 4096) return MLS_ERR_UNSUPPORTED;
   const int s_row_bytes = (int)(p.ld_sn * (int64_t)sizeof(ST));
-  const int s_bytes = WBITS == 4 ? (int)(p.N * p.ld_sn * (int64_t)sizeof(ST)) : 0;
+  // the scale descriptor spans exactly the scales that exist: row N - 1 starts at
+  // (N - 1) ld_sn and holds G groups (ld_sn may be below G, e.g. 0 for one row broadcast)
+  const int s_bytes =
+      WBITS == 4 ? (int)(((p.N - 1) * p.ld_sn + p.K / p.group) * (int64_t)sizeof(ST)) : 0;
   // rows of x: 1 or 2 (3 and 4 rows measured slower than the MFMA skinny kernel: the dot
   // products grow with M while the widening is shared); x of both rows in LDS within 32 KiB
   if (p.M > 2) return MLS_ERR_UNSUPPORTED;
@@ -670,7 +673,7 @@ static int launch_gemv1_st(const WqArgs& p) {
     if (p.ld_sg != 1 || (G * (int64_t)sizeof(ST)) % 4 != 0 || (p.ld_sn * (int64_t)sizeof(ST)) % 4 != 0 ||
         !aligned(p.s, 4))
       return MLS_ERR_UNSUPPORTED;
-    if ((int64_t)p.N * p.ld_sn * (int64_t)sizeof(ST) > 0x7FFFFFFF) return MLS_ERR_UNSUPPORTED;
+    if (((int64_t)p.N * p.ld_sn + G) * (int64_t)sizeof(ST) > 0x7FFFFFFF) return MLS_ERR_UNSUPPORTED;
     s_dw = (int)(G * (int64_t)sizeof(ST) / 4);
   }
   const int64_t cpl = cdiv(p.K / KC, 64);

@@ -161,8 +161,11 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
   auto group_of = [&](int st) __attribute__((always_inline)) { return (int)(((float)st + 0.5f) * inv_spg); };
   const int g0 = group_of(s_lo);
   if constexpr (WBITS == 4 && SL) {
+    // the range is the block's true extent of s, ((rows_w - 1) ld_sn + (G - 1) ld_sg + 1)
+    // scales, for any strides (transposed [G][N] scales, a broadcast row with ld_sn = 0)
+    const int64_t s_ext = (int64_t)(rows_w - 1) * ld_sn + (int64_t)(K / group - 1) * ld_sg + 1;
     const __amdgpu_buffer_rsrc_t rss = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(s + (int64_t)n_base * ld_sn), (short)0, (int)(rows_w * ld_sn * (int64_t)sizeof(ST)), 0x00020000);
+        (void*)(s + (int64_t)n_base * ld_sn), (short)0, (int)(s_ext * (int64_t)sizeof(ST)), 0x00020000);
 #pragma unroll
     for (int i = 0; i < SLG * 16 * R / 64; ++i) {
       const int e = 64 * i + lane, row = e % (16 * R), gl = e / (16 * R);

@@ -38,11 +38,12 @@ if not torch.cuda.is_available():
 # This implementation only ever runs compiled gfx950 code.
 INTERPRETER = False
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 LIB_PATH = Path(os.environ.get("MLS_LIB") or
                 Path(__file__).resolve().parent.parent / "libmls_hip.so")
 
 MLS_F32, MLS_F16, MLS_BF16 = 0, 1, 2
+MLS_F64 = 3  # mls_moe_combine only
 MLS_OK, MLS_ERR_ARG, MLS_ERR_UNSUPPORTED, MLS_ERR_HIP = 0, -1, -2, -3
 MLS_FP8_NATIVE = 1
 MLS_FP8_A_E5M2 = 2

@@ -50,9 +50,15 @@ def gather_rows(x: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
     return x.index_select(0, idx.to(torch.int64))
 
 
+def _combine_dt(dtype: torch.dtype, what: str) -> int:
+    """dtype code of a combine operand: the three GEMM dtypes and fp64."""
+    return kernels.MLS_F64 if dtype == torch.float64 else dt_code(dtype, what)
+
+
 def combine_rows(expert_out: torch.Tensor, weights: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
-    """out[t] = sum_k weights[t, k] * expert_out[pos[t, k]], fp32 accumulation, output in
-    expert_out's dtype (kernels/moe_routing.py:100-113)."""
+    """out[t] = sum_k weights[t, k] * expert_out[pos[t, k]], output in expert_out's dtype,
+    accumulated in fp32, or in fp64 when expert_out is fp64 (the reference's ACC64, which
+    its fp64 gradcheck relies on; kernels/moe_routing.py:54-72, 100-113)."""
     dev = require_hip("combine_rows", expert_out, weights, pos)
     T, K = pos.shape
     D = expert_out.shape[1]
@@ -61,9 +67,9 @@ def combine_rows(expert_out: torch.Tensor, weights: torch.Tensor, pos: torch.Ten
     p = pos.to(torch.int64).contiguous()
     out = torch.empty(T, D, dtype=x.dtype, device=dev)
     kernels.check(kernels.lib().mls_moe_combine(
-        x.data_ptr(), dt_code(x.dtype, "combine_rows"), ld(x), x.shape[0], 1, 0, w.data_ptr(),
-        dt_code(w.dtype, "combine_rows weights"), p.data_ptr(), T, K, out.data_ptr(), dt_code(out.dtype, "combine_rows"),
-        ld(out), D, stream(dev)), "combine_rows")
+        x.data_ptr(), _combine_dt(x.dtype, "combine_rows"), ld(x), x.shape[0], 1, 0, w.data_ptr(),
+        _combine_dt(w.dtype, "combine_rows weights"), p.data_ptr(), T, K, out.data_ptr(),
+        _combine_dt(out.dtype, "combine_rows"), ld(out), D, stream(dev)), "combine_rows")
     return out
 
 

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = kernels.load_library()
-    assert lib.mls_abi_version() == kernels.ABI_VERSION == 6
+    assert lib.mls_abi_version() == kernels.ABI_VERSION == 7
     assert isinstance(lib.mls_last_error(), bytes)
 
 
@@ -171,6 +171,12 @@ def test_gate_up_and_combine_reject():
     assert L.mls_moe_combine(1, bf, 8, 4, 0, 0, 1, bf, 1, 2, 2, 1, bf, 8, 8, NULL) == kernels.MLS_ERR_ARG
     assert L.mls_moe_combine(1, bf, 8, 4, 2, 16, 1, bf, 1, 2, 2, 1, bf, 8, 8, NULL) == kernels.MLS_ERR_ARG
     assert L.mls_moe_combine(NULL, bf, 8, 0, 1, 0, NULL, bf, NULL, 0, 2, NULL, bf, 8, 8, NULL) == 0
+    # fp64 rows need an fp64 output, and an fp64 output needs fp64 rows; unknown codes fail
+    f64, f32 = kernels.MLS_F64, kernels.MLS_F32
+    assert L.mls_moe_combine(1, f64, 8, 4, 1, 0, 1, f64, 1, 2, 2, 1, f32, 8, 8, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_moe_combine(1, f32, 8, 4, 1, 0, 1, f64, 1, 2, 2, 1, f64, 8, 8, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_moe_combine(1, 4, 8, 4, 1, 0, 1, f32, 1, 2, 2, 1, f32, 8, 8, NULL) == kernels.MLS_ERR_ARG
+    assert L.mls_moe_combine(NULL, f64, 8, 0, 1, 0, NULL, f64, NULL, 0, 2, NULL, f64, 8, 8, NULL) == 0
     # split count: the down projection of config E's expert MLP splits K in 4; a wide output does not
     assert L.mls_int4_grouped_splits(1024, 8, 4096, 14336, 128) == 4
     assert L.mls_int4_grouped_splits(1024, 8, 14336, 4096, 128) == 1

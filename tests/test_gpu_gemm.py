@@ -180,8 +180,9 @@ def test_gemv_other_dtypes(dev, dtype, M):
 @pytest.mark.parametrize("N,K,gs,dtype,sdt", [
     (1000, 3072, 32, torch.bfloat16, torch.float16),   # ragged N, chunks past K, 4 scale instructions
     (777, 4096, 128, torch.float16, torch.float32),    # fp32 scales: 2 scale instructions per wavefront
-    (64, 512, 128, torch.bfloat16, torch.float16),     # one chunk per lane, 8 rows per wavefront
-    (4100, 2048, 64, torch.bfloat16, torch.float16),   # last block holds 4 of its 16 rows
+    (64, 512, 128, torch.bfloat16, torch.float16),     # one chunk per lane; N < 8192: 2 rows per wavefront
+    (4100, 2048, 64, torch.bfloat16, torch.float16),   # 2 rows per wavefront; last block holds 4 of its 8 rows
+    (8200, 2048, 64, torch.bfloat16, torch.float16),   # N >= 8192: 8 rows per wavefront, last block ragged
 ])
 def test_gemv_m1_edges(dev, N, K, gs, dtype, sdt):
     """M = 1 with 16-bit activations (x and scales through LDS): ragged N, K not a multiple of the
@@ -200,6 +201,43 @@ def test_gemv_m1_edges(dev, N, K, gs, dtype, sdt):
     s8 = s8.to(sdt)
     _check(int8_matmul(ab.to(dev), q, s8),
            ref.int8_matmul(ab.float().numpy(), q.cpu().numpy(), s8.float().cpu().numpy()), f"int8 M=1 N={N} K={K}")
+
+
+def _scale_layout(s: torch.Tensor, layout: str) -> torch.Tensor:
+    """The same [N, G] scale values under another stride pattern."""
+    N, G = s.shape
+    if layout == "transposed":        # stored [G][N]: strides (1, N)
+        return s.t().contiguous().t()
+    if layout == "row_broadcast":     # one row for every n: strides (0, 1)
+        return s[:1].expand(N, G)
+    if layout == "group_broadcast":   # one group for every k: strides (ld, 0)
+        return s[:, :1].expand(N, G)
+    if layout == "padded":            # rows G + 3 apart
+        w = torch.zeros(N, G + 3, dtype=s.dtype, device=s.device)
+        w[:, :G] = s
+        return w[:, :G]
+    raise ValueError(layout)
+
+
+@pytest.mark.parametrize("layout", ["transposed", "row_broadcast", "group_broadcast", "padded"])
+@pytest.mark.parametrize("M,N,K,gs,sdt", [
+    (1, 1000, 4096, 128, torch.float16),    # M = 1 GEMV (x and scales through LDS where the strides allow)
+    (2, 1000, 4096, 128, torch.float16),    # two-row GEMV / skinny kernel
+    (4, 1000, 4096, 128, torch.float16),    # skinny MFMA kernel, scale slice in LDS
+    (5, 1000, 1088, 64, torch.float32),     # skinny, 64-k steps, fp32 scales
+    (64, 1000, 4096, 128, torch.float16),   # medium GEMM, scale table in LDS
+    (300, 1000, 1024, 128, torch.float16),  # MFMA engine
+])
+def test_int4_scale_strides(dev, layout, M, N, K, gs, sdt):
+    """int4_matmul honours any scale strides, as the reference does (dequant_matmul.py:182):
+    transposed [G][N] storage, broadcast views with a zero stride and padded rows give the
+    result of the same values stored contiguously."""
+    a, w = _data(M, N, K, 1300 + M + N, 0.02)
+    p, s = quantize_int4(w.to(dev), gs)
+    sv = _scale_layout(s.to(sdt), layout)
+    ab = a.to(torch.bfloat16)
+    want = ref.int4_matmul(ab.float().numpy(), p.cpu().numpy(), sv.float().contiguous().cpu().numpy(), gs)
+    _check(int4_matmul(ab.to(dev), p, sv, gs), want, f"int4 scales {layout} M={M} N={N} K={K} g{gs}")
 
 
 def test_gemv_m1_unaligned_output_and_long_rows(dev):

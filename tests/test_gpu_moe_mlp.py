@@ -112,6 +112,75 @@ def test_combine_rows(dev, D, dt):
             _check16(out, want, f"combine {dt} D={D}")
 
 
+@pytest.mark.parametrize("D", [8, 24, 1000])
+@pytest.mark.parametrize("wdt", [torch.float64, torch.float32])
+def test_combine_rows_fp64(dev, D, wdt):
+    """fp64 expert outputs are combined in fp64 with an fp64 result (the reference's ACC64,
+    kernels/moe_routing.py:58-72, 112): within a few fp64 ulps of the oracle's fp64 sum,
+    a bound that fp32 accumulation (errors ~1e-7) fails by seven orders of magnitude."""
+    T, K = 40, 3
+    g = torch.Generator().manual_seed(D + 7)
+    x = torch.randn(T * K, D, generator=g, dtype=torch.float64)
+    w = torch.rand(T, K, generator=g, dtype=torch.float64).to(wdt)
+    pos = torch.randperm(T * K, generator=g).reshape(T, K)
+    out = combine_rows(x.to(dev), w.to(dev), pos.to(dev))
+    assert out.dtype == torch.float64 and out.shape == (T, D)
+    want = ref.combine_rows(x.numpy(), w.double().numpy(), pos.numpy())
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-13, atol=1e-13)
+
+
+def test_combine_rows_gradcheck_fp64_through_overlay(dev, tmp_path):
+    """The reference's gradcheck of its combine (tests/test_backward.py:113-119) on device
+    tensors, with the autograd Function resolved through the overlay: a checkout's
+    kernels.autograd_ops (a stub shaped like the reference's CombineRowsFn,
+    kernels/autograd_ops.py:59-71, whose backward restates kernels/moe_backward.py's
+    formulas in torch ops) binds this build's combine_rows as its forward. Finite
+    differences at eps = 1e-6 see through the forward only if it accumulates in fp64."""
+    import sys
+    import textwrap
+    import kernels
+    import kernels.moe_routing as mr
+    ck = tmp_path / "checkout" / "kernels"
+    ck.mkdir(parents=True)
+    (ck / "moe_backward.py").write_text(textwrap.dedent("""
+        import torch
+        def combine_backward(dout, expert_out, weights, pos):
+            deo = torch.zeros_like(expert_out)
+            deo[pos.reshape(-1)] = (weights.unsqueeze(-1) * dout.unsqueeze(1)).reshape(-1, expert_out.shape[1])
+            dw = (dout.unsqueeze(1) * expert_out[pos]).sum(-1)
+            return deo, dw
+    """))
+    (ck / "autograd_ops.py").write_text(textwrap.dedent("""
+        import torch
+        from kernels.moe_backward import combine_backward
+        from kernels.moe_routing import combine_rows
+        class CombineRowsFn(torch.autograd.Function):
+            @staticmethod
+            def forward(ctx, expert_out, weights, pos):
+                ctx.save_for_backward(expert_out, weights, pos)
+                return combine_rows(expert_out, weights, pos)
+            @staticmethod
+            def backward(ctx, dout):
+                expert_out, weights, pos = ctx.saved_tensors
+                deo, dw = combine_backward(dout, expert_out, weights, pos)
+                return deo, dw, None
+    """))
+    kernels.__path__.append(str(ck))
+    try:
+        import kernels.autograd_ops as ao
+        assert ao.combine_rows is mr.combine_rows
+        T, K, D = 6, 2, 8
+        g = torch.Generator().manual_seed(0)
+        eo = torch.randn(T * K, D, dtype=torch.float64, generator=g).to(dev).requires_grad_(True)
+        w = torch.rand(T, K, dtype=torch.float64, generator=g).to(dev).requires_grad_(True)
+        pos = torch.randperm(T * K, generator=g).reshape(T, K).to(dev)
+        assert torch.autograd.gradcheck(lambda a, b: ao.CombineRowsFn.apply(a, b, pos), (eo, w), eps=1e-6)
+    finally:
+        kernels.__path__.remove(str(ck))
+        for m in ("kernels.autograd_ops", "kernels.moe_backward"):
+            sys.modules.pop(m, None)
+
+
 def test_combine_rows_edges(dev):
     x = torch.randn(8, 32, device=dev)
     empty = combine_rows(x, torch.zeros(0, 2, device=dev), torch.zeros(0, 2, dtype=torch.int64, device=dev))
