@@ -199,6 +199,89 @@ def time_steps(fns, warmup: int, steps: int) -> float:
     return ms / steps
 
 
+def clocked_steps(fns, warmup: int, steps: int, waves: int) -> dict:
+    """Execution spans of `steps` launches of a clocked kernel copy (libmls_floor.so), with
+    time_steps' protocol (one graph of warmup + timed steps, one untimed replay, WARM_MS of
+    eager launches, every copy once more, then the timed replay). fns[i](clocks_ptr)
+    launches step i's kernel, whose every wavefront stores its {t0, t1} realtime clocks
+    (first instruction; all memory operations complete) at clocks_ptr; timed step i
+    writes its own slice, all other launches a scratch slice. Per timed launch: start =
+    min t0, end = max t1, exec = end - start; across launches: period = start_(i+1) -
+    start_i (the launch-to-launch time, what time_steps measures), gap = start_(i+1) -
+    end_i (from the last wavefront's end to the next launch's first wavefront)."""
+    import ctypes
+    import torch
+    lib = _floor_lib()
+    khz = ctypes.c_int(0)
+    if lib.mlsf_wallclock_khz(ctypes.byref(khz)) != 0 or khz.value <= 0:
+        raise RuntimeError("bench: cannot read the GPU's realtime counter rate")
+    n = len(fns)
+    clocks = torch.zeros(steps + 1, waves, 2, dtype=torch.int64, device="cuda")
+    base, slot = clocks.data_ptr(), waves * 16
+    scratch = base + steps * slot
+    for f in fns:
+        f(scratch)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(warmup):
+            fns[i % n](scratch)
+        for i in range(steps):
+            fns[(warmup + i) % n](base + i * slot)
+    g.replay()
+    torch.cuda.synchronize()
+    deadline, i = time.perf_counter() + WARM_MS * 1e-3, 0
+    while time.perf_counter() < deadline:
+        fns[i % n](scratch)
+        i += 1
+        if i % 16 == 0:
+            torch.cuda.synchronize()
+    for f in fns:
+        f(scratch)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    c = clocks[:steps].double().cpu()
+    if bool((c[:, :, 0] == 0).any()) or bool((c[:, :, 1] < c[:, :, 0]).any()):
+        raise RuntimeError("bench: a clocked launch left wavefront clocks unwritten or out of order")
+    us = 1e3 / khz.value
+    t0, t1 = c[:, :, 0], c[:, :, 1]
+    start, end = t0.min(1).values, t1.max(1).values
+    exec_ = (end - start) * us
+    period = (start[1:] - start[:-1]) * us
+    gap = (start[1:] - end[:-1]) * us
+    med = lambda v: float(v.median())
+    return {"exec_us": round(float(exec_.mean()), 3), "exec_us_median": round(med(exec_), 3),
+            "period_us": round(float(period.mean()), 3), "gap_us": round(float(gap.mean()), 3),
+            "gap_us_median": round(med(gap), 3),
+            "ramp_us": round(float(((t0.max(1).values - start) * us).mean()), 3),
+            "wave_us": round(float(((t1 - t0) * us).mean()), 3), "waves": waves, "launches": steps,
+            "tick_us": round(us, 4)}
+
+
+def graph_events_ms(fns, warmup: int, steps: int) -> float:
+    """ms per step of `steps` launches captured in one graph and timed with events around
+    a single replay (after one untimed replay): a cross-check of time_steps that needs no
+    stamp kernel; the replay's own launch cost (~11.6 us) is spread over all steps."""
+    import torch
+    n = len(fns)
+    for f in fns:
+        f()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(warmup + steps):
+            fns[i % n]()
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (warmup + steps)
+
+
 def wall_median_ms(fn, warmup: int = 3, iters: int = 30) -> float:
     """The reference's own timing protocol (bench/_util.py:36-51): median host wall time
     of one call followed by a device synchronize."""
@@ -382,6 +465,107 @@ def floor_rows(dev, steps: int, warmup: int, nbytes=8_667_136, copies=125, block
              "roofline": {"bound": "hbm", "achieved": round(gbs_st, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(gbs_st / HBM_PEAK_GBS, 4)},
              "blocks": blocks, "buffers_rotated": copies, "stored_bytes": blocks * 4 * 8, "note": note}]
+
+
+def clock_rows(dev, steps: int, warmup: int, long_steps: int = 2000):
+    """Where an M = 1 step's time goes: the library's INT4 (headline) and INT8 GEMVs and
+    the floor kernels at the same sizes and grids, as clocked copies (libmls_floor.so:
+    gemv1.h's kernel body, or the calibration kernel, with realtime clocks read by every
+    wavefront at its first instruction and after its last memory operation completed).
+    Each row gives the copy's execution span per launch (first wavefront's start to last
+    wavefront's end), the launch-to-launch period and the gap between launches, next to
+    the library kernel's own step time from time_steps in the same run and, for the
+    GEMVs, from events around one graph replay of `long_steps` launches. The clocked
+    GEMV copies must reproduce the library's output bit for bit before they are timed."""
+    import ctypes
+    import torch
+    from kernels.dequant_matmul import int4_matmul, int8_matmul
+    from serve.quantize import quantize_int4, quantize_int8
+    lib = _floor_lib()
+    lib.mlsf_gemv1_clocked.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                       ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p,
+                                       ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.mlsf_empty_clocked.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    lib.mlsf_stream_clocked.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    N = K = 4096
+
+    def st():
+        return torch.cuda.current_stream(dev).cuda_stream
+
+    def call(rc, want=0):
+        if rc != want:
+            raise RuntimeError(f"clocked kernel launch returned {rc}, expected {want}")
+
+    out = []
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(1, K, generator=g, device=dev).to(torch.bfloat16)
+    for bits in (4, 8):
+        if bits == 4:
+            w, s = quantize_int4(torch.randn(N, K, generator=g, device=dev) * 0.02, 128)
+            lib_fn = lambda w, s: int4_matmul(x, w, s, 128)
+            ld_sn, group, waves = s.stride(0), 128, N // 4
+        else:
+            w, s = quantize_int8(torch.randn(N, K, generator=g, device=dev) * 0.02)
+            lib_fn = lambda w, s: int8_matmul(x, w, s)
+            ld_sn, group, waves = 1, 0, N
+        s = s.to(torch.float16)
+        wbytes = w.numel() + s.numel() * 2
+        nbytes = wbytes + 2 * K * 2
+        copies = max(2, -(-ROTATE_BYTES // wbytes))
+        ws = [w] + [w.clone() for _ in range(copies - 1)]
+        ss = [s] + [s.clone() for _ in range(copies - 1)]
+        y = torch.empty(1, N, dtype=torch.bfloat16, device=dev)
+        clk = torch.zeros(waves, 2, dtype=torch.int64, device=dev)
+        call(lib.mlsf_gemv1_clocked(bits, x.data_ptr(), w.data_ptr(), w.stride(0), s.data_ptr(), ld_sn, group,
+                                    y.data_ptr(), N, K, 0, clk.data_ptr(), st()), waves)
+        same = bool(torch.equal(y, lib_fn(w, s)))
+        row = {"name": f"clocks_int{bits}_gemv_m1_4096x4096", "bytes_per_step": nbytes,
+               "clocked_copy_bit_identical_to_library": same}
+        if same:
+            ms_lib = time_steps([lambda i=i: lib_fn(ws[i], ss[i]) for i in range(copies)], warmup, steps)
+            ms_ev = graph_events_ms([lambda i=i: lib_fn(ws[i], ss[i]) for i in range(copies)], warmup, long_steps)
+            def fns(wait):
+                return [lambda p, i=i: call(lib.mlsf_gemv1_clocked(bits, x.data_ptr(), ws[i].data_ptr(),
+                                                                   ws[i].stride(0), ss[i].data_ptr(), ld_sn, group,
+                                                                   y.data_ptr(), N, K, wait, p, st()), waves)
+                        for i in range(copies)]
+            ck = clocked_steps(fns(0), warmup, steps, waves)
+            ckw = clocked_steps(fns(1), warmup, steps, waves)
+            row.update({"library_step_us": round(ms_lib * 1e3, 3),
+                        f"library_step_us_events_{long_steps}_launches": round(ms_ev * 1e3, 3),
+                        "clocked": ck, "clocked_memory_end": ckw,
+                        "exec_TB/s": round(nbytes / (ck["exec_us"] * 1e-6) / 1e12, 4),
+                        "exec_frac": round(nbytes / (ck["exec_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                        "step_frac": round(nbytes / (ms_lib * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+        out.append(row)
+        del ws, ss
+        # the floor kernels at the same bytes and grid: an empty launch, a pure streaming read,
+        # and the read with one 8-byte store per wavefront
+        blocks = waves // 4
+        gb = torch.Generator(device=dev).manual_seed(9)
+        nb = (nbytes + 15) // 16 * 16
+        bcopies = max(2, -(-ROTATE_BYTES // nb))
+        bufs = [torch.randint(0, 2**31 - 1, (nb // 4,), generator=gb, device=dev, dtype=torch.int32)
+                for _ in range(bcopies)]
+        sink = torch.zeros(blocks * 8, dtype=torch.int32, device=dev)
+        kinds = [("empty", None), ("stream_read", 0), ("stream_read_store", 1)]
+        for kind, store in kinds:
+            def sfns(wait):
+                if store is None:
+                    return [lambda p: call(lib.mlsf_empty_clocked(blocks, p, st()))]
+                return [lambda p, b=b: call(lib.mlsf_stream_clocked(b.data_ptr(), nb, blocks, sink.data_ptr(), store,
+                                                                    wait, p, st())) for b in bufs]
+            ck = clocked_steps(sfns(0), warmup, steps, waves)
+            r = {"name": f"clocks_floor_{kind}_{blocks}_blocks" + ("" if store is None else f"_{nb}B"),
+                 "clocked": ck, "note": "calibration kernel (libmls_floor.so), clocked"}
+            if store is not None:
+                r["clocked_memory_end"] = clocked_steps(sfns(1), warmup, steps, waves)
+                r["exec_TB/s"] = round(nb / (ck["exec_us"] * 1e-6) / 1e12, 4)
+                r["period_TB/s"] = round(nb / (ck["period_us"] * 1e-6) / 1e12, 4)
+            out.append(r)
+        del bufs
+    return out
 
 
 def int8_dgrad_row(dev, steps: int, warmup: int, M=4096, N=11008, K=4096):
@@ -959,6 +1143,7 @@ def main(argv=None) -> int:
                           + floor_rows(dev, args.steps, args.warmup, nbytes=16_801_792, copies=64,
                                        blocks=512)[1:]),
         "cpu": lambda: cpu_baseline(),
+        "clocks": lambda: clock_rows(dev, args.steps, args.warmup),
     }
     for kind, peak in (("fp8_rowwise", FP8_PEAK_TFLOPS), ("fp8_tensorwise", FP8_PEAK_TFLOPS),
                        ("bf16", BF16_PEAK_TFLOPS)):
@@ -985,7 +1170,8 @@ def main(argv=None) -> int:
     if not args.no_extra:
         for k in ("int4_m2", "int4_m4", "int4_m16", "int8_gemv", "int8_m2", "int8_prefill", "int8_dgrad", "fp8_gemm", "fp8_native",
                   "fp8_bwd", "fp8_bwd_native", "moe_int4", "moe_mlp_int4", "paged_attn", "quantize_int4",
-                  "ref_shapes", "copy", "floor", "vendor_fp8_rowwise", "vendor_fp8_tensorwise", "vendor_bf16"):
+                  "ref_shapes", "copy", "floor", "clocks", "vendor_fp8_rowwise", "vendor_fp8_tensorwise",
+                  "vendor_bf16"):
             log(f"{k} ...")
             row = runners[k]()
             log(json.dumps(row))
@@ -1005,6 +1191,16 @@ def main(argv=None) -> int:
     roof["traffic_source"] = (f"{TRAFFIC_FILE}: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE per dispatch of this "
                               "kernel, scaled by the same counters on a copy kernel of known size; a stored "
                               "measurement, not taken in this run")
+    # the step split into the kernel's execution on the GPU and the launch around it, from
+    # the clocked copy of the same kernel body in this run (extra row clocks_int4_gemv_m1_...)
+    ck = next((r for r in extra if r.get("name") == "clocks_int4_gemv_m1_4096x4096" and "clocked" in r), None)
+    if ck is not None:
+        c = ck["clocked"]
+        roof["step_split"] = {"kernel_exec_us": c["exec_us"], "launch_gap_us": c["gap_us"],
+                              "clocked_period_us": c["period_us"], "exec_frac": ck["exec_frac"],
+                              "library_step_us_events_2000": ck["library_step_us_events_2000_launches"],
+                              "source": "clocked copy of the kernel body (libmls_floor.so), realtime clocks per "
+                                        "wavefront: exec = first wavefront start to last wavefront end"}
     line = {
         "metric": METRIC,
         "value": head["TB/s"],
