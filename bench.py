@@ -394,22 +394,52 @@ def int8_gemv(dev, M: int, steps: int, warmup: int, N: int = 4096, K: int = 4096
     return dict(ms=ms, bytes=nbytes, flops=2 * M * N * K, copies=copies, parity=par, call=fns[0])
 
 
-def int8_prefill(dev, steps: int, warmup: int, M=2048, N=11008, K=4096):
+def int8_prefill(dev, steps: int, warmup: int, M=2048, N=11008, K=4096, act=None):
     import torch
     from kernels.dequant_matmul import int8_matmul
     from serve.quantize import quantize_int8
+    act = act or torch.bfloat16
     g = torch.Generator(device=dev).manual_seed(2)
     q, s = quantize_int8(torch.randn(N, K, generator=g, device=dev) * 0.02)
     s = s.to(torch.float16)
     copies = 6
-    xs = [torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+    xs = [torch.randn(M, K, generator=g, device=dev).to(act) for _ in range(copies)]
     qs = [q] + [q.clone() for _ in range(copies - 1)]
     r = _rows(M)
-    par = gate(int8_matmul(xs[0], q, s)[r], xs[0][r].float() @ _deq8(q, s).t(), "bf16")
+    par = gate(int8_matmul(xs[0], q, s)[r], xs[0][r].float() @ _deq8(q, s).t(),
+               "bf16" if act != torch.float32 else "fp32")
     fns = [lambda i=i: int8_matmul(xs[i], qs[i], s) for i in range(copies)]
     ms = time_steps(fns, warmup, steps) if par["ok"] else None
-    nbytes = N * K + N * 2 + M * K * 2 + M * N * 2
+    esz = xs[0].element_size()
+    nbytes = N * K + N * 2 + M * K * esz + M * N * esz
     return dict(ms=ms, bytes=nbytes, flops=2 * M * N * K, copies=copies, parity=par)
+
+
+def fp32_rows(dev, steps: int, warmup: int):
+    """fp32 activations at the reference engine's call shapes (its serving path runs fp32
+    end to end, serve/engine.py:166): M = 1 / 5 (decode of one / five sequences), 64 (a
+    prefill chunk), 2048 (a long prompt), K = N = 4096, INT4 g128 and INT8 with fp16
+    scales; and config C's INT8 prefill (2048 x 11008 x 4096) in fp32. M <= 16 runs the
+    VALU GEMV, larger M the bf16 hi + lo split on the matrix cores."""
+    import torch
+    out = []
+    small = max(8, steps // 8)
+    for bits in (4, 8):
+        for M in (1, 5, 64, 2048):
+            fn = int4_gemv if bits == 4 else int8_gemv
+            r = fn(dev, M, steps if M <= 64 else small, warmup if M <= 64 else 4, act=torch.float32,
+                   seed=40 + M + bits)
+            name = f"fp32_int{bits}{'_g128' if bits == 4 else ''}_m{M}_4096x4096"
+            row = _mfma_row(name, r, BF16_PEAK_TFLOPS) if M >= 2048 else _hbm_row(name, r)
+            if row.get("ms_per_step") is not None and M >= 2048:
+                row["hbm_frac"] = round(r["bytes"] / (r["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+            row["path"] = "VALU GEMV (fp32 FMAs)" if M <= 16 else "bf16 hi + lo split, bf16 MFMA"
+            out.append(row)
+    r = int8_prefill(dev, small, 4, act=torch.float32)
+    row = _mfma_row("fp32_int8_prefill_2048x11008x4096", r, BF16_PEAK_TFLOPS,
+                    {"path": "bf16 hi + lo split, bf16 MFMA (two MFMAs per bf16 one)"})
+    out.append(row)
+    return out
 
 
 def floor_rows(dev, steps: int, warmup: int, nbytes=8_667_136, copies=125, blocks=256):
@@ -1072,7 +1102,7 @@ def main(argv=None) -> int:
     ap.add_argument("--only", default=None,
                     help="run one workload: int4_gemv, int4_m4, int4_m16, int8_gemv, int8_prefill, "
                          "fp8_gemm, fp8_native, fp8_bwd, fp8_bwd_native, moe_int4, moe_mlp_int4, paged_attn, "
-                         "quantize_int4, ref_shapes, "
+                         "quantize_int4, ref_shapes, fp32 (fp32 activations), clocks (M=1 step split), "
                          "copy (counter calibration), vendor_fp8_rowwise / vendor_fp8_tensorwise / "
                          "vendor_bf16 (hipBLASLt calibration), cpu (the CPU baseline alone)")
     ap.add_argument("--no-extra", action="store_true")
@@ -1144,6 +1174,7 @@ def main(argv=None) -> int:
                                        blocks=512)[1:]),
         "cpu": lambda: cpu_baseline(),
         "clocks": lambda: clock_rows(dev, args.steps, args.warmup),
+        "fp32": lambda: fp32_rows(dev, args.steps, args.warmup),
     }
     for kind, peak in (("fp8_rowwise", FP8_PEAK_TFLOPS), ("fp8_tensorwise", FP8_PEAK_TFLOPS),
                        ("bf16", BF16_PEAK_TFLOPS)):
@@ -1168,7 +1199,8 @@ def main(argv=None) -> int:
         return 1
     extra = []
     if not args.no_extra:
-        for k in ("int4_m2", "int4_m4", "int4_m16", "int8_gemv", "int8_m2", "int8_prefill", "int8_dgrad", "fp8_gemm", "fp8_native",
+        for k in ("int4_m2", "int4_m4", "int4_m16", "int8_gemv", "int8_m2", "int8_prefill", "fp32", "int8_dgrad",
+                  "fp8_gemm", "fp8_native",
                   "fp8_bwd", "fp8_bwd_native", "moe_int4", "moe_mlp_int4", "paged_attn", "quantize_int4",
                   "ref_shapes", "copy", "floor", "clocks", "vendor_fp8_rowwise", "vendor_fp8_tensorwise",
                   "vendor_bf16"):

@@ -137,6 +137,28 @@ int mls_int4_gemm(const void* a, int a_dt, int64_t lda,
                   void* c, int c_dt, int64_t ldc,
                   int64_t M, int64_t N, int64_t K, mls_stream_t stream);
 
+/* The same two GEMMs (kernels/dequant_matmul.py:39-100, 140-185) with a caller workspace,
+ * for fp32 activations on the matrix cores: with a_dt = F32 and M > 16 (and K % 64 == 0,
+ * 16-byte aligned weight rows, an 8-byte aligned c, INT4 groups a multiple of 64) x is
+ * split into bf16 hi and lo parts (hi = x truncated to bf16, lo = bf16(x - hi): x to about
+ * 2^-16 of its magnitude) in the workspace, and both are multiplied on the bf16 MFMA with
+ * fp32 accumulation and added in fp32; every other call runs as mls_int8_gemm /
+ * mls_int4_gemm and ignores the workspace. mls_wq_gemm_workspace(wbits, M, N, K, a_dt,
+ * group) gives the bytes (256-byte aligned workspace; 0: none used). */
+int64_t mls_wq_gemm_workspace(int wbits, int64_t M, int64_t N, int64_t K, int a_dt, int group);
+int mls_int8_gemm_ws(const void* a, int a_dt, int64_t lda,
+                     const int8_t* w, int64_t ldw,
+                     const void* s, int s_dt,
+                     void* c, int c_dt, int64_t ldc,
+                     int64_t M, int64_t N, int64_t K,
+                     void* workspace, int64_t ws_bytes, mls_stream_t stream);
+int mls_int4_gemm_ws(const void* a, int a_dt, int64_t lda,
+                     const uint8_t* w, int64_t ldw,
+                     const void* s, int s_dt, int64_t ld_sn, int64_t ld_sg, int group,
+                     void* c, int c_dt, int64_t ldc,
+                     int64_t M, int64_t N, int64_t K,
+                     void* workspace, int64_t ws_bytes, mls_stream_t stream);
+
 /* Replaces _int8_dgrad_kernel + int8_dgrad (kernels/dequant_matmul.py:103-132, 155-167):
  * dx[m][k] = sum_n dy[m][n] * s[n] * w[n][k] (the input gradient of y = x W^T). */
 int mls_int8_dgrad(const void* dy, int dy_dt, int64_t lddy,
@@ -147,10 +169,12 @@ int mls_int8_dgrad(const void* dy, int dy_dt, int64_t lddy,
 
 /* The same input gradient on the matrix cores, with the reference's arithmetic
  * (kernels/dequant_matmul.py:127-128): ys = (dy * s) rounded to dy's dtype, times the int8
- * weights on the 16-bit MFMA, fp32 accumulation. Needs a caller workspace of
- * mls_int8_dgrad_workspace(M, N, K, dy_dt) bytes, 256-byte aligned (the scaled dy, the
- * transposed weights and a vector of ones); 0 means this shape takes mls_int8_dgrad's
- * route (fp32 dy), for which workspace may be null. Runs on `stream`, three launches. */
+ * weights on the 16-bit MFMA, fp32 accumulation; fp32 dy with M > 16: ys in fp32 as bf16
+ * hi + lo parts (as mls_int8_gemm_ws), both multiplied and added in fp32. Needs a caller
+ * workspace of mls_int8_dgrad_workspace(M, N, K, dy_dt) bytes, 256-byte aligned (the scaled
+ * dy, the transposed weights and a vector of ones); 0 means this shape takes mls_int8_dgrad's
+ * route (fp32 dy with M <= 16), for which workspace may be null. Runs on `stream`, three
+ * launches. */
 int64_t mls_int8_dgrad_workspace(int64_t M, int64_t N, int64_t K, int dy_dt);
 int mls_int8_dgrad_ws(const void* dy, int dy_dt, int64_t lddy,
                       const int8_t* w, int64_t ldw,

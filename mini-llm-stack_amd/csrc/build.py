@@ -23,7 +23,7 @@ PKG = CSRC.parent
 OUT = PKG / "libmls_hip.so"
 BUILD = CSRC / "_build"
 SOURCES = ["abi.hip", "e4m3.hip", "quant.hip", "gemv.hip", "gemv_mfma.hip", "gemm_mfma16.hip", "gemm_grouped.hip",
-           "wq_abi.hip", "gemm_small.hip", "gemm_bytes.hip", "gemm_fp8.hip", "dgrad.hip", "moe.hip", "transpose.hip", "paged_attn.hip"]
+           "wq_abi.hip", "gemm_small.hip", "gemm_bytes.hip", "gemm_fp8.hip", "dgrad.hip", "moe.hip", "transpose.hip", "paged_attn.hip", "split.hip"]
 ARCH = "gfx950"
 
 

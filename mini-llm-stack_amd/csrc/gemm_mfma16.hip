@@ -319,7 +319,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_gemm_kernel(const Mfma16P
 // The compiler keeps LDS reads behind pending LDS-direct loads; with this order the
 // only such wait is the barrier's own, after the MFMAs have covered the load.
 
-template <int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN, bool GROUPED>
+template <int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN, bool GROUPED, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WM * WN) void mfma16_adma_kernel(const Mfma16Params p) {
   constexpr int BK = 64;
   constexpr int NW = WM * WN, NT = 64 * NW;
@@ -526,7 +526,9 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_adma_kernel(const Mfma16P
     __syncthreads();
   }
 
-  // ---- epilogue: acc[i][j][r] = C[m = m0+wm0+16j+lr][n = n0+wn0+16i+4lk+r]
+  // ---- epilogue: acc[i][j][r] = C[m = m0+wm0+16j+lr][n = n0+wn0+16i+4lk+r]; split rows:
+  // tiles 2j' and 2j' + 1 hold the hi and lo parts of output row (m0 + wm0) / 2 + 16j' + lr
+  static_assert(!SPLIT || (!GROUPED && TM % 2 == 0 && (WTM % 32) == 0), "split rows pair whole 32-row groups");
   OT* c = static_cast<OT*>(p.c);
 #pragma unroll
   for (int i = 0; i < TN; ++i) {
@@ -537,12 +539,13 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_adma_kernel(const Mfma16P
       for (int r = 0; r < 4; ++r) sn[r] = scale_at(smat, p.s_dt, min(nb + r, N - 1));
     }
 #pragma unroll
-    for (int j = 0; j < TM; ++j) {
-      const int m = m0 + wm0 + j * 16 + lr;
-      if (m >= row_hi) continue;
+    for (int j = 0; j < (SPLIT ? TM / 2 : TM); ++j) {
+      const int m = SPLIT ? (m0 + wm0) / 2 + j * 16 + lr : m0 + wm0 + j * 16 + lr;
+      if (m >= (SPLIT ? p.m_out : row_hi)) continue;
       float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] * sn[r];
+      for (int r = 0; r < 4; ++r)
+        v[r] = (SPLIT ? acc[i][2 * j][r] + acc[i][2 * j + 1][r] : acc[i][j][r]) * sn[r];
       OT* dst = c + (int64_t)m * p.ldc + nb;
       if (nb + 3 < N && (p.ldc % 4) == 0) {
         store4<OT>(dst, v[0], v[1], v[2], v[3]);
@@ -578,7 +581,7 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_adma_kernel(const Mfma16P
 // 208 us.
 typedef uint32_t lds16_t __attribute__((ext_vector_type(4)));
 
-template <typename MT, typename OT, int BM, int BN, int WM, int WN>
+template <typename MT, typename OT, int BM, int BN, int WM, int WN, bool SPLIT = false>
 __global__ __launch_bounds__(64 * WM * WN) void mfma16_w8_kernel(const Mfma16Params p) {
   constexpr int BK = 64;
   constexpr int NW = WM * WN, NT = 64 * NW;
@@ -714,7 +717,9 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_w8_kernel(const Mfma16Par
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // ---- epilogue: acc[i][j][r] = C[m = m0+wm0+16j+lr][n = n0+wn0+16i+4lk+r]
+  // ---- epilogue: acc[i][j][r] = C[m = m0+wm0+16j+lr][n = n0+wn0+16i+4lk+r]; split rows:
+  // tiles 2j' and 2j' + 1 hold the hi and lo parts of output row (m0 + wm0) / 2 + 16j' + lr
+  static_assert(!SPLIT || (TM % 2 == 0 && (WTM % 32) == 0), "split rows pair whole 32-row groups");
   OT* c = static_cast<OT*>(p.c);
 #pragma unroll
   for (int i = 0; i < TN; ++i) {
@@ -723,12 +728,13 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_w8_kernel(const Mfma16Par
 #pragma unroll
     for (int r = 0; r < 4; ++r) sn[r] = scale_at(p.s, p.s_dt, (int64_t)min(nb + r, N - 1) * p.ld_sn);
 #pragma unroll
-    for (int j = 0; j < TM; ++j) {
-      const int m = m0 + wm0 + j * 16 + lr;
-      if (m >= M) continue;
+    for (int j = 0; j < (SPLIT ? TM / 2 : TM); ++j) {
+      const int m = SPLIT ? (m0 + wm0) / 2 + j * 16 + lr : m0 + wm0 + j * 16 + lr;
+      if (m >= (SPLIT ? p.m_out : M)) continue;
       float v[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) v[r] = acc[i][j][r] * sn[r];
+      for (int r = 0; r < 4; ++r)
+        v[r] = (SPLIT ? acc[i][2 * j][r] + acc[i][2 * j + 1][r] : acc[i][j][r]) * sn[r];
       OT* dst = c + (int64_t)m * p.ldc + nb;
       if (nb + 3 < N && (p.ldc % 4) == 0) {
         store4<OT>(dst, v[0], v[1], v[2], v[3]);
@@ -741,26 +747,26 @@ __global__ __launch_bounds__(64 * WM * WN) void mfma16_w8_kernel(const Mfma16Par
   }
 }
 
-template <typename MT, typename OT, int BN>
+template <typename MT, typename OT, int BN, bool SPLIT = false>
 static int launch_w8(Mfma16Params p, hipStream_t st) {
   p.n_tiles = (int)cdiv(p.N, BN);
   static const int gm = env_int("MLS_TILE_GM", 4);  // row tiles per run of the tile order (0: column-major)
   p.tile_gm = gm;
   const int64_t blocks = (int64_t)p.n_tiles * p.m_tiles;
-  hipLaunchKernelGGL((mfma16_w8_kernel<MT, OT, 256, BN, 2, 4>), dim3((unsigned)blocks), dim3(512), 0, st, p);
+  hipLaunchKernelGGL((mfma16_w8_kernel<MT, OT, 256, BN, 2, 4, SPLIT>), dim3((unsigned)blocks), dim3(512), 0, st, p);
   return check_launch("INT8 GEMM");
 }
 
-template <int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN, bool GROUPED>
+template <int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN, bool GROUPED, bool SPLIT = false>
 static int launch_adma(Mfma16Params p, hipStream_t st) {
   if constexpr (BKIND == B_INT8 && !GROUPED && BM == 256 && WM == 2 && WN == 4) {
     static const bool w8 = env_int("MLS_W8", 1) != 0;  // 0: the kernel above, for A/B runs
-    if (w8) return launch_w8<MT, OT, BN>(p, st);
+    if (w8) return launch_w8<MT, OT, BN, SPLIT>(p, st);
 
   }
   p.n_tiles = (int)cdiv(p.N, BN);
   const size_t lds = (size_t)2 * (BM + BN) * 8 * 16 + (BKIND == B_INT4 ? (size_t)2 * 2 * BN * 4 : 0);
-  auto kern = mfma16_adma_kernel<BKIND, MT, OT, BM, BN, WM, WN, GROUPED>;
+  auto kern = mfma16_adma_kernel<BKIND, MT, OT, BM, BN, WM, WN, GROUPED, SPLIT>;
   static bool attr_set = false;
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -897,6 +903,32 @@ int launch_gemm_wq_mfma(int wbits, const WqArgs& w) {
   }
   return w.a_dt == MLS_BF16 ? dense16<A_RAW16, B_INT8, __bf16, __bf16>(p, w.stream)
                             : dense16<A_RAW16, B_INT8, _Float16, _Float16>(p, w.stream);
+}
+
+// The engine on split rows (fp32 activations as bf16 hi + lo, split.hip): w.a is the
+// [split_rows(m_out)][lda] bf16 split matrix, w.M its row count, the output fp32 [m_out][ldc].
+// 256-row tiles (INT8) or 128-row tiles; the epilogue adds each row's hi and lo products.
+int launch_gemm_wq_mfma_split(int wbits, const WqArgs& w, int64_t m_out) {
+  if (w.K % 64 != 0 || w.lda % 8 != 0 || !aligned(w.a, 16)) return MLS_ERR_UNSUPPORTED;
+  if (wbits == 4 && w.group % 32 != 0) return MLS_ERR_UNSUPPORTED;
+  if (!aligned(w.w, 16) || w.ldw % 16 != 0 || !aligned(w.c, 8)) return MLS_ERR_UNSUPPORTED;
+  if (w.M > 0x3FFFFFFF || w.N > 0x3FFFFFFF || w.K > 0x3FFFFFFF) return MLS_ERR_UNSUPPORTED;
+  if (!tile_fits(w.lda * 2, w.ldw)) return MLS_ERR_UNSUPPORTED;
+  Mfma16Params p{};
+  p.a = w.a; p.lda = w.lda; p.b = w.w; p.ldb = w.ldw;
+  p.s = w.s; p.s_dt = w.s_dt; p.ld_sn = w.ld_sn; p.ld_sg = w.ld_sg; p.group = w.group;
+  p.c = w.c; p.ldc = w.ldc; p.M = (int)w.M; p.N = (int)w.N; p.K = (int)w.K;
+  p.m_out = (int)m_out;
+  if (wbits == 8 && w.M >= 256) {
+    p.m_tiles = (int)cdiv(p.M, 256);
+    const int64_t mt = p.m_tiles;
+    const int64_t c256 = cdiv(mt * cdiv(p.N, 256), 256) * 256, c192 = cdiv(mt * cdiv(p.N, 192), 256) * 192;
+    if (c192 < c256) return launch_adma<B_INT8, __bf16, float, 256, 192, 2, 4, false, true>(p, w.stream);
+    return launch_adma<B_INT8, __bf16, float, 256, 256, 2, 4, false, true>(p, w.stream);
+  }
+  p.m_tiles = (int)cdiv(p.M, 128);
+  if (wbits == 8) return launch_adma<B_INT8, __bf16, float, 128, 256, 2, 4, false, true>(p, w.stream);
+  return launch_adma<B_INT4, __bf16, float, 128, 256, 2, 4, false, true>(p, w.stream);
 }
 
 int launch_grouped_int4(const GroupedArgs& g) {

@@ -29,6 +29,8 @@
 //
 // The weight operand is MFMA "A" and x is "B", so lane l's accumulator holds
 // C[n = 4 (l / 16) + i][m = l % 16], i = 0..3: 4 consecutive outputs of one row m.
+#include <type_traits>
+
 #include "mfma16.h"
 
 namespace mls {
@@ -61,6 +63,7 @@ struct SmallArgs {
   int ldc;
   int M, N, K;
   int m_tiles, G;  // row tiles; INT4 groups per weight row
+  int m_out;       // split rows (fp32 x as bf16 hi + lo, mfma16.h): output rows, fp32 output
 };
 
 __device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
@@ -79,9 +82,13 @@ __device__ __forceinline__ uint4 perm_x(const uint4& v) {
 // (a & m) | c with m and c in registers: one v_and_or_b32
 __device__ __forceinline__ uint32_t andor(uint32_t a, uint32_t m, uint32_t c) { return (a & m) | c; }
 
-template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64 = false>
+template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64 = false, bool SPLIT = false>
 __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
   using MM = Mfma16<AT>;
+  // split rows: 16-row tiles 2t and 2t + 1 hold the hi and lo parts of output rows
+  // m0 / 2 + 16 t .. + 15, added in the epilogue; the output is fp32
+  using OT = std::conditional_t<SPLIT, float, AT>;
+  static_assert(!SPLIT || TM % 2 == 0, "split rows pair 16-row tiles");
   constexpr bool I4 = WBITS == 4;
   static_assert(!S64 || I4, "64-k INT4 steps");
   constexpr int KS = I4 && !S64 ? 128 : 64;  // k per step
@@ -240,39 +247,51 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) red[((wave * TN + tn) * TM + tm) * 64 + lane] = acc[tn][tm];
   __syncthreads();
-  AT* c = static_cast<AT*>(p.c);
-  for (int slot = threadIdx.x; slot < TN * TM * 64; slot += 256) {
-    const int l = slot & 63, tm = (slot >> 6) % TM, tn = (slot >> 6) / TM;
-    f32x4 v = red[(tn * TM + tm) * 64 + l];
+  OT* c = static_cast<OT*>(p.c);
+  constexpr int TMO = SPLIT ? TM / 2 : TM;  // output row tiles
+  for (int slot = threadIdx.x; slot < TN * TMO * 64; slot += 256) {
+    const int l = slot & 63, to = (slot >> 6) % TMO, tn = (slot >> 6) / TMO;
+    f32x4 v;
+    int m;
+    if constexpr (SPLIT) {
+      v = red[(tn * TM + 2 * to) * 64 + l] + red[(tn * TM + 2 * to + 1) * 64 + l];
 #pragma unroll
-    for (int ww = 1; ww < 4; ++ww) v += red[((ww * TN + tn) * TM + tm) * 64 + l];
-    const int m = m0 + 16 * tm + (l & 15), nb = n0 + 16 * tn + 4 * (l >> 4);
-    if (m >= p.M || nb >= p.N) continue;
+      for (int ww = 1; ww < 4; ++ww)
+        v += red[((ww * TN + tn) * TM + 2 * to) * 64 + l] + red[((ww * TN + tn) * TM + 2 * to + 1) * 64 + l];
+      m = m0 / 2 + 16 * to + (l & 15);
+    } else {
+      v = red[(tn * TM + to) * 64 + l];
+#pragma unroll
+      for (int ww = 1; ww < 4; ++ww) v += red[((ww * TN + tn) * TM + to) * 64 + l];
+      m = m0 + 16 * to + (l & 15);
+    }
+    const int nb = n0 + 16 * tn + 4 * (l >> 4);
+    if (m >= (SPLIT ? p.m_out : p.M) || nb >= p.N) continue;
     if constexpr (!I4) {
       const ST* sv = static_cast<const ST*>(p.s);
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] *= to_f32(sv[min(nb + i, p.N - 1)]);
     }
-    AT* dst = c + (int64_t)m * p.ldc + nb;
-    if (nb + 3 < p.N && ((uintptr_t)dst & 7) == 0) {
-      store4<AT>(dst, v[0], v[1], v[2], v[3]);
+    OT* dst = c + (int64_t)m * p.ldc + nb;
+    if (nb + 3 < p.N && ((uintptr_t)dst & (SPLIT ? 15 : 7)) == 0) {
+      store4<OT>(dst, v[0], v[1], v[2], v[3]);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (nb + i < p.N) dst[i] = from_f32<AT>(v[i]);
+        if (nb + i < p.N) dst[i] = from_f32<OT>(v[i]);
     }
   }
 }
 
-template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64>
+template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64, bool SPLIT = false>
 int launch_small(SmallArgs a, hipStream_t st) {
   a.m_tiles = (int)cdiv(a.M, 16 * TM);
   const int64_t nt = cdiv(cdiv(a.N, 16 * TN), 8) * 8;
   const int red = 4 * TN * TM * 64 * 16;
   const int sc = WBITS == 4 ? 16 * TN * a.G * (int)sizeof(ST) + 256 * 4 : 0;  // + padding of the last dword load
   if (a.m_tiles > 65535) return MLS_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((gemm_small_kernel<WBITS, AT, ST, TM, TN, D, S64>), dim3((unsigned)nt, (unsigned)a.m_tiles), dim3(256),
-                     red > sc ? red : sc, st, a);
+  hipLaunchKernelGGL((gemm_small_kernel<WBITS, AT, ST, TM, TN, D, S64, SPLIT>), dim3((unsigned)nt, (unsigned)a.m_tiles),
+                     dim3(256), red > sc ? red : sc, st, a);
   return MLS_OK;
 }
 
@@ -286,14 +305,14 @@ double small_cost(int64_t M, int64_t N, int64_t K, int wbits, int tm, int tn) {
   return (double)cdiv(blocks, 256) * per_block;
 }
 
-template <int WBITS, typename AT, typename ST, bool S64 = false>
+template <int WBITS, typename AT, typename ST, bool S64 = false, bool SPLIT = false>
 int dispatch_small(SmallArgs a, hipStream_t st) {
   static const int force = env_int("MLS_SMALL_TILE", 0);  // TM * 10 + TN (sweeps)
-  int best_tm = 1, best_tn = 1;
+  int best_tm = SPLIT ? 2 : 1, best_tn = 1;
   double best = 1e300;
-  for (int tm = 1; tm <= 4; tm *= 2)
+  for (int tm = SPLIT ? 2 : 1; tm <= 4; tm *= 2)
     for (int tn = 1; tn <= 4; tn *= 2) {
-      if (tm > 1 && a.M <= 16 * tm / 2) continue;  // a row tile mostly past M
+      if (tm > (SPLIT ? 2 : 1) && a.M <= 16 * tm / 2) continue;  // a row tile mostly past M
       if (WBITS == 4 && tm * tn > 8) continue;      // INT4 4 x 4 would spill registers
       const double c = small_cost(a.M, a.N, a.K, WBITS, tm, tn);
       if (c < best * 0.999) {
@@ -302,14 +321,16 @@ int dispatch_small(SmallArgs a, hipStream_t st) {
         best_tn = tn;
       }
     }
-  if (force) {
+  if (force && (!SPLIT || force / 10 >= 2)) {
     best_tm = force / 10;
     best_tn = force % 10;
   }
   // ring depth 2: deeper rings (up to 8 steps in flight) measured slower at M = 4..128
 #define MLS_SMALL(TM_, TN_) \
-  if (best_tm == TM_ && best_tn == TN_) return launch_small<WBITS, AT, ST, TM_, TN_, 2, S64>(a, st)
-  MLS_SMALL(1, 1); MLS_SMALL(1, 2); MLS_SMALL(1, 4);
+  if (best_tm == TM_ && best_tn == TN_) return launch_small<WBITS, AT, ST, TM_, TN_, 2, S64, SPLIT>(a, st)
+  if constexpr (!SPLIT) {
+    MLS_SMALL(1, 1); MLS_SMALL(1, 2); MLS_SMALL(1, 4);
+  }
   MLS_SMALL(2, 1); MLS_SMALL(2, 2); MLS_SMALL(2, 4);
   MLS_SMALL(4, 1); MLS_SMALL(4, 2);
   if constexpr (WBITS == 8) MLS_SMALL(4, 4);
@@ -319,8 +340,11 @@ int dispatch_small(SmallArgs a, hipStream_t st) {
 
 }  // namespace
 
-int launch_gemm_small(int wbits, const WqArgs& p) {
+// m_out > 0: p.a holds split rows (bf16 hi + lo of fp32 activations, mfma16.h), p.M of
+// them; the output is fp32 with m_out rows.
+static int small_impl(int wbits, const WqArgs& p, int64_t m_out) {
   if (p.a_dt != MLS_BF16 && p.a_dt != MLS_F16) return MLS_ERR_UNSUPPORTED;
+  if (m_out > 0 && (p.a_dt != MLS_BF16 || p.M % 32 != 0)) return MLS_ERR_UNSUPPORTED;
   // INT4 steps of 128 k (groups a multiple of 128) or of 64 k (groups of 64)
   const bool s64 = wbits == 4 && p.group % 128 != 0;
   const int KS = wbits == 4 && !s64 ? 128 : 64;
@@ -334,6 +358,7 @@ int launch_gemm_small(int wbits, const WqArgs& p) {
   a.w = p.w; a.ldw = (int)p.ldw; a.w_bytes = (int)(p.N * p.ldw);
   a.s = p.s; a.ld_sn = (int)p.ld_sn; a.ld_sg = (int)p.ld_sg; a.group = p.group;
   a.c = p.c; a.ldc = (int)p.ldc; a.M = (int)p.M; a.N = (int)p.N; a.K = (int)p.K;
+  a.m_out = (int)m_out;
   const int ssz = p.s_dt == MLS_F16 ? 2 : 4;
   if (wbits == 4) {
     a.G = (int)(p.K / p.group);
@@ -345,6 +370,14 @@ int launch_gemm_small(int wbits, const WqArgs& p) {
     // the descriptor spans the scales that exist: row N - 1 starts at (N - 1) ld_sn and
     // holds G groups (ld_sn may be below G, e.g. 0 for one row broadcast to every n)
     a.s_bytes = (int)(((p.N - 1) * p.ld_sn + a.G) * ssz);
+  }
+  if (m_out > 0) {
+    if (wbits == 4 && s64) return p.s_dt == MLS_F16 ? dispatch_small<4, __bf16, _Float16, true, true>(a, p.stream)
+                                                    : dispatch_small<4, __bf16, float, true, true>(a, p.stream);
+    if (wbits == 4) return p.s_dt == MLS_F16 ? dispatch_small<4, __bf16, _Float16, false, true>(a, p.stream)
+                                             : dispatch_small<4, __bf16, float, false, true>(a, p.stream);
+    return p.s_dt == MLS_F16 ? dispatch_small<8, __bf16, _Float16, false, true>(a, p.stream)
+                             : dispatch_small<8, __bf16, float, false, true>(a, p.stream);
   }
   if (wbits == 4 && s64) {
     if (p.a_dt == MLS_BF16) return p.s_dt == MLS_F16 ? dispatch_small<4, __bf16, _Float16, true>(a, p.stream)
@@ -362,6 +395,12 @@ int launch_gemm_small(int wbits, const WqArgs& p) {
                                                    : dispatch_small<8, __bf16, float>(a, p.stream);
   return p.s_dt == MLS_F16 ? dispatch_small<8, _Float16, _Float16>(a, p.stream)
                            : dispatch_small<8, _Float16, float>(a, p.stream);
+}
+
+int launch_gemm_small(int wbits, const WqArgs& p) { return small_impl(wbits, p, 0); }
+
+int launch_gemm_small_split(int wbits, const WqArgs& p, int64_t m_out) {
+  return m_out > 0 ? small_impl(wbits, p, m_out) : MLS_ERR_UNSUPPORTED;
 }
 
 }  // namespace mls

@@ -37,7 +37,29 @@ struct Mfma16Params {
   const int32_t* a_rows;          // grouped: sorted row m is row a_rows[m] of a (null: row m)
   int a_src_rows;                 // grouped: rows of a when a_rows is set
   int tile_gm;                    // dense: row tiles per run of the tile order (0: column-major)
+  int m_out;                      // split rows (fp32 activations as bf16 hi + lo, split.hip): rows of
+                                  // the output; a's M rows hold the hi and lo parts (0: not split)
 };
+
+// fp32 activations on the 16-bit matrix cores (split.hip): x = hi + lo, two bf16 rows per
+// row of x, arranged so that row R of the split matrix is part (R >> 4) & 1 (0: hi, 1: lo)
+// of row m = 16 (R >> 5) + (R & 15). A kernel whose 16-row MFMA tiles start at multiples of
+// 32 then holds the hi and lo products of one output row in the same lane, in the
+// accumulators of tiles 2j and 2j + 1, and adds them in its epilogue (fp32).
+__host__ __device__ constexpr int split_row(int m, int part) { return 32 * (m >> 4) + 16 * part + (m & 15); }
+inline int64_t split_rows(int64_t M) { return 32 * cdiv(M, 16); }
+
+// x = hi + lo: hi = x truncated to bf16 (exact; never overflows), lo = x - hi (exact in
+// fp32, below 2^-7 |x|), rounded to bf16 by the caller; non-finite x: hi = x (a NaN stays
+// a quiet NaN), lo = 0.
+__device__ __forceinline__ void split_f32(float x, float& hi, float& lo) {
+  const uint32_t u = __float_as_uint(x);
+  const bool nonfinite = (u & 0x7F800000u) == 0x7F800000u;
+  // a NaN whose payload lies only in the low 16 bits stays a (quiet) NaN, not an infinity
+  hi = __uint_as_float((u & 0xFFFF0000u) | (nonfinite && (u & 0x007FFFFFu) ? 0x00400000u : 0u));
+  lo = nonfinite ? 0.0f : x - hi;
+}
+
 
 template <typename T> struct Mfma16;
 template <> struct Mfma16<__bf16> {

@@ -44,6 +44,17 @@ int launch_gemm_wq_mfma(int wbits, const WqArgs& p);
 // Any shape, any dtype: one thread per output element.
 int launch_gemm_wq_generic(int wbits, const WqArgs& p);
 
+// fp32 activations on the 16-bit matrix cores (split.hip, mfma16.h): p.a holds p.M split
+// rows (bf16 hi and lo parts of m_out rows of x, p.M = split_rows(m_out)); the output is
+// fp32 [m_out][ldc]. MLS_ERR_UNSUPPORTED outside the kernels' fast paths.
+int launch_gemm_small_split(int wbits, const WqArgs& p, int64_t m_out);
+int launch_gemm_wq_mfma_split(int wbits, const WqArgs& p, int64_t m_out);
+// x fp32 [M][ldx] -> split rows [split_rows(M)][K] bf16 (zeros for rows past M).
+int launch_split_rows(const float* x, int64_t ldx, int64_t M, int64_t K, void* x2, hipStream_t st);
+// The GEMM of split rows q.a ([q.M][q.lda] bf16, q.M = split_rows(m_out)) into fp32 q.c:
+// the medium GEMM where the engine would have few tiles, else the engine.
+int launch_split_gemm(int wbits, const WqArgs& q, int64_t m_out);
+
 // Per-expert INT4 GEMM over expert-sorted row segments (MFMA).
 struct GroupedArgs {
   WqArgs base;            // base.M = total rows; base.w/base.s point at expert 0

@@ -2,6 +2,7 @@
 // then dispatch by shape: the VALU decode GEMV for small M (and fp32
 // activations), the MFMA tiled GEMM for larger M with 16-bit activations, and a
 // one-thread-per-output kernel for shapes neither fast path covers.
+#include "mfma16.h"
 #include "wq.h"
 
 using namespace mls;
@@ -73,7 +74,92 @@ int run(const char* fn, int wbits, const WqArgs& p) {
   return check_launch(fn);
 }
 
+// fp32 activations with M > 16 on the 16-bit matrix cores (split.hip): x is split into
+// bf16 hi and lo rows in the workspace, then the medium GEMM (few engine tiles) or the
+// engine multiplies both and adds them in its epilogue. Taken only where the engine is
+// sure to accept the split rows, so the split pass never runs for nothing.
+bool split_ok(int wbits, const WqArgs& p) {
+  static const bool enabled = env_int("MLS_SPLIT", 1) != 0;  // 0: the VALU GEMV (A/B runs)
+  if (!enabled || p.a_dt != MLS_F32 || p.M <= 16 || p.M > 0x3FFFFFFF || p.K < 64 || p.K % 64 != 0) return false;
+  if (!aligned(p.w, 16) || p.ldw % 16 != 0 || !aligned(p.c, 8)) return false;
+  if (wbits == 4 && p.group % 64 != 0) return false;
+  const int64_t m2 = split_rows(p.M);
+  return m2 <= 0x3FFFFFFF && p.N <= 0x3FFFFFFF && p.K <= 0x3FFFFFFF && p.K * 2 * 256 < (1ll << 31) &&
+         p.ldw * 256 < (1ll << 31);
+}
+
+int64_t split_ws_bytes(const WqArgs& p) { return split_rows(p.M) * p.K * 2; }
+
+int run_split(const char* fn, int wbits, const WqArgs& p, void* ws) {
+  int rc = launch_split_rows(static_cast<const float*>(p.a), p.lda, p.M, p.K, ws, p.stream);
+  if (rc != MLS_OK) return rc;
+  WqArgs q = p;
+  q.a = ws;
+  q.a_dt = MLS_BF16;
+  q.lda = p.K;
+  q.M = split_rows(p.M);
+  rc = launch_split_gemm(wbits, q, p.M);
+  if (rc == MLS_ERR_UNSUPPORTED) return fail(MLS_ERR_HIP, "%s: split rows written but no split GEMM took them", fn);
+  if (rc != MLS_OK) return rc;
+  return check_launch(fn);
+}
+
+int run_ws(const char* fn, int wbits, const WqArgs& p, void* ws, int64_t ws_bytes) {
+  if (p.M == 0 || p.N == 0 || !split_ok(wbits, p)) return run(fn, wbits, p);
+  const int64_t need = split_ws_bytes(p);
+  if (!ws || ws_bytes < need || !aligned(ws, 256))
+    return fail(MLS_ERR_ARG, "%s: workspace of %lld bytes at %p (need %lld, 256-byte aligned)", fn,
+                (long long)ws_bytes, ws, (long long)need);
+  return run_split(fn, wbits, p, ws);
+}
+
 }  // namespace
+
+namespace mls {
+
+// The medium GEMM where the engine would have few tiles (as use_small, on the split rows),
+// else the engine.
+int launch_split_gemm(int wbits, const WqArgs& q, int64_t m_out) {
+  const int64_t eng_bm = wbits == 8 && q.M >= 256 ? 256 : 128;
+  int rc = MLS_ERR_UNSUPPORTED;
+  if (q.M <= 512 && cdiv(q.M, eng_bm) * cdiv(q.N, 256) < 128) rc = launch_gemm_small_split(wbits, q, m_out);
+  if (rc == MLS_ERR_UNSUPPORTED) rc = launch_gemm_wq_mfma_split(wbits, q, m_out);
+  return rc;
+}
+
+}  // namespace mls
+
+extern "C" int64_t mls_wq_gemm_workspace(int wbits, int64_t M, int64_t N, int64_t K, int a_dt, int group) {
+  if ((wbits != 4 && wbits != 8) || M <= 0 || N <= 0 || K <= 0) return 0;
+  // the checks of split_ok that do not depend on pointers or strides (those can only turn
+  // the split off, and then no workspace is used)
+  WqArgs p{};
+  p.a_dt = a_dt; p.M = M; p.N = N; p.K = K; p.group = wbits == 4 ? group : 0;
+  if (a_dt != MLS_F32 || M <= 16 || K < 64 || K % 64 != 0 || (wbits == 4 && (group < 1 || group % 64 != 0))) return 0;
+  if (M > 0x3FFFFFFF || split_rows(M) > 0x3FFFFFFF || N > 0x3FFFFFFF || K > 0x3FFFFFFF || K * 2 * 256 >= (1ll << 31))
+    return 0;
+  return split_ws_bytes(p);
+}
+
+extern "C" int mls_int8_gemm_ws(const void* a, int a_dt, int64_t lda, const int8_t* w, int64_t ldw, const void* s,
+                                int s_dt, void* c, int c_dt, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                void* workspace, int64_t ws_bytes, mls_stream_t stream) {
+  WqArgs p{a, a_dt, lda, reinterpret_cast<const uint8_t*>(w), ldw, s, s_dt, 1, 0, 0,
+           c, ldc, M, N, K, (hipStream_t)stream};
+  int rc = validate("mls_int8_gemm_ws", 8, p, c_dt);
+  if (rc != MLS_OK) return rc;
+  return run_ws("mls_int8_gemm_ws", 8, p, workspace, ws_bytes);
+}
+
+extern "C" int mls_int4_gemm_ws(const void* a, int a_dt, int64_t lda, const uint8_t* w, int64_t ldw, const void* s,
+                                int s_dt, int64_t ld_sn, int64_t ld_sg, int group, void* c, int c_dt, int64_t ldc,
+                                int64_t M, int64_t N, int64_t K, void* workspace, int64_t ws_bytes,
+                                mls_stream_t stream) {
+  WqArgs p{a, a_dt, lda, w, ldw, s, s_dt, ld_sn, ld_sg, group, c, ldc, M, N, K, (hipStream_t)stream};
+  int rc = validate("mls_int4_gemm_ws", 4, p, c_dt);
+  if (rc != MLS_OK) return rc;
+  return run_ws("mls_int4_gemm_ws", 4, p, workspace, ws_bytes);
+}
 
 extern "C" int mls_int8_gemm(const void* a, int a_dt, int64_t lda, const int8_t* w, int64_t ldw,
                              const void* s, int s_dt, void* c, int c_dt, int64_t ldc, int64_t M,

@@ -68,6 +68,10 @@ SIGNATURES = {
     "mls_int8_gemm": ([_P, _I, _I64, _P, _I64, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P], _I),
     "mls_int4_gemm": ([_P, _I, _I64, _P, _I64, _P, _I, _I64, _I64, _I, _P, _I, _I64,
                        _I64, _I64, _I64, _P], _I),
+    "mls_wq_gemm_workspace": ([_I, _I64, _I64, _I64, _I, _I], _I64),
+    "mls_int8_gemm_ws": ([_P, _I, _I64, _P, _I64, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P], _I),
+    "mls_int4_gemm_ws": ([_P, _I, _I64, _P, _I64, _P, _I, _I64, _I64, _I, _P, _I, _I64,
+                          _I64, _I64, _I64, _P, _I64, _P], _I),
     "mls_int8_dgrad": ([_P, _I, _I64, _P, _I64, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P], _I),
     "mls_int8_dgrad_workspace": ([_I64, _I64, _I64, _I], _I64),
     "mls_int8_dgrad_ws": ([_P, _I, _I64, _P, _I64, _P, _I, _P, _I, _I64, _I64, _I64, _I64, _P, _I64, _P],

@@ -11,7 +11,9 @@ INT4: w_packed [N, K/2] uint8, two nibbles per byte (even k in the low nibble),
 The work runs in libmls_hip.so on gfx950 (include/mls.h): a decode GEMV that
 streams the packed weights with 16-byte loads for small M, and an MFMA GEMM that
 dequantizes weight tiles into LDS for larger M. The library picks the kernel
-from the shape. Outputs have a.dtype; scales may be fp32 or fp16 (other float
+from the shape. fp32 activations with M > 16 (the reference's fp32 engine) run on
+the bf16 matrix cores as hi + lo parts, x split into a workspace taken from torch's
+caching allocator. Outputs have a.dtype; scales may be fp32 or fp16 (other float
 dtypes are converted to fp32, as the reference does for every scale).
 """
 
@@ -39,9 +41,14 @@ def int8_matmul(a: torch.Tensor, w_q: torch.Tensor, scale: torch.Tensor):
     a, w_q = rows(a), rows(w_q)
     s, sdt = scale_vector(scale.reshape(-1).contiguous())
     c = torch.empty(M, N, dtype=a.dtype, device=dev)
-    kernels.check(kernels.lib().mls_int8_gemm(
+    lib = kernels.lib()
+    # fp32 activations with M > 16 run on the matrix cores as bf16 hi + lo parts, split
+    # into a workspace from torch's caching allocator; other calls need none
+    need = lib.mls_wq_gemm_workspace(8, M, N, K, adt, 0)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
+    kernels.check(lib.mls_int8_gemm_ws(
         a.data_ptr(), adt, ld(a), w_q.data_ptr(), ld(w_q), s.data_ptr(), sdt,
-        c.data_ptr(), adt, ld(c), M, N, K, stream(dev)), "int8_matmul")
+        c.data_ptr(), adt, ld(c), M, N, K, ws.data_ptr() if need else None, need, stream(dev)), "int8_matmul")
     return c
 
 
@@ -90,8 +97,11 @@ def int4_matmul(a: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor,
         scale = scale.to(torch.float32)
     sdt = dt_code(scale.dtype, "int4_matmul scale")
     c = torch.empty(M, N, dtype=a.dtype, device=dev)
-    kernels.check(kernels.lib().mls_int4_gemm(
+    lib = kernels.lib()
+    need = lib.mls_wq_gemm_workspace(4, M, N, K, adt, group_size)
+    ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None
+    kernels.check(lib.mls_int4_gemm_ws(
         a.data_ptr(), adt, ld(a), w_packed.data_ptr(), ld(w_packed),
         scale.data_ptr(), sdt, scale.stride(0), scale.stride(1), group_size,
-        c.data_ptr(), adt, ld(c), M, N, K, stream(dev)), "int4_matmul")
+        c.data_ptr(), adt, ld(c), M, N, K, ws.data_ptr() if need else None, need, stream(dev)), "int4_matmul")
     return c

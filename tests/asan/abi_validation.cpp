@@ -32,6 +32,9 @@ int launch_grouped_int4_partial(const GroupedArgs&, int, float*, int64_t, int64_
   reached("launch_grouped_int4_partial");
 }
 int grouped_splits(int64_t, int, int64_t, int64_t, int) { return 1; }
+int launch_gemm_small_split(int, const WqArgs&, int64_t) { reached("launch_gemm_small_split"); }
+int launch_gemm_wq_mfma_split(int, const WqArgs&, int64_t) { reached("launch_gemm_wq_mfma_split"); }
+int launch_split_rows(const float*, int64_t, int64_t, int64_t, void*, hipStream_t) { reached("launch_split_rows"); }
 }  // namespace mls
 
 namespace {
@@ -94,6 +97,39 @@ void int4_gemm_cases() {
   expect("int4 huge", call(2, 1, 32, BIG, BIG, 64), MLS_ERR_ARG);
 }
 
+void workspace_cases() {
+  // fp32 activations with M > 16 take the split route: the workspace is checked first
+  void* c = const_cast<void*>(P(3));
+  const int64_t need = mls_wq_gemm_workspace(8, 64, 32, 64, F32, 0);
+  if (need != 128 * 64 * 2) {
+    std::fprintf(stderr, "FAIL workspace size %lld\n", (long long)need);
+    ++failures;
+  }
+  auto w8 = [&](void* ws, int64_t bytes, int64_t M) {
+    return mls_int8_gemm_ws(P(0), F32, 64, PT<int8_t>(1), 64, P(2), F32, c, F32, 32, M, 32, 64, ws, bytes, nullptr);
+  };
+  void* ws = const_cast<void*>(P(15));  // 0x10000: 256-byte aligned
+  expect("int8 ws null", w8(nullptr, need, 64), MLS_ERR_ARG, "workspace");
+  expect("int8 ws short", w8(ws, need - 1, 64), MLS_ERR_ARG, "workspace");
+  expect("int8 ws misaligned", w8(static_cast<char*>(ws) + 16, need, 64), MLS_ERR_ARG, "aligned");
+  expect("int8 ws negative M", w8(ws, need, -1), MLS_ERR_ARG, "negative");
+  expect("int8 ws empty M", w8(nullptr, 0, 0), MLS_OK);
+  expect("int8 ws huge", mls_int8_gemm_ws(P(0), F32, BIG, PT<int8_t>(1), BIG, P(2), F32, c, F32, BIG, BIG, BIG, BIG,
+                                          ws, need, nullptr),
+         MLS_ERR_UNSUPPORTED, "too large");
+  expect("int4 ws null", mls_int4_gemm_ws(P(0), F32, 64, PT<uint8_t>(1), 32, P(2), F16, 1, 1, 64, c, F32, 32, 64, 32,
+                                          64, nullptr, 0, nullptr),
+         MLS_ERR_ARG, "workspace");
+  expect("int4 ws group", mls_int4_gemm_ws(P(0), F32, 64, PT<uint8_t>(1), 32, P(2), F16, 1, 1, 48, c, F32, 32, 64, 32,
+                                           64, ws, need, nullptr),
+         MLS_ERR_ARG, "group");
+  if (mls_wq_gemm_workspace(8, 16, 32, 64, F32, 0) != 0 || mls_wq_gemm_workspace(4, 64, 32, 64, F32, 32) != 0 ||
+      mls_wq_gemm_workspace(8, 64, 32, 64, BF, 0) != 0 || mls_wq_gemm_workspace(8, INT64_MAX, 32, 64, F32, 0) != 0) {
+    std::fprintf(stderr, "FAIL workspace query outside the split route\n");
+    ++failures;
+  }
+}
+
 void grouped_cases() {
   const int32_t* off = PT<int32_t>(4);
   const int32_t* rows = PT<int32_t>(5);
@@ -148,6 +184,7 @@ int main() {
   }
   int8_gemm_cases();
   int4_gemm_cases();
+  workspace_cases();
   grouped_cases();
   // a long message is truncated, not overrun
   char name[600];

@@ -24,7 +24,7 @@ def declared_symbols() -> list[str]:
 
 def test_header_declares_the_boundary():
     syms = declared_symbols()
-    assert len(syms) == len(set(syms)) == 27
+    assert len(syms) == len(set(syms)) == 30
     assert set(syms) == set(kernels.SIGNATURES)
 
 
@@ -124,9 +124,10 @@ def test_grouped_reject_empty_k():
 
 
 def test_dgrad_workspace_and_rejects():
-    """The matrix-core dgrad's workspace: scaled dy [M][Np] 16-bit + transposed weights
-    [K][Np] bytes + K fp32 ones, Np = N rounded up to 64, each part 256-byte aligned; 0 for
-    fp32 dy (the VALU route). A short or misaligned workspace is rejected on the host."""
+    """The matrix-core dgrad's workspace: scaled dy [M][Np] 16-bit (fp32 dy: its bf16 hi and
+    lo rows, 32 per 16 rows of dy) + transposed weights [K][Np] bytes + K fp32 ones, Np = N
+    rounded up to 64, each part 256-byte aligned; 0 for fp32 dy with M <= 16 (the VALU
+    route). A short or misaligned workspace is rejected on the host."""
     L = kernels.load_library()
     bf = kernels.MLS_BF16
     M, N, K = 40, 100, 72
@@ -134,7 +135,8 @@ def test_dgrad_workspace_and_rejects():
     up = lambda b: -(-b // 256) * 256
     assert L.mls_int8_dgrad_workspace(M, N, K, bf) == up(M * Np * 2) + up(K * Np) + up(K * 4)
     assert L.mls_int8_dgrad_workspace(M, N, K, kernels.MLS_F16) == up(M * Np * 2) + up(K * Np) + up(K * 4)
-    assert L.mls_int8_dgrad_workspace(M, N, K, kernels.MLS_F32) == 0
+    assert L.mls_int8_dgrad_workspace(M, N, K, kernels.MLS_F32) == up(96 * Np * 2) + up(K * Np) + up(K * 4)
+    assert L.mls_int8_dgrad_workspace(16, N, K, kernels.MLS_F32) == 0
     assert L.mls_int8_dgrad_workspace(0, N, K, bf) == 0
     need = L.mls_int8_dgrad_workspace(M, N, K, bf)
     args = (1, bf, N, 1, K, 1, kernels.MLS_F32, 1, bf, K, M, N, K)
