@@ -1083,6 +1083,66 @@ def ref_shape_rows(dev, steps: int, warmup: int):
     return out
 
 
+def unquantized_rows(dev, steps: int, warmup: int):
+    """The reference's own comparison points (bench/bench_quantize.py:44-68, published in
+    bench/results/quantize.json): the unquantized GEMM a @ W^T (fp16, through torch: the
+    vendor library) and the anti-pattern that dequantizes all of W and then multiplies
+    (serve/quantize.py:24-25, 94), at its shapes (N = K = 2048, M in {1, 16, 128}, fp16), and
+    the unquantized bf16 GEMM at the headline's shape (M = 1, K = N = 4096). Same protocol
+    as the fused rows (graph replay over >= 1 GiB of rotated weight copies; torch's calls
+    captured like this build's), plus the reference's own (median host wall time of a call
+    and a synchronize, bench/_util.py:36-51). Calibration only: the vendor library and
+    torch's elementwise kernels, not this build's."""
+    import torch
+    from serve.quantize import dequantize_int8, quantize_int8
+    out = []
+    shapes = [(M, 2048, 2048, torch.float16, f"m{M}_2048x2048_fp16") for M in (1, 16, 128)]
+    shapes.append((1, 4096, 4096, torch.bfloat16, "m1_4096x4096_bf16"))
+    for M, N, K, dt, tag in shapes:
+        g = torch.Generator(device=dev).manual_seed(60 + M + N)
+        a = torch.randn(M, K, generator=g, device=dev).to(dt)
+        w = torch.randn(N, K, generator=g, device=dev)
+        wfp = w.to(dt)
+        copies = max(2, -(-ROTATE_BYTES // (N * K * 2)))
+        ws = [wfp] + [wfp.clone() for _ in range(copies - 1)]
+        impls = {"fp_matmul": (lambda i: a @ ws[i].t(), N * K * 2 + (M * K + M * N) * 2)}
+        if dt == torch.float16:
+            q8, s8 = quantize_int8(w)
+            q8s = [q8] + [q8.clone() for _ in range(max(2, -(-ROTATE_BYTES // (N * K))) - 1)]
+            impls["dequant_then_matmul_int8"] = (
+                lambda i: a @ dequantize_int8(q8s[i % len(q8s)], s8).to(dt).t(), N * K + N * 4 + (M * K + M * N) * 2)
+        for impl, (fn, nbytes) in impls.items():
+            n = copies if impl == "fp_matmul" else len(q8s)
+            fns = [lambda i=i: fn(i) for i in range(n)]
+            try:
+                ms = time_steps(fns, warmup, steps)
+                how = "graph"
+            except Exception as ex:  # a library call that cannot be captured: eager launches
+                log(f"{impl} {tag}: graph capture failed ({type(ex).__name__}); timing eager launches")
+                torch.cuda.synchronize()
+                for i in range(warmup):
+                    fns[i % n]()
+                st, en = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                st.record()
+                for i in range(steps):
+                    fns[(warmup + i) % n]()
+                en.record()
+                torch.cuda.synchronize()
+                ms = st.elapsed_time(en) / steps
+                how = "eager"
+            row = {"name": f"unquantized_{impl}_{tag}", "ms_per_step": round(ms, 6),
+                   "TB/s": round(nbytes / (ms * 1e-3) / 1e12, 4),
+                   "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                                "unit": "GB/s", "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+                   "bytes_per_step": nbytes, "launch": how,
+                   "ms_reference_protocol": round(wall_median_ms(fns[0]), 4),
+                   "calibration": "torch / the vendor library, not this build's kernels"}
+            out.append(row)
+        del ws
+    return out
+
+
 def load_traffic(name: str):
     """HBM bytes per launch measured with rocprofv3 --pmc (profiles/traffic.json), if any."""
     f = ROOT / TRAFFIC_FILE
@@ -1102,7 +1162,8 @@ def main(argv=None) -> int:
     ap.add_argument("--only", default=None,
                     help="run one workload: int4_gemv, int4_m4, int4_m16, int8_gemv, int8_prefill, "
                          "fp8_gemm, fp8_native, fp8_bwd, fp8_bwd_native, moe_int4, moe_mlp_int4, paged_attn, "
-                         "quantize_int4, ref_shapes, fp32 (fp32 activations), clocks (M=1 step split), "
+                         "quantize_int4, ref_shapes, unquantized (the reference's fp16 / dequantize-then-matmul "
+                         "comparison rows), fp32 (fp32 activations), clocks (M=1 step split), "
                          "copy (counter calibration), vendor_fp8_rowwise / vendor_fp8_tensorwise / "
                          "vendor_bf16 (hipBLASLt calibration), cpu (the CPU baseline alone)")
     ap.add_argument("--no-extra", action="store_true")
@@ -1175,6 +1236,7 @@ def main(argv=None) -> int:
         "cpu": lambda: cpu_baseline(),
         "clocks": lambda: clock_rows(dev, args.steps, args.warmup),
         "fp32": lambda: fp32_rows(dev, args.steps, args.warmup),
+        "unquantized": lambda: unquantized_rows(dev, max(64, args.steps // 4), 16),
     }
     for kind, peak in (("fp8_rowwise", FP8_PEAK_TFLOPS), ("fp8_tensorwise", FP8_PEAK_TFLOPS),
                        ("bf16", BF16_PEAK_TFLOPS)):
@@ -1202,7 +1264,7 @@ def main(argv=None) -> int:
         for k in ("int4_m2", "int4_m4", "int4_m16", "int8_gemv", "int8_m2", "int8_prefill", "fp32", "int8_dgrad",
                   "fp8_gemm", "fp8_native",
                   "fp8_bwd", "fp8_bwd_native", "moe_int4", "moe_mlp_int4", "paged_attn", "quantize_int4",
-                  "ref_shapes", "copy", "floor", "clocks", "vendor_fp8_rowwise", "vendor_fp8_tensorwise",
+                  "ref_shapes", "unquantized", "copy", "floor", "clocks", "vendor_fp8_rowwise", "vendor_fp8_tensorwise",
                   "vendor_bf16"):
             log(f"{k} ...")
             row = runners[k]()
