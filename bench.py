@@ -419,7 +419,7 @@ def fp32_rows(dev, steps: int, warmup: int):
     """fp32 activations at the reference engine's call shapes (its serving path runs fp32
     end to end, serve/engine.py:166): M = 1 / 5 (decode of one / five sequences), 64 (a
     prefill chunk), 2048 (a long prompt), K = N = 4096, INT4 g128 and INT8 with fp16
-    scales; and config C's INT8 prefill (2048 x 11008 x 4096) in fp32. M <= 16 runs the
+    scales; and config C's INT8 prefill (2048 x 11008 x 4096) in fp32. M = 1 runs the
     VALU GEMV, larger M the bf16 hi + lo split on the matrix cores."""
     import torch
     out = []
@@ -433,7 +433,8 @@ def fp32_rows(dev, steps: int, warmup: int):
             row = _mfma_row(name, r, BF16_PEAK_TFLOPS) if M >= 2048 else _hbm_row(name, r)
             if row.get("ms_per_step") is not None and M >= 2048:
                 row["hbm_frac"] = round(r["bytes"] / (r["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
-            row["path"] = "VALU GEMV (fp32 FMAs)" if M <= 16 else "bf16 hi + lo split, bf16 MFMA"
+            row["path"] = ("VALU GEMV (fp32 FMAs)" if M == 1 else
+                           "bf16 hi + lo split, skinny MFMA GEMV" if M <= 16 else "bf16 hi + lo split, bf16 MFMA")
             out.append(row)
     r = int8_prefill(dev, small, 4, act=torch.float32)
     row = _mfma_row("fp32_int8_prefill_2048x11008x4096", r, BF16_PEAK_TFLOPS,

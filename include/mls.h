@@ -138,8 +138,8 @@ int mls_int4_gemm(const void* a, int a_dt, int64_t lda,
                   int64_t M, int64_t N, int64_t K, mls_stream_t stream);
 
 /* The same two GEMMs (kernels/dequant_matmul.py:39-100, 140-185) with a caller workspace,
- * for fp32 activations on the matrix cores: with a_dt = F32 and M > 16 (and K % 64 == 0,
- * 16-byte aligned weight rows, an 8-byte aligned c, INT4 groups a multiple of 64) x is
+ * for fp32 activations on the matrix cores: with a_dt = F32 and M >= 2 (and K % 64 == 0,
+ * 16-byte aligned weight rows, a 16-byte aligned c, INT4 groups a multiple of 64) x is
  * split into bf16 hi and lo parts (hi = x truncated to bf16, lo = bf16(x - hi): x to about
  * 2^-16 of its magnitude) in the workspace, and both are multiplied on the bf16 MFMA with
  * fp32 accumulation and added in fp32; every other call runs as mls_int8_gemm /

@@ -82,8 +82,8 @@ __device__ __forceinline__ uint4 perm_x(const uint4& v) {
 // (a & m) | c with m and c in registers: one v_and_or_b32
 __device__ __forceinline__ uint32_t andor(uint32_t a, uint32_t m, uint32_t c) { return (a & m) | c; }
 
-template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64 = false, bool SPLIT = false>
-__global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
+template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64 = false, bool SPLIT = false, int WV = 4>
+__global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) {
   using MM = Mfma16<AT>;
   // split rows: 16-row tiles 2t and 2t + 1 hold the hi and lo parts of output rows
   // m0 / 2 + 16 t .. + 15, added in the epilogue; the output is fp32
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
   const int m0 = mt * 16 * TM, n0 = nt * 16 * TN;
   if (n0 >= p.N) return;  // padding column tile
   const int nsteps = p.K / KS;
-  const int s_lo = nsteps * wave / 4, s_hi = nsteps * (wave + 1) / 4;
+  const int s_lo = nsteps * wave / WV, s_hi = nsteps * (wave + 1) / WV;
 
   // every argument into SGPRs at once (one round of kernel-argument loads)
   asm volatile("" ::"s"(p.a), "s"(p.lda), "s"(p.a_bytes), "s"(p.w), "s"(p.ldw), "s"(p.w_bytes), "s"(p.s),
@@ -159,7 +159,7 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
     const __amdgpu_buffer_rsrc_t rss = __builtin_amdgcn_make_buffer_rsrc((void*)p.s, (short)0, p.s_bytes, 0x00020000);
     const int dw_row = p.G * (int)sizeof(ST) / 4;  // dwords per row (G * sizeof(ST) % 4 == 0)
     const float inv2 = 0.5f / (float)dw_row;
-    for (int q0 = wave * 64; q0 < BN * dw_row; q0 += 256) {
+    for (int q0 = wave * 64; q0 < BN * dw_row; q0 += 64 * WV) {
       const int d = min(q0 + lane, BN * dw_row - 1);
       const int r = (int)((float)(2 * d + 1) * inv2);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rss, (__attribute__((address_space(3))) void*)(smem + q0 * 4), 4,
@@ -239,9 +239,9 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
     }
   }
 
-  // ---- the 4 partial tiles meet in LDS; each thread finishes TN * TM / 4 accumulators
+  // ---- the WV partial tiles meet in LDS; each thread finishes TN * TM / WV accumulators
   __syncthreads();  // (INT4: every wavefront is done with the scale table the buffer reuses)
-  f32x4* red = reinterpret_cast<f32x4*>(smem);  // [4][TN][TM][64]
+  f32x4* red = reinterpret_cast<f32x4*>(smem);  // [WV][TN][TM][64]
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
@@ -249,20 +249,20 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
   __syncthreads();
   OT* c = static_cast<OT*>(p.c);
   constexpr int TMO = SPLIT ? TM / 2 : TM;  // output row tiles
-  for (int slot = threadIdx.x; slot < TN * TMO * 64; slot += 256) {
+  for (int slot = threadIdx.x; slot < TN * TMO * 64; slot += 64 * WV) {
     const int l = slot & 63, to = (slot >> 6) % TMO, tn = (slot >> 6) / TMO;
     f32x4 v;
     int m;
     if constexpr (SPLIT) {
       v = red[(tn * TM + 2 * to) * 64 + l] + red[(tn * TM + 2 * to + 1) * 64 + l];
 #pragma unroll
-      for (int ww = 1; ww < 4; ++ww)
+      for (int ww = 1; ww < WV; ++ww)
         v += red[((ww * TN + tn) * TM + 2 * to) * 64 + l] + red[((ww * TN + tn) * TM + 2 * to + 1) * 64 + l];
       m = m0 / 2 + 16 * to + (l & 15);
     } else {
       v = red[(tn * TM + to) * 64 + l];
 #pragma unroll
-      for (int ww = 1; ww < 4; ++ww) v += red[((ww * TN + tn) * TM + to) * 64 + l];
+      for (int ww = 1; ww < WV; ++ww) v += red[((ww * TN + tn) * TM + to) * 64 + l];
       m = m0 + 16 * to + (l & 15);
     }
     const int nb = n0 + 16 * tn + 4 * (l >> 4);
@@ -283,16 +283,53 @@ __global__ __launch_bounds__(256) void gemm_small_kernel(const SmallArgs p) {
   }
 }
 
-template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64, bool SPLIT = false>
-int launch_small(SmallArgs a, hipStream_t st) {
+template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64, bool SPLIT, int WV>
+int launch_small_wv(SmallArgs a, hipStream_t st) {
   a.m_tiles = (int)cdiv(a.M, 16 * TM);
   const int64_t nt = cdiv(cdiv(a.N, 16 * TN), 8) * 8;
-  const int red = 4 * TN * TM * 64 * 16;
-  const int sc = WBITS == 4 ? 16 * TN * a.G * (int)sizeof(ST) + 256 * 4 : 0;  // + padding of the last dword load
+  const int red = WV * TN * TM * 64 * 16;
+  const int sc = WBITS == 4 ? 16 * TN * a.G * (int)sizeof(ST) + 64 * WV * 4 : 0;  // + padding of the last dword load
   if (a.m_tiles > 65535) return MLS_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((gemm_small_kernel<WBITS, AT, ST, TM, TN, D, S64, SPLIT>), dim3((unsigned)nt, (unsigned)a.m_tiles),
-                     dim3(256), red > sc ? red : sc, st, a);
+  auto kern = gemm_small_kernel<WBITS, AT, ST, TM, TN, D, S64, SPLIT, WV>;
+  const int lds = red > sc ? red : sc;
+  if (lds > 65536) {  // above the default dynamic LDS limit: raise it once per instantiation
+    static bool attr_set = false;
+    if (!attr_set) {
+      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+        return MLS_ERR_UNSUPPORTED;
+      attr_set = true;
+    }
+  }
+  hipLaunchKernelGGL(kern, dim3((unsigned)nt, (unsigned)a.m_tiles), dim3(64 * WV), lds, st, a);
   return MLS_OK;
+}
+
+// Registers per lane a (TM, TN) tile keeps live: accumulators and the ring of D steps of
+// operands (16-byte pieces: TM XP of x and TN of weights per step), 4 VGPRs each.
+template <int WBITS, int TM, int TN, int D, bool S64>
+constexpr int small_regs() {
+  constexpr int XP = WBITS == 4 && !S64 ? 4 : 2;
+  return 4 * TM * TN + 4 * D * (TM * XP + TN);
+}
+
+// Wavefronts per block: the K steps are split over them, so more wavefronts keep more
+// steps in flight per CU. 16 wavefronts (four per SIMD, 128 VGPRs a lane) hold one step
+// each in flight (D = 1: the other wavefronts of the SIMD cover the latency), 8 (256
+// VGPRs) two, 4 two. MLS_SMALL_WAVES = 4, 8 or 16 forces a count (sweeps); a count whose
+// registers or reduction buffer would not fit falls back to fewer wavefronts.
+template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64, bool SPLIT = false>
+int launch_small(SmallArgs a, hipStream_t st) {
+  static const int force = env_int("MLS_SMALL_WAVES", 0);
+  const int KS = WBITS == 4 && !S64 ? 128 : 64;
+  const int nsteps = a.K / KS;
+  int wv = nsteps >= 32 ? 16 : nsteps >= 16 ? 8 : 4;
+  if (force == 4 || force == 8 || force == 16) wv = force;
+  // (the partial tiles of all wavefronts meet in LDS: WV TN TM KiB within 128 KiB)
+  if constexpr (small_regs<WBITS, TM, TN, 1, S64>() <= 56 && 16 * TN * TM <= 128)
+    if (wv >= 16) return launch_small_wv<WBITS, AT, ST, TM, TN, 1, S64, SPLIT, 16>(a, st);
+  if constexpr (small_regs<WBITS, TM, TN, 2, S64>() <= 112 && 8 * TN * TM <= 128)
+    if (wv >= 8) return launch_small_wv<WBITS, AT, ST, TM, TN, 2, S64, SPLIT, 8>(a, st);
+  return launch_small_wv<WBITS, AT, ST, TM, TN, D, S64, SPLIT, 4>(a, st);
 }
 
 // Time model for a tile of TM x TN: every block loads K * (16 TM * 2 + 16 TN * bytes per

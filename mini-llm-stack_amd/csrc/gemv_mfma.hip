@@ -124,13 +124,21 @@ constexpr int SLG = 16;
 // address units (not HBM) bounded the kernel. The 16-byte chunk index of row r is XOR-ed
 // with r & (CH - 1) (conflict-free 16-row reads). Rows of the slice at or past M hold
 // zeros or stale data; they feed only output columns m >= M, which are never stored.
-template <int WBITS, typename AT, typename ST, int R, int WAVES, int U, bool SL, bool XL, bool S64>
+//
+// Split x (SPL, fp32 activations as bf16 hi + lo, mfma16.h): a holds the split rows of
+// M <= 16 rows of x, the hi parts in rows 0..15 and the lo parts in rows 16..31; every MFMA
+// on an x operand runs once on each part into the same accumulator, and the output is fp32.
+// x comes straight from global (the LDS slice of both parts would not fit).
+template <int WBITS, typename AT, typename ST, int R, int WAVES, int U, bool SL, bool XL, bool S64, bool SPL = false>
 // One wavefront per SIMD is the design point (a grid of N / 16 blocks of WAVES
 // wavefronts), so the compiler may spend registers on keeping a chunk's loads in flight.
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemv_mfma_kernel(
     const AT* __restrict__ a, int64_t lda, const uint8_t* __restrict__ w, int64_t ldw,
-    const ST* __restrict__ s, int64_t ld_sn, int64_t ld_sg, int group, AT* __restrict__ c,
-    int64_t ldc, int M, int N, int K) {
+    const ST* __restrict__ s, int64_t ld_sn, int64_t ld_sg, int group,
+    std::conditional_t<SPL, float, AT>* __restrict__ c, int64_t ldc, int M, int N, int K) {
+  using OT = std::conditional_t<SPL, float, AT>;
+  static_assert(!(SPL && XL), "split x comes from global");
+  constexpr int XPARTS = SPL ? 2 : 1;
   constexpr bool W16 = WBITS == 8 || !S64;    // 16 weight bytes per lane and step (else 8)
   constexpr int KB = WBITS == 4 && W16 ? 128 : 64;  // k per step
   constexpr int NMF = WBITS == 4 && W16 ? 4 : 2;    // MFMAs per step and 16-row tile
@@ -177,9 +185,12 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rss, dst, 4, off, 0, 0, 0);
     }
   }
-  // rows of x past M and weight rows past N read as zeros
+  // rows of x past M and weight rows past N read as zeros (split x: the lo parts' M rows
+  // start 16 rows down, through a descriptor of their own)
   const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
       (void*)a, (short)0, (int)(M * lda * (int64_t)sizeof(AT)), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsx_lo = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a + (SPL ? 16 * lda : 0)), (short)0, (int)(M * lda * (int64_t)sizeof(AT)), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(w + (int64_t)n_base * ldw), (short)0, (int)(rows_w * ldw), 0x00020000);
   // this lane's byte offsets inside a step (x row m = r)
@@ -216,7 +227,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
     }
   }
   for (int s0 = s_lo; s0 < s_hi; s0 += U) {
-    uint4 wv[U][R], xv[U][NMF];
+    uint4 wv[U][R], xv[U][NMF], xvl[SPL ? U : 1][SPL ? NMF : 1];
     float sc[WBITS == 4 ? U : 1][R][4];
     // All loads of the chunk first, and no branch between them and the MFMAs (a
     // conditional step lets the compiler sink its loads to the use and serialise the
@@ -240,6 +251,12 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
         for (int j = 0; j < NMF; ++j)
           xv[u][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
                                                    rsx, x_off + 16 * j, xs_off, 0));
+        if constexpr (SPL) {
+#pragma unroll
+          for (int j = 0; j < NMF; ++j)
+            xvl[u][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rsx_lo, x_off + 16 * j, xs_off, 0));
+        }
       }
       if constexpr (WBITS == 4 && !SL) {
         const int64_t g = (int64_t)(st * KB / group) * ld_sg;
@@ -255,7 +272,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
     // them (vector loads complete in order; a count above 63 waits for more, which is
     // still correct).
     if constexpr (SL || XL) {
-      constexpr int LPU = R + (XL ? 0 : NMF) + ((WBITS == 4 && !SL) ? 4 * R : 0);
+      constexpr int LPU = R + (XL ? 0 : XPARTS * NMF) + ((WBITS == 4 && !SL) ? 4 * R : 0);
       if (s0 == s_lo) wait_vmcnt_le<(U * LPU < 63 ? U * LPU : 63)>();
     }
     if constexpr (WBITS == 4 && SL) {
@@ -288,28 +305,45 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if constexpr (WBITS == 4) {
-        uint4 xo[NMF];
+        uint4 xo[XPARTS][NMF];
 #pragma unroll
-        for (int j = 0; j < NMF; ++j) xo[j] = x_perm(xv[u][j]);
+        for (int j = 0; j < NMF; ++j) {
+          xo[0][j] = x_perm(xv[u][j]);
+          if constexpr (SPL) xo[XPARTS - 1][j] = x_perm(xvl[u][j]);
+        }
         f32x4 xs = zero;
 #pragma unroll
-        for (int j = 0; j < NMF; ++j) xs = Mx<AT>::mma(ones, xo[j], xs);
+        for (int h = 0; h < XPARTS; ++h)
+#pragma unroll
+          for (int j = 0; j < NMF; ++j) xs = Mx<AT>::mma(ones, xo[h][j], xs);
 #pragma unroll
         for (int t = 0; t < R; ++t) {
           const uint32_t d[4] = {wv[u][t].x, wv[u][t].y, wv[u][t].z, wv[u][t].w};
           f32x4 pp = zero;
 #pragma unroll
-          for (int j = 0; j < NMF; ++j) pp = Mx<AT>::mma(nib_operand<AT>(d[j]), xo[j], pp);
+          for (int j = 0; j < NMF; ++j) {
+            const uint4 wop = nib_operand<AT>(d[j]);
+#pragma unroll
+            for (int h = 0; h < XPARTS; ++h) pp = Mx<AT>::mma(wop, xo[h][j], pp);
+          }
 #pragma unroll
           for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(sc[u][t][i], fmaf(-Mx<AT>::OFF4, xs[i], pp[i]), acc[t][i]);
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < NMF; ++j) xsum = Mx<AT>::mma(ones, xv[u][j], xsum);
+        for (int j = 0; j < NMF; ++j) {
+          xsum = Mx<AT>::mma(ones, xv[u][j], xsum);
+          if constexpr (SPL) xsum = Mx<AT>::mma(ones, xvl[u][j], xsum);
+        }
 #pragma unroll
         for (int t = 0; t < R; ++t) {
-          acc[t] = Mx<AT>::mma(byte_operand<AT>(wv[u][t].x, wv[u][t].y), xv[u][0], acc[t]);
-          acc[t] = Mx<AT>::mma(byte_operand<AT>(wv[u][t].z, wv[u][t].w), xv[u][1], acc[t]);
+          const uint4 w0 = byte_operand<AT>(wv[u][t].x, wv[u][t].y), w1 = byte_operand<AT>(wv[u][t].z, wv[u][t].w);
+          acc[t] = Mx<AT>::mma(w0, xv[u][0], acc[t]);
+          acc[t] = Mx<AT>::mma(w1, xv[u][1], acc[t]);
+          if constexpr (SPL) {
+            acc[t] = Mx<AT>::mma(w0, xvl[u][0], acc[t]);
+            acc[t] = Mx<AT>::mma(w1, xvl[u][1], acc[t]);
+          }
         }
       }
     }
@@ -336,13 +370,13 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] *= ld_scale(s, (int64_t)min(nb + i, N - 1) * ld_sn);
     }
-    AT* dst = c + (int64_t)m * ldc + nb;
-    if (nb + 3 < N && ((uintptr_t)dst & 7) == 0) {
-      store4<AT>(dst, v[0], v[1], v[2], v[3]);
+    OT* dst = c + (int64_t)m * ldc + nb;
+    if (nb + 3 < N && ((uintptr_t)dst & (sizeof(OT) * 4 - 1)) == 0) {
+      store4<OT>(dst, v[0], v[1], v[2], v[3]);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (nb + i < N) dst[i] = from_f32<AT>(v[i]);
+        if (nb + i < N) dst[i] = from_f32<OT>(v[i]);
     }
   }
 }
@@ -355,9 +389,9 @@ int env_pair(int& r, int& waves) {
   return sscanf(v, "%d,%d", &r, &waves) == 2;
 }
 
-template <int WBITS, typename AT, typename ST, int R, int WAVES, bool S64>
+template <int WBITS, typename AT, typename ST, int R, int WAVES, bool S64, bool SPL = false>
 int launch_one(const WqArgs& p) {
-  constexpr int U = 8;
+  constexpr int U = SPL ? 4 : 8;  // split x: both parts' registers for half the steps
   constexpr int KB = WBITS == 4 && !S64 ? 128 : 64;
   const int64_t blocks = cdiv(p.N, 16 * R);
   // the LDS scale slice: every wavefront's steps span at most SLG groups, and the slice's
@@ -369,12 +403,14 @@ int launch_one(const WqArgs& p) {
                   16 * R * p.ld_sn * (int64_t)sizeof(ST) < (1ll << 30) && (int64_t)(p.K / p.group) * p.ld_sg * (int64_t)sizeof(ST) < (1ll << 30);
   // x through LDS: one chunk per wavefront, and the wavefronts' slices within 128 KiB
   static const bool xl_env = env_int("MLS_GEMV_MFMA_XL", 1) != 0;
-  constexpr bool XL_FITS = WAVES * U * 16 * KB * 2 <= 128 * 1024;
+  constexpr bool XL_FITS = !SPL && WAVES * U * 16 * KB * 2 <= 128 * 1024;
   const bool xl = XL_FITS && xl_env && per_wave <= U;
+  using OT = std::conditional_t<SPL, float, AT>;
   auto go = [&](auto slc, auto xlc) {
-    hipLaunchKernelGGL((gemv_mfma_kernel<WBITS, AT, ST, R, WAVES, U, decltype(slc)::value, decltype(xlc)::value, S64>),
+    hipLaunchKernelGGL((gemv_mfma_kernel<WBITS, AT, ST, R, WAVES, U, decltype(slc)::value, decltype(xlc)::value, S64,
+                                         SPL>),
                        dim3((unsigned)blocks), dim3(64 * WAVES), 0, p.stream, static_cast<const AT*>(p.a), p.lda, p.w,
-                       p.ldw, static_cast<const ST*>(p.s), p.ld_sn, p.ld_sg, p.group, static_cast<AT*>(p.c), p.ldc,
+                       p.ldw, static_cast<const ST*>(p.s), p.ld_sn, p.ld_sg, p.group, static_cast<OT*>(p.c), p.ldc,
                        (int)p.M, (int)p.N, (int)p.K);
   };
   using T_ = std::true_type;
@@ -391,29 +427,59 @@ int launch_one(const WqArgs& p) {
   return MLS_OK;
 }
 
-template <int WBITS, typename AT, typename ST, bool S64>
+template <int WBITS, typename AT, typename ST, bool S64, bool SPL = false>
 int launch_shape(const WqArgs& p) {
   constexpr int KB = WBITS == 4 && !S64 ? 128 : 64;
   const int64_t nsteps = p.K / KB;
   int r = 1, waves = nsteps >= 64 ? 8 : 4;  // about 8 steps (one chunk) per wavefront
   if (nsteps >= 128) waves = 16;
   // (twice the wavefronts with at most 4 steps each measured slower: M=16 6.05 -> 6.50 us)
-  env_pair(r, waves);
-  if (r == 2) {  // two tiles per wavefront: at most 8 wavefronts (16 spill)
-    if (waves >= 8) return launch_one<WBITS, AT, ST, 2, 8, S64>(p);
-    return launch_one<WBITS, AT, ST, 2, 4, S64>(p);
+  if constexpr (SPL) {  // split x: chunks of 4 steps, about one per wavefront
+    waves = nsteps >= 64 ? 16 : nsteps >= 32 ? 8 : 4;
   }
-  if (waves == 16) return launch_one<WBITS, AT, ST, 1, 16, S64>(p);
-  if (waves == 8) return launch_one<WBITS, AT, ST, 1, 8, S64>(p);
-  return launch_one<WBITS, AT, ST, 1, 4, S64>(p);
+  env_pair(r, waves);
+  if constexpr (!SPL) {
+    if (r == 2) {  // two tiles per wavefront: at most 8 wavefronts (16 spill)
+      if (waves >= 8) return launch_one<WBITS, AT, ST, 2, 8, S64>(p);
+      return launch_one<WBITS, AT, ST, 2, 4, S64>(p);
+    }
+  }
+  if (waves == 16) return launch_one<WBITS, AT, ST, 1, 16, S64, SPL>(p);
+  if (waves == 8) return launch_one<WBITS, AT, ST, 1, 8, S64, SPL>(p);
+  return launch_one<WBITS, AT, ST, 1, 4, S64, SPL>(p);
 }
 
-template <int WBITS, typename AT, bool S64 = false>
+template <int WBITS, typename AT, bool S64 = false, bool SPL = false>
 int launch_st(const WqArgs& p) {
-  return p.s_dt == MLS_F16 ? launch_shape<WBITS, AT, _Float16, S64>(p) : launch_shape<WBITS, AT, float, S64>(p);
+  return p.s_dt == MLS_F16 ? launch_shape<WBITS, AT, _Float16, S64, SPL>(p)
+                           : launch_shape<WBITS, AT, float, S64, SPL>(p);
 }
 
 }  // namespace
+
+// Shape checks shared by the 16-bit and the split-x launches.
+static bool gemv_mfma_fits(int wbits, const WqArgs& p) {
+  if (p.M < 1 || p.M > 16) return false;
+  // INT4 steps of 128 k (groups a multiple of 128) or of 64 k (other multiples of 64)
+  const bool s64 = wbits == 4 && p.group % 128 != 0;
+  const int KB = wbits == 4 && !s64 ? 128 : 64;
+  if (p.K % KB != 0) return false;
+  if (wbits == 4 && p.group % 64 != 0) return false;
+  if (!aligned(p.a, 16) || (p.lda * 2) % 16 != 0) return false;
+  if (!aligned(p.w, 16) || p.ldw % 16 != 0) return false;
+  // 32-bit buffer offsets: 32 rows of x and a 32-row weight tile
+  // (and the past-the-end x offset 0x7FFFFFF0 added to an x offset must not wrap)
+  if (32 * p.lda * 2 >= (1ll << 31) || 32 * p.ldw >= (1ll << 31)) return false;
+  return p.N <= 0x7FFFFFFF - 32 && p.K <= 0x3FFFFFFF;
+}
+
+int launch_gemv_mfma_split(int wbits, const WqArgs& q) {
+  if (q.a_dt != MLS_BF16 || !gemv_mfma_fits(wbits, q)) return MLS_ERR_UNSUPPORTED;
+  const bool s64 = wbits == 4 && q.group % 128 != 0;
+  if (wbits == 4 && s64) return launch_st<4, __bf16, true, true>(q);
+  if (wbits == 4) return launch_st<4, __bf16, false, true>(q);
+  return launch_st<8, __bf16, false, true>(q);
+}
 
 int launch_gemv_mfma(int wbits, const WqArgs& p) {
   static const bool enabled = [] {

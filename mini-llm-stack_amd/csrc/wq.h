@@ -48,6 +48,9 @@ int launch_gemm_wq_generic(int wbits, const WqArgs& p);
 // rows (bf16 hi and lo parts of m_out rows of x, p.M = split_rows(m_out)); the output is
 // fp32 [m_out][ldc]. MLS_ERR_UNSUPPORTED outside the kernels' fast paths.
 int launch_gemm_small_split(int wbits, const WqArgs& p, int64_t m_out);
+// The skinny MFMA GEMV on split rows of M <= 16 rows of x (hi parts in rows 0..15, lo parts
+// in rows 16..31 of p.a; p.M = the rows of x), fp32 output.
+int launch_gemv_mfma_split(int wbits, const WqArgs& p);
 int launch_gemm_wq_mfma_split(int wbits, const WqArgs& p, int64_t m_out);
 // x fp32 [M][ldx] -> split rows [split_rows(M)][K] bf16 (zeros for rows past M).
 int launch_split_rows(const float* x, int64_t ldx, int64_t M, int64_t K, void* x2, hipStream_t st);

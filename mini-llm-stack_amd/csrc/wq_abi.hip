@@ -74,15 +74,17 @@ int run(const char* fn, int wbits, const WqArgs& p) {
   return check_launch(fn);
 }
 
-// fp32 activations with M > 16 on the 16-bit matrix cores (split.hip): x is split into
-// bf16 hi and lo rows in the workspace, then the medium GEMM (few engine tiles) or the
-// engine multiplies both and adds them in its epilogue. Taken only where the engine is
+// fp32 activations with M >= 2 on the 16-bit matrix cores (split.hip): x is split into
+// bf16 hi and lo rows in the workspace, then the skinny GEMV (M <= 16), the medium GEMM
+// (few engine tiles) or the engine multiplies both and adds them. Taken only where the engine is
 // sure to accept the split rows, so the split pass never runs for nothing.
+// 2 <= M <= 16 takes the skinny MFMA GEMV on the split rows (each x MFMA once per part).
 bool split_ok(int wbits, const WqArgs& p) {
   static const bool enabled = env_int("MLS_SPLIT", 1) != 0;  // 0: the VALU GEMV (A/B runs)
-  if (!enabled || p.a_dt != MLS_F32 || p.M <= 16 || p.M > 0x3FFFFFFF || p.K < 64 || p.K % 64 != 0) return false;
-  if (!aligned(p.w, 16) || p.ldw % 16 != 0 || !aligned(p.c, 8)) return false;
+  if (!enabled || p.a_dt != MLS_F32 || p.M < 2 || p.M > 0x3FFFFFFF || p.K < 64 || p.K % 64 != 0) return false;
+  if (!aligned(p.w, 16) || p.ldw % 16 != 0 || !aligned(p.c, 16)) return false;
   if (wbits == 4 && p.group % 64 != 0) return false;
+  if (p.M <= 16 && wbits == 4 && p.group % 128 == 0 && p.K % 128 != 0) return false;  // (K % group == 0 anyway)
   const int64_t m2 = split_rows(p.M);
   return m2 <= 0x3FFFFFFF && p.N <= 0x3FFFFFFF && p.K <= 0x3FFFFFFF && p.K * 2 * 256 < (1ll << 31) &&
          p.ldw * 256 < (1ll << 31);
@@ -98,7 +100,12 @@ int run_split(const char* fn, int wbits, const WqArgs& p, void* ws) {
   q.a_dt = MLS_BF16;
   q.lda = p.K;
   q.M = split_rows(p.M);
-  rc = launch_split_gemm(wbits, q, p.M);
+  if (p.M <= 16) {
+    q.M = p.M;  // the skinny kernel reads the M hi rows and, 16 rows down, the M lo rows
+    rc = launch_gemv_mfma_split(wbits, q);
+  } else {
+    rc = launch_split_gemm(wbits, q, p.M);
+  }
   if (rc == MLS_ERR_UNSUPPORTED) return fail(MLS_ERR_HIP, "%s: split rows written but no split GEMM took them", fn);
   if (rc != MLS_OK) return rc;
   return check_launch(fn);
@@ -135,7 +142,7 @@ extern "C" int64_t mls_wq_gemm_workspace(int wbits, int64_t M, int64_t N, int64_
   // the split off, and then no workspace is used)
   WqArgs p{};
   p.a_dt = a_dt; p.M = M; p.N = N; p.K = K; p.group = wbits == 4 ? group : 0;
-  if (a_dt != MLS_F32 || M <= 16 || K < 64 || K % 64 != 0 || (wbits == 4 && (group < 1 || group % 64 != 0))) return 0;
+  if (a_dt != MLS_F32 || M < 2 || K < 64 || K % 64 != 0 || (wbits == 4 && (group < 1 || group % 64 != 0))) return 0;
   if (M > 0x3FFFFFFF || split_rows(M) > 0x3FFFFFFF || N > 0x3FFFFFFF || K > 0x3FFFFFFF || K * 2 * 256 >= (1ll << 31))
     return 0;
   return split_ws_bytes(p);

@@ -11,7 +11,7 @@ INT4: w_packed [N, K/2] uint8, two nibbles per byte (even k in the low nibble),
 The work runs in libmls_hip.so on gfx950 (include/mls.h): a decode GEMV that
 streams the packed weights with 16-byte loads for small M, and an MFMA GEMM that
 dequantizes weight tiles into LDS for larger M. The library picks the kernel
-from the shape. fp32 activations with M > 16 (the reference's fp32 engine) run on
+from the shape. fp32 activations with M >= 2 (the reference's fp32 engine) run on
 the bf16 matrix cores as hi + lo parts, x split into a workspace taken from torch's
 caching allocator. Outputs have a.dtype; scales may be fp32 or fp16 (other float
 dtypes are converted to fp32, as the reference does for every scale).
@@ -42,7 +42,7 @@ def int8_matmul(a: torch.Tensor, w_q: torch.Tensor, scale: torch.Tensor):
     s, sdt = scale_vector(scale.reshape(-1).contiguous())
     c = torch.empty(M, N, dtype=a.dtype, device=dev)
     lib = kernels.lib()
-    # fp32 activations with M > 16 run on the matrix cores as bf16 hi + lo parts, split
+    # fp32 activations with M >= 2 run on the matrix cores as bf16 hi + lo parts, split
     # into a workspace from torch's caching allocator; other calls need none
     need = lib.mls_wq_gemm_workspace(8, M, N, K, adt, 0)
     ws = torch.empty(need, dtype=torch.uint8, device=dev) if need else None

@@ -34,6 +34,7 @@ int launch_grouped_int4_partial(const GroupedArgs&, int, float*, int64_t, int64_
 int grouped_splits(int64_t, int, int64_t, int64_t, int) { return 1; }
 int launch_gemm_small_split(int, const WqArgs&, int64_t) { reached("launch_gemm_small_split"); }
 int launch_gemm_wq_mfma_split(int, const WqArgs&, int64_t) { reached("launch_gemm_wq_mfma_split"); }
+int launch_gemv_mfma_split(int, const WqArgs&) { reached("launch_gemv_mfma_split"); }
 int launch_split_rows(const float*, int64_t, int64_t, int64_t, void*, hipStream_t) { reached("launch_split_rows"); }
 }  // namespace mls
 
@@ -123,7 +124,7 @@ void workspace_cases() {
   expect("int4 ws group", mls_int4_gemm_ws(P(0), F32, 64, PT<uint8_t>(1), 32, P(2), F16, 1, 1, 48, c, F32, 32, 64, 32,
                                            64, ws, need, nullptr),
          MLS_ERR_ARG, "group");
-  if (mls_wq_gemm_workspace(8, 16, 32, 64, F32, 0) != 0 || mls_wq_gemm_workspace(4, 64, 32, 64, F32, 32) != 0 ||
+  if (mls_wq_gemm_workspace(8, 1, 32, 64, F32, 0) != 0 || mls_wq_gemm_workspace(4, 64, 32, 64, F32, 32) != 0 ||
       mls_wq_gemm_workspace(8, 64, 32, 64, BF, 0) != 0 || mls_wq_gemm_workspace(8, INT64_MAX, 32, 64, F32, 0) != 0) {
     std::fprintf(stderr, "FAIL workspace query outside the split route\n");
     ++failures;

@@ -1,5 +1,5 @@
 """fp32 activations on the matrix cores (the reference's engine runs fp32 end to end,
-serve/engine.py:166, so every QuantLinear call there carries fp32 x): with M > 16, x is
+serve/engine.py:166, so every QuantLinear call there carries fp32 x): with M >= 2, x is
 split into bf16 hi + lo parts and both are multiplied on the bf16 MFMA with fp32
 accumulation and added in fp32.
 
@@ -157,18 +157,46 @@ def test_fp32_split_nonfinite(dev):
 
 
 def test_fp32_small_m_unchanged(dev):
-    """M <= 16 keeps the VALU GEMV (HBM-bound; fp32 FMAs): no workspace is asked for."""
+    """M = 1 keeps the VALU GEMV (HBM-bound; fp32 FMAs): no workspace is asked for; from
+    M = 2 on the split rows are 32 per 16 rows of x."""
     import kernels
     L = kernels.lib()
-    assert L.mls_wq_gemm_workspace(8, 16, 4096, 4096, kernels.MLS_F32, 0) == 0
+    assert L.mls_wq_gemm_workspace(8, 1, 4096, 4096, kernels.MLS_F32, 0) == 0
+    assert L.mls_wq_gemm_workspace(8, 16, 4096, 4096, kernels.MLS_F32, 0) == 32 * 4096 * 2
     assert L.mls_wq_gemm_workspace(8, 17, 4096, 4096, kernels.MLS_F32, 0) == 64 * 4096 * 2
     assert L.mls_wq_gemm_workspace(8, 2048, 4096, 4096, kernels.MLS_BF16, 0) == 0
     assert L.mls_wq_gemm_workspace(4, 64, 4096, 4096, kernels.MLS_F32, 32) == 0  # groups of 32: VALU
-    M, N, K = 5, 1000, 1024
+    M, N, K = 1, 1000, 1024
     g = torch.Generator().manual_seed(4)
     a = torch.randn(M, K, generator=g)
     q, s = quantize_int8(torch.randn(N, K, generator=g) * 0.02)
-    _check32(int8_matmul(a.to(dev), q.to(dev), s.to(dev)), ref.int8_matmul(a.numpy(), q.numpy(), s.numpy()), "M=5")
+    _check32(int8_matmul(a.to(dev), q.to(dev), s.to(dev)), ref.int8_matmul(a.numpy(), q.numpy(), s.numpy()), "M=1")
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+@pytest.mark.parametrize("M,N,K,gs", [
+    (2, 4096, 4096, 128),   # speculative verify with one draft token
+    (5, 4096, 4096, 128),   # verify with gamma = 4, or a decode batch of 5
+    (16, 1000, 1152, 128),  # ragged N, 9 steps
+    (7, 333, 768, 256),     # odd M, ragged N, a group of two steps
+    (3, 520, 1088, 64),     # groups of 64: 64-k steps
+    (16, 512, 14336, 128),  # long K: 16 wavefronts
+])
+def test_fp32_split_skinny(dev, bits, M, N, K, gs):
+    """2 <= M <= 16 with fp32 x: the skinny MFMA GEMV runs every x MFMA on the hi and the lo
+    part into one accumulator."""
+    g = torch.Generator().manual_seed(M * 13 + N + bits)
+    a = torch.randn(M, K, generator=g)
+    w = torch.randn(N, K, generator=g) * 0.02
+    if bits == 8:
+        q, s = quantize_int8(w)
+        out = int8_matmul(a.to(dev), q.to(dev), s.to(torch.float16).to(dev))
+        want = ref.int8_matmul(a.numpy(), q.numpy(), s.to(torch.float16).float().numpy())
+    else:
+        q, s = quantize_int4(w, gs)
+        out = int4_matmul(a.to(dev), q.to(dev), s.to(dev), gs)
+        want = ref.int4_matmul(a.numpy(), q.numpy(), s.numpy(), gs)
+    _check32(out, want, f"fp32 skinny int{bits} M={M} N={N} K={K}")
 
 
 def test_int8_dgrad_fp32_training_shape(dev):
