@@ -64,6 +64,9 @@ struct SmallArgs {
   int M, N, K;
   int m_tiles, G;  // row tiles; INT4 groups per weight row
   int m_out;       // split rows (fp32 x as bf16 hi + lo, mfma16.h): output rows, fp32 output
+  // x slices in LDS (kernels with 8 or 16 wavefronts): byte offset of the first slice,
+  // log2 of a slice row's 16-byte chunks (a slice row holds xs_steps steps of one x row)
+  int x_lds, xs_log2, xs_steps;
 };
 
 __device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
@@ -82,7 +85,16 @@ __device__ __forceinline__ uint4 perm_x(const uint4& v) {
 // (a & m) | c with m and c in registers: one v_and_or_b32
 __device__ __forceinline__ uint32_t andor(uint32_t a, uint32_t m, uint32_t c) { return (a & m) | c; }
 
-template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64 = false, bool SPLIT = false, int WV = 4>
+// x through LDS (XLS, the 8- and 16-wavefront kernels): loaded per lane in MFMA layout, a
+// 16-byte x piece touched 16 rows' cache lines at a quarter of their width, and the address
+// unit (TA busy ~14.8k cycles per CU at M = 128, N = K = 2048, most of it stalled on the
+// L1, ~41 L1 accesses per load instruction) bounded the kernel. Each wavefront now first
+// brings its K range of the tile's 16 TM rows of x into its own LDS slice with LDS-direct
+// loads of whole 16-byte chunks, row by row (consecutive lanes, consecutive chunks of a
+// row), the chunk index XOR-ed with row & 7; the MFMA pieces are then read from LDS. Each
+// wavefront reads only its own slice, so its own vmcnt wait is the only synchronisation.
+template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64 = false, bool SPLIT = false, int WV = 4,
+          bool XLS = false>
 __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) {
   using MM = Mfma16<AT>;
   // split rows: 16-row tiles 2t and 2t + 1 hold the hi and lo parts of output rows
@@ -123,17 +135,32 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) wo[tn] = (n0 + 16 * tn + r16) * p.ldw + WB * q;
 
+  // ---- XLS: this wavefront's x slice, [16 TM rows][2^xs_log2 chunks], before anything else
+  uint8_t* xsl = smem + p.x_lds + wave * ((16 * TM) << (p.xs_log2 + 4));
+  if constexpr (XLS) {
+    const int cpr_mask = (1 << p.xs_log2) - 1;
+    const int total = (16 * TM) << p.xs_log2;  // chunks of the slice
+    for (int c0 = 0; c0 < total; c0 += 64) {
+      const int sidx = c0 + lane, row = sidx >> p.xs_log2, cp = sidx & cpr_mask;
+      const int cl = cp ^ (row & 7);  // logical chunk stored at physical slot cp
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (__attribute__((address_space(3))) void*)(xsl + c0 * 16), 16,
+                                               (m0 + row) * p.lda * 2 + cl * 16, s_lo * KS * 2, 0, 0);
+    }
+  }
+
   struct Slot {
-    uint4 x[TM][XP];
+    uint4 x[XLS ? 1 : TM][XLS ? 1 : XP];
     uint4 w[TN];
   };
   auto load = [&](Slot& sl, int st) __attribute__((always_inline)) {
     const int live = st < s_hi;
     const int sx = live ? st * KS * 2 : kPastEnd, sw = live ? st * 4 * WB : kPastEnd;
+    if constexpr (!XLS) {
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm)
+      for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-      for (int h = 0; h < XP; ++h) sl.x[tm][h] = ld16(rsa, xo[tm] + 16 * h, sx);
+        for (int h = 0; h < XP; ++h) sl.x[tm][h] = ld16(rsa, xo[tm] + 16 * h, sx);
+    }
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
       if constexpr (WB == 8) {
@@ -148,6 +175,13 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
 #pragma unroll
   for (int d = 0; d < D; ++d) load(sl[d], s_lo + d);
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (XLS && !I4) {
+    // the slice's LDS-direct loads were issued first and complete first: wait for all but
+    // the ring's D TN weight loads (the compiler does not model the LDS-direct writes)
+    constexpr int N_ = D * TN;
+    __builtin_amdgcn_s_waitcnt((N_ & 0xF) | ((N_ >> 4) << 14) | 0x70 | 0xF00);
+    asm volatile("" ::: "memory");
+  }
 
   // ---- INT4 group scales of the block's 16 TN rows into LDS ([row][group] in ST), issued
   // after the first two steps' operands: the first step waits for nearly all of those
@@ -180,6 +214,21 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
   const uint4 ones = make_uint4(Nib<AT>::ONE2, Nib<AT>::ONE2, Nib<AT>::ONE2, Nib<AT>::ONE2);
   const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // this lane's x pieces of step st: from the slot (registers) or the LDS slice
+  auto x_piece = [&](const Slot& sl, int st, int tm, int h) __attribute__((always_inline)) -> uint4 {
+    if constexpr (XLS) {
+      // a step past the wavefront's range (the ring's last round) multiplies zeros, as the
+      // register path's past-the-end loads do: its slice position holds another step's x
+      const bool live = st < s_hi;  // wave-uniform
+      const int row = 16 * tm + r16;
+      const int cl = (live ? st - s_lo : 0) * (KS * 2 / 16) + XP * q + h;
+      const uint4 v = *reinterpret_cast<const uint4*>(xsl + ((row << p.xs_log2) + (cl ^ (row & 7))) * 16);
+      return live ? v : make_uint4(0u, 0u, 0u, 0u);
+    } else {
+      return sl.x[tm][h];
+    }
+  };
+
   auto compute = [&](const Slot& sl, int st) __attribute__((always_inline)) {
     if constexpr (I4) {
       constexpr int NJ = XP;  // weight dwords (8 nibbles each) per lane and step
@@ -188,7 +237,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) xpm[tm][j] = perm_x(sl.x[tm][j]);
+        for (int j = 0; j < NJ; ++j) xpm[tm][j] = perm_x(x_piece(sl, st, tm, j));
         xs[tm] = zero;
 #pragma unroll
         for (int j = 0; j < NJ; ++j) xs[tm] = MM::mma(ones, xpm[tm][j], xs[tm]);
@@ -224,8 +273,8 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
         const uint4 w0 = make_uint4(o[0], o[1], o[2], o[3]), w1 = make_uint4(o[4], o[5], o[6], o[7]);
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm) {
-          acc[tn][tm] = MM::mma(w0, sl.x[tm][0], acc[tn][tm]);
-          acc[tn][tm] = MM::mma(w1, sl.x[tm][1], acc[tn][tm]);
+          acc[tn][tm] = MM::mma(w0, x_piece(sl, st, tm, 0), acc[tn][tm]);
+          acc[tn][tm] = MM::mma(w1, x_piece(sl, st, tm, 1), acc[tn][tm]);
         }
       }
     }
@@ -285,12 +334,27 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
 
 template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64, bool SPLIT, int WV>
 int launch_small_wv(SmallArgs a, hipStream_t st) {
+  constexpr bool XLS = WV >= 8;  // x slices in LDS (a wavefront count with few steps each)
   a.m_tiles = (int)cdiv(a.M, 16 * TM);
   const int64_t nt = cdiv(cdiv(a.N, 16 * TN), 8) * 8;
   const int red = WV * TN * TM * 64 * 16;
-  const int sc = WBITS == 4 ? 16 * TN * a.G * (int)sizeof(ST) + 64 * WV * 4 : 0;  // + padding of the last dword load
+  int sc = WBITS == 4 ? 16 * TN * a.G * (int)sizeof(ST) + 64 * WV * 4 : 0;  // + padding of the last dword load
   if (a.m_tiles > 65535) return MLS_ERR_UNSUPPORTED;
-  auto kern = gemm_small_kernel<WBITS, AT, ST, TM, TN, D, S64, SPLIT, WV>;
+  if constexpr (XLS) {
+    // a slice row holds a power of two of steps (at least the most any wavefront has): a
+    // power-of-two chunk count, so lanes find their row and chunk by shifts
+    constexpr int KS = WBITS == 4 && !S64 ? 128 : 64;
+    const int smax = (int)cdiv(a.K / KS, WV);
+    int steps = 1;
+    while (steps < smax) steps *= 2;
+    const int chunks = steps * KS * 2 / 16;  // >= 8, a power of two
+    a.xs_log2 = __builtin_ctz((unsigned)chunks);
+    a.xs_steps = steps;
+    a.x_lds = (sc + 255) / 256 * 256;
+    sc = a.x_lds + WV * 16 * TM * chunks * 16;
+    if (sc > 160 * 1024) return MLS_ERR_UNSUPPORTED;
+  }
+  auto kern = gemm_small_kernel<WBITS, AT, ST, TM, TN, D, S64, SPLIT, WV, XLS>;
   const int lds = red > sc ? red : sc;
   if (lds > 65536) {  // above the default dynamic LDS limit: raise it once per instantiation
     static bool attr_set = false;
@@ -322,14 +386,20 @@ int launch_small(SmallArgs a, hipStream_t st) {
   static const int force = env_int("MLS_SMALL_WAVES", 0);
   const int KS = WBITS == 4 && !S64 ? 128 : 64;
   const int nsteps = a.K / KS;
-  int wv = nsteps >= 32 ? 16 : nsteps >= 16 ? 8 : 4;
+  // 8 wavefronts with x slices in LDS from 16 steps on (the reference's bench shape, 2048 x
+  // 2048 at M = 128: INT8 8.46 -> 8.10 us, INT4 g64 10.24 -> 8.52 us; 16 wavefronts measured
+  // 8.40 / 9.38 us)
+  int wv = nsteps >= 16 ? 8 : 4;
   if (force == 4 || force == 8 || force == 16) wv = force;
   // (the partial tiles of all wavefronts meet in LDS: WV TN TM KiB within 128 KiB)
+  int rc = MLS_ERR_UNSUPPORTED;
   if constexpr (small_regs<WBITS, TM, TN, 1, S64>() <= 56 && 16 * TN * TM <= 128)
-    if (wv >= 16) return launch_small_wv<WBITS, AT, ST, TM, TN, 1, S64, SPLIT, 16>(a, st);
+    if (wv >= 16) rc = launch_small_wv<WBITS, AT, ST, TM, TN, 1, S64, SPLIT, 16>(a, st);
   if constexpr (small_regs<WBITS, TM, TN, 2, S64>() <= 112 && 8 * TN * TM <= 128)
-    if (wv >= 8) return launch_small_wv<WBITS, AT, ST, TM, TN, 2, S64, SPLIT, 8>(a, st);
-  return launch_small_wv<WBITS, AT, ST, TM, TN, D, S64, SPLIT, 4>(a, st);
+    if (rc == MLS_ERR_UNSUPPORTED && wv >= 8) rc = launch_small_wv<WBITS, AT, ST, TM, TN, 2, S64, SPLIT, 8>(a, st);
+  // (the x slices too large for LDS: 4 wavefronts, x in registers)
+  if (rc == MLS_ERR_UNSUPPORTED) rc = launch_small_wv<WBITS, AT, ST, TM, TN, D, S64, SPLIT, 4>(a, st);
+  return rc;
 }
 
 // Time model for a tile of TM x TN: every block loads K * (16 TM * 2 + 16 TN * bytes per
