@@ -1166,7 +1166,7 @@ def main(argv=None) -> int:
                          "quantize_int4, ref_shapes, unquantized (the reference's fp16 / dequantize-then-matmul "
                          "comparison rows), fp32 (fp32 activations), clocks (M=1 step split), "
                          "copy (counter calibration), vendor_fp8_rowwise / vendor_fp8_tensorwise / "
-                         "vendor_bf16 (hipBLASLt calibration), cpu (the CPU baseline alone)")
+                         "vendor_bf16 / vendor_bf16_prefill (hipBLASLt calibration), cpu (the CPU baseline alone)")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
@@ -1245,6 +1245,11 @@ def main(argv=None) -> int:
             f"vendor_hipblaslt_{kind}_4096x8192x8192", r, peak,
             {"calibration": "vendor library through torch, not this build's kernels"}))(
             vendor_gemm(dev, small, 4, kind)))
+    # the unquantized bf16 GEMM at config C's shape, the INT8 prefill row's comparison point
+    runners["vendor_bf16_prefill"] = lambda: (lambda r: None if r is None else _mfma_row(
+        "vendor_hipblaslt_bf16_2048x11008x4096", r, BF16_PEAK_TFLOPS,
+        {"calibration": "vendor library through torch, not this build's kernels"}))(
+        vendor_gemm(dev, small, 4, "bf16", M=2048, N=11008, K=4096))
     if args.only:
         log(f"running {args.only}")
         row = runners[args.only]()
@@ -1266,7 +1271,7 @@ def main(argv=None) -> int:
                   "fp8_gemm", "fp8_native",
                   "fp8_bwd", "fp8_bwd_native", "moe_int4", "moe_mlp_int4", "paged_attn", "quantize_int4",
                   "ref_shapes", "unquantized", "copy", "floor", "clocks", "vendor_fp8_rowwise", "vendor_fp8_tensorwise",
-                  "vendor_bf16"):
+                  "vendor_bf16", "vendor_bf16_prefill"):
             log(f"{k} ...")
             row = runners[k]()
             log(json.dumps(row))

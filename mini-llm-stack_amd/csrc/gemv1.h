@@ -345,7 +345,7 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
       lds_direct16(rsx, smem + mi * XB + wave * 1024 + i * 4096, lane * 16, xo + wave * 1024 + i * 4096);
   }
   uint8_t* sl = smem + MX * XB + wave * (S_SLICE * 4);
-  float srow[R];
+  ST srow_raw[R];
   if constexpr (WBITS == 4) {
     // slice = the R rows' s_dw scale dwords back to back (rows past N read zeros); lane q of
     // instruction i loads slice dword 64 i + q, row r = dword / s_dw found by compares (R <= 4);
@@ -360,8 +360,12 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
       lds_direct4(rss, sl + 256 * i, r * s_row_bytes + (q - r * s_dw) * 4, n0 * s_row_bytes);
     }
   } else {
+    // the row scales, loaded ahead of the weights (they return first) and made live below,
+    // where the wait for the LDS-direct loads already covers them: left to the compiler,
+    // each load sank into the storing lane's branch and cost a full memory round trip
+    // after the reduction
 #pragma unroll
-    for (int r = 0; r < R; ++r) srow[r] = to_f32(s[min(n0 + r, N - 1)]);  // uniform: scalar loads
+    for (int r = 0; r < R; ++r) srow_raw[r] = s[min(n0 + r, N - 1)];
   }
   __builtin_amdgcn_sched_barrier(0);
 
@@ -376,18 +380,42 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
       wv[r][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, lane * 16 + 1024 * j,
                                                                                  (n0 + r) * ldw, 2));
 
+  // the slice index of each (row, chunk)'s group scale (a division by the runtime group
+  // size), computed while the loads are in flight instead of after the barrier
+  int sidx[R][CPL];
+  if constexpr (WBITS == 4) {
+    const int P = s_dw * 4 / (int)sizeof(ST);  // scales per slice row
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int g = ((lane + 64 * j) * KC) / group;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        sidx[r][j] = min(r * P + g, S_SLICE * 4 / (int)sizeof(ST) - 1);
+        asm volatile("" : "+v"(sidx[r][j]));
+      }
+    }
+  }
+
   // 3. the LDS-direct loads have landed once only the weight loads are outstanding; after
   //    the barrier every wavefront's quarter of x is there
   wait_vmcnt<R * CPL>();
   __builtin_amdgcn_s_barrier();
+  asm volatile("" ::"s"(y));  // the output pointer's kernel-argument load, here and not after the sums
+  float srow[R];
+  if constexpr (WBITS == 8) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      asm volatile("" : "+v"(srow_raw[r]));
+      srow[r] = to_f32(srow_raw[r]);
+    }
+  }
   float sc[R][CPL];
   if constexpr (WBITS == 4) {
     const ST* st = reinterpret_cast<const ST*>(sl);
-    const int P = s_dw * 4 / (int)sizeof(ST);  // scales per slice row
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) sc[r][j] = to_f32(st[min(r * P + ((lane + 64 * j) * KC) / group, S_SLICE * 4 / (int)sizeof(ST) - 1)]);
+      for (int j = 0; j < CPL; ++j) sc[r][j] = to_f32(st[sidx[r][j]]);
   }
   if constexpr (MX == 1) {
     // one row of x (the M = 1 GEMV)
