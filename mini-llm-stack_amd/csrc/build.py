@@ -22,9 +22,14 @@ CSRC = Path(__file__).resolve().parent
 PKG = CSRC.parent
 OUT = PKG / "libmls_hip.so"
 BUILD = CSRC / "_build"
-SOURCES = ["abi.hip", "e4m3.hip", "quant.hip", "gemv.hip", "gemv_mfma.hip", "gemm_mfma16.hip", "gemm_grouped.hip",
+SOURCES = ["abi.hip", "e4m3.hip", "quant.hip", "gemv.hip", "gemv_mfma.hip", "gemv_mfma8.hip", "gemm_mfma16.hip", "gemm_grouped.hip",
            "wq_abi.hip", "gemm_small.hip", "gemm_bytes.hip", "gemm_fp8.hip", "dgrad.hip", "moe.hip", "transpose.hip", "paged_attn.hip", "split.hip"]
 ARCH = "gfx950"
+# Per-source device-code options. gemv_mfma.hip (the skinny GEMM's INT4 kernels): MFMA
+# results in VGPRs (the kernel scales every MFMA result with VALU FMAs; in AGPRs each one is
+# first copied back with v_accvgpr_read, 56 extra VALU instructions per wavefront at
+# K = 4096). Its INT8 kernels (gemv_mfma8.hip) measured slower that way and keep the default.
+EXTRA_FLAGS = {"gemv_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def hipcc() -> str:
@@ -44,7 +49,7 @@ def common_flags() -> list[str]:
 
 def compile_one(src: str, verbose: bool) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
-    cmd = [hipcc(), *common_flags(), "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [hipcc(), *common_flags(), *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
