@@ -29,7 +29,9 @@ ARCH = "gfx950"
 # results in VGPRs (the kernel scales every MFMA result with VALU FMAs; in AGPRs each one is
 # first copied back with v_accvgpr_read, 56 extra VALU instructions per wavefront at
 # K = 4096). Its INT8 kernels (gemv_mfma8.hip) measured slower that way and keep the default.
-EXTRA_FLAGS = {"gemv_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+EXTRA_FLAGS = {"gemv_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+               "gemm_small.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+               "gemm_grouped.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def hipcc() -> str:

@@ -412,6 +412,18 @@ double small_cost(int64_t M, int64_t N, int64_t K, int wbits, int tm, int tn) {
   return (double)cdiv(blocks, 256) * per_block;
 }
 
+// Whether the 8-wavefront kernel's x slices of a TM-row-tile block fit in LDS (as
+// launch_small_wv sizes them), i.e. whether a tile height keeps x out of the registers.
+bool small_xls_fits(const SmallArgs& a, int wbits, bool s64, int tm, int tn, int ssz) {
+  const int ks = wbits == 4 && !s64 ? 128 : 64;
+  const int nsteps = a.K / ks;
+  if (nsteps < 16) return false;  // 4 wavefronts, no slices
+  int steps = 1;
+  while (steps < (nsteps + 7) / 8) steps *= 2;
+  const int sc = wbits == 4 ? 16 * tn * a.G * ssz + 64 * 8 * 4 : 0;
+  return (sc + 255) / 256 * 256 + 8 * 16 * tm * (steps * ks * 2 / 16) * 16 <= 160 * 1024;
+}
+
 template <int WBITS, typename AT, typename ST, bool S64 = false, bool SPLIT = false>
 int dispatch_small(SmallArgs a, hipStream_t st) {
   static const int force = env_int("MLS_SMALL_TILE", 0);  // TM * 10 + TN (sweeps)
@@ -422,7 +434,15 @@ int dispatch_small(SmallArgs a, hipStream_t st) {
       if (tm > (SPLIT ? 2 : 1) && a.M <= 16 * tm / 2) continue;  // a row tile mostly past M
       if (WBITS == 4 && tm * tn > 8) continue;      // INT4 4 x 4 would spill registers
       const double c = small_cost(a.M, a.N, a.K, WBITS, tm, tn);
-      if (c < best * 0.999) {
+      // the model counts bytes only; the widening of every weight, once per block, costs
+      // VALU time on top. A taller tile within 30% of the best byte count is taken when its
+      // x slices fit in LDS: each weight is then widened for twice the rows (the reference's
+      // bench shape, 2048 x 2048 at M = 128: 1 x 4 -> 2 x 2 tiles, INT8 8.05 -> 6.80 us, INT4
+      // g128 7.51 -> 6.91 us, g64 8.50 -> 7.33 us; across M = 32..256 x (2048^2, 4096^2,
+      // 11008 x 4096) no shape measured slower than the bytes-only choice)
+      const bool taller_tie = c <= best * 1.3 && tm > best_tm &&
+                              small_xls_fits(a, WBITS, S64, tm, tn, (int)sizeof(ST));
+      if (c < best * 0.999 || taller_tie) {
         best = c;
         best_tm = tm;
         best_tn = tn;
