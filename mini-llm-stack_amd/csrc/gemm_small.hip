@@ -88,8 +88,8 @@ __device__ __forceinline__ uint32_t andor(uint32_t a, uint32_t m, uint32_t c) { 
 // x through LDS (XLS, the 8- and 16-wavefront kernels): loaded per lane in MFMA layout, a
 // 16-byte x piece touched 16 rows' cache lines at a quarter of their width, and the address
 // unit (TA busy ~14.8k cycles per CU at M = 128, N = K = 2048, most of it stalled on the
-// L1, ~41 L1 accesses per load instruction) bounded the kernel. Each wavefront now first
-// brings its K range of the tile's 16 TM rows of x into its own LDS slice with LDS-direct
+// L1, ~41 L1 accesses per load instruction) bounded the kernel. Each wavefront now brings
+// its K range of the tile's 16 TM rows of x into its own LDS slice with LDS-direct
 // loads of whole 16-byte chunks, row by row (consecutive lanes, consecutive chunks of a
 // row), the chunk index XOR-ed with row & 7; the MFMA pieces are then read from LDS. Each
 // wavefront reads only its own slice, so its own vmcnt wait is the only synchronisation.
@@ -135,18 +135,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) wo[tn] = (n0 + 16 * tn + r16) * p.ldw + WB * q;
 
-  // ---- XLS: this wavefront's x slice, [16 TM rows][2^xs_log2 chunks], before anything else
   uint8_t* xsl = smem + p.x_lds + wave * ((16 * TM) << (p.xs_log2 + 4));
-  if constexpr (XLS) {
-    const int cpr_mask = (1 << p.xs_log2) - 1;
-    const int total = (16 * TM) << p.xs_log2;  // chunks of the slice
-    for (int c0 = 0; c0 < total; c0 += 64) {
-      const int sidx = c0 + lane, row = sidx >> p.xs_log2, cp = sidx & cpr_mask;
-      const int cl = cp ^ (row & 7);  // logical chunk stored at physical slot cp
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (__attribute__((address_space(3))) void*)(xsl + c0 * 16), 16,
-                                               (m0 + row) * p.lda * 2 + cl * 16, s_lo * KS * 2, 0, 0);
-    }
-  }
 
   struct Slot {
     uint4 x[XLS ? 1 : TM][XLS ? 1 : XP];
@@ -175,11 +164,25 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
 #pragma unroll
   for (int d = 0; d < D; ++d) load(sl[d], s_lo + d);
   __builtin_amdgcn_sched_barrier(0);
+
+  // ---- XLS: this wavefront's x slice, [16 TM rows][2^xs_log2 chunks], right after the
+  // ring's first weight loads: the weights come from HBM and the slice mostly from L2, so
+  // issued first the weights' latency runs under the slice's transfer (issued after the
+  // slice, they queued behind all of it: the reference's bench shape, INT8 M = 128, ~0.2 us)
+  if constexpr (XLS) {
+    const int cpr_mask = (1 << p.xs_log2) - 1;
+    const int total = (16 * TM) << p.xs_log2;  // chunks of the slice
+    for (int c0 = 0; c0 < total; c0 += 64) {
+      const int sidx = c0 + lane, row = sidx >> p.xs_log2, cp = sidx & cpr_mask;
+      const int cl = cp ^ (row & 7);  // logical chunk stored at physical slot cp
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (__attribute__((address_space(3))) void*)(xsl + c0 * 16), 16,
+                                               (m0 + row) * p.lda * 2 + cl * 16, s_lo * KS * 2, 0, 0);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   if constexpr (XLS && !I4) {
-    // the slice's LDS-direct loads were issued first and complete first: wait for all but
-    // the ring's D TN weight loads (the compiler does not model the LDS-direct writes)
-    constexpr int N_ = D * TN;
-    __builtin_amdgcn_s_waitcnt((N_ & 0xF) | ((N_ >> 4) << 14) | 0x70 | 0xF00);
+    // every load so far (the compiler does not model the LDS-direct writes)
+    __builtin_amdgcn_s_waitcnt(0 | 0x70 | 0xF00);
     asm volatile("" ::: "memory");
   }
 
