@@ -757,6 +757,225 @@ static int launch_w8(Mfma16Params p, hipStream_t st) {
   return check_launch("INT8 GEMM");
 }
 
+// ---------------------------------------------------------------------------
+// INT4 weight-only GEMM (dense, 256-row tiles) on the INT8 kernel's schedule above: the
+// activation tile arrives by LDS-direct loads, the next stage's weights are widened and
+// stored between the current stage's MFMA groups, one barrier per stage. Per block and
+// stage the weights are BN rows x 64 k = BN * 4 pieces of 8 bytes (16 k); a thread widens
+// its piece's two dwords, one per k-step's MFMA group, each into one 16-byte LDS chunk
+// (8 k) of exact 16 (v - 8) (x = d ^ 0x88888888 turns a nibble v into v ^ 8; masked into
+// the high nibble of a byte it is the signed 16 (v - 8), one sign-extending convert per
+// byte). Group scales by summation by parts: the block's table of coefficients
+// c_g = (s_g - s_{g+1}) / 16 (c_{G-1} = s_{G-1} / 16; the 1/16 undoes the widening's
+// factor) is computed once into LDS, the running products T are never cleared, and
+// each group end adds c_g T to the result, one FMA per accumulator:
+//   sum_g s_g P_g = sum_{g < G-1} (s_g - s_{g+1}) T_g + s_{G-1} T_{G-1},  T_g = P_0 + ... + P_g.
+// Compared with the 128-row kernel (mfma16_adma_kernel), each widened weight feeds twice
+// the rows, and a group end is one FMA per accumulator instead of an FMA and a clear.
+constexpr int kW4MaxGroups = 64;  // coefficient table rows (32 KiB at BN = 128)
+
+template <typename MT, typename OT, int BM, int BN, int WM, int WN, bool SPLIT = false>
+__global__ __launch_bounds__(64 * WM * WN) void mfma16_w4_kernel(const Mfma16Params p) {
+  constexpr int BK = 64;
+  constexpr int NW = WM * WN, NT = 64 * NW;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 16, TN = WTN / 16;
+  constexpr int PW = BM * 8 / NT;  // activation loads per wavefront and stage
+  static_assert(PW >= 1 && BM * 8 % NT == 0, "activation slots");
+  static_assert(BN * 4 == NT, "one 8-byte weight piece per thread and stage");
+  constexpr int B_RSTEP = NT / 4;
+  static_assert(B_RSTEP % 8 == 0, "swizzle");
+
+  __shared__ __align__(16) uint4 As[2][BM * 8];
+  __shared__ __align__(16) uint4 Bs[2][BN * 8];
+  __shared__ __align__(16) float cT[kW4MaxGroups][BN];
+
+  const int L = xcd_remap(blockIdx.x, gridDim.x);
+  int nt, mt;
+  tile_order(L, p.m_tiles, p.n_tiles, p.tile_gm, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int M = p.M, N = p.N;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm0 = (wave / WN) * WTM, wn0 = (wave % WN) * WTN;
+
+  const int rows_a = min(BM, M - m0), rows_b = min(BN, N - n0);
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)((const uint8_t*)p.a + (int64_t)m0 * p.lda * 2), (short)0, (int)(rows_a * p.lda * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(p.b + (int64_t)n0 * p.ldb), (short)0, (int)(rows_b * p.ldb), 0x00020000);
+  int a_off[PW];
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int s = (wave * PW + i) * 64 + lane, row = s >> 3, lc = (s & 7) ^ (row & 7);
+    a_off[i] = row * (int)p.lda * 2 + lc * 16;
+  }
+  // piece tid: row tid >> 2, k 16 (tid & 3) .. + 15 of the stage (8 bytes at k0 / 2 + 8 (tid & 3));
+  // its dword h widens into LDS chunk 2 (tid & 3) + h of the row
+  const int b_row = tid >> 2, b_kc = tid & 3;
+  const int b_off = b_row * (int)p.ldb + b_kc * 8;
+  const int b_lds0 = b_row * 8 + ((2 * b_kc) ^ swz(b_row));
+  const int b_lds1 = b_row * 8 + ((2 * b_kc + 1) ^ swz(b_row));
+
+  // the coefficient table: entry (g, n) for row n0 + n (rows past N repeat row N - 1, whose
+  // outputs are not stored); consecutive threads read consecutive groups of one row
+  const int G = p.K / p.group;
+  for (int idx = tid; idx < G * BN; idx += NT) {
+    const int n = idx / G, g = idx % G;
+    const int64_t r = (int64_t)min(n0 + n, N - 1) * p.ld_sn;
+    const float sg = scale_at(p.s, p.s_dt, r + (int64_t)g * p.ld_sg);
+    const float sn = g + 1 < G ? scale_at(p.s, p.s_dt, r + (int64_t)(g + 1) * p.ld_sg) : 0.0f;
+    cT[g][n] = (sg - sn) * 0.0625f;
+  }
+
+  uint2 rb;
+  auto load_b = [&](int k0) __attribute__((always_inline)) {
+    rb = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rsb, b_off, k0 / 2, 0));
+  };
+  // dword h of the piece -> one 16-byte chunk of 8 exact values 16 (v - 8), k order
+  auto store_half = [&](uint4* bs, int h) __attribute__((always_inline)) {
+    const uint32_t x = (h == 0 ? rb.x : rb.y) ^ 0x88888888u;
+    const uint32_t hi = x & 0xF0F0F0F0u;         // byte b: k = 2b + 1
+    const uint32_t lo = (x << 4) & 0xF0F0F0F0u;  // byte b: k = 2b
+    bs[h == 0 ? b_lds0 : b_lds1] =
+        make_uint4(pack_exact2<MT>(sbyte_f32<0>(lo), sbyte_f32<0>(hi)), pack_exact2<MT>(sbyte_f32<1>(lo), sbyte_f32<1>(hi)),
+                   pack_exact2<MT>(sbyte_f32<2>(lo), sbyte_f32<2>(hi)), pack_exact2<MT>(sbyte_f32<3>(lo), sbyte_f32<3>(hi)));
+  };
+  auto dma_a = [&](uint4* as, int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < PW; ++i) lds_load16(rsa, as + (wave * PW + i) * 64, a_off[i], k0 * 2);
+  };
+
+  f32x4 acc[TN][TM], tot[TN][TM];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) {
+      acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      tot[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  const int lr = lane & 15, lk = lane >> 4;
+  const int nk = p.K / BK;
+
+  // prologue: stage 0 in buffers 0, stage 1's weights in registers; the barrier also
+  // publishes the coefficient table
+  dma_a(As[0], 0);
+  load_b(0);
+  store_half(Bs[0], 0);
+  store_half(Bs[0], 1);
+  load_b(BK);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int r = kt & 1;
+    uint32_t abase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)As[r];
+    uint32_t bbase = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)Bs[r];
+    asm volatile("" : "+v"(abase), "+v"(bbase));
+    const auto* as = reinterpret_cast<const __attribute__((address_space(3))) lds16_t*>(abase);
+    const auto* bs = reinterpret_cast<const __attribute__((address_space(3))) lds16_t*>(bbase);
+    uint4* as_next = As[r ^ 1];
+    uint4* bs_next = Bs[r ^ 1];
+    const int k0 = kt * BK;
+    uint4 aop[2][TM], bop[2][TN];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int ch = ks * 4 + lk;
+#pragma unroll
+      for (int i = 0; i < TN; ++i) {
+        const int row = wn0 + i * 16 + lr;
+        bop[ks][i] = __builtin_bit_cast(uint4, bs[row * 8 + (ch ^ swz(row))]);
+      }
+#pragma unroll
+      for (int j = 0; j < TM; ++j) {
+        const int row = wm0 + j * 16 + lr;
+        aop[ks][j] = __builtin_bit_cast(uint4, as[row * 8 + (ch ^ swz(row))]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    dma_a(as_next, k0 + BK);  // stage kt + 1 (past the end: zeros / unused)
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      // k-step ks's MFMAs with half of stage kt + 1's weights widened and stored beside them
+#pragma unroll
+      for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j) tot[i][j] = Mfma16<MT>::mma(bop[ks][i], aop[ks][j], tot[i][j]);
+      store_half(bs_next, ks);
+      __builtin_amdgcn_sched_barrier(0);
+      const int kend = k0 + 32 * (ks + 1);
+      if (kend % p.group == 0) {  // group kend / group - 1 ends: acc += c_g T
+        const int g = kend / p.group - 1;
+#pragma unroll
+        for (int i = 0; i < TN; ++i) {
+          const float4 c4 = *reinterpret_cast<const float4*>(&cT[g][wn0 + i * 16 + 4 * lk]);
+          const float c[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+          for (int j = 0; j < TM; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) acc[i][j][q] = fmaf(c[q], tot[i][j][q], acc[i][j][q]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    load_b(k0 + 2 * BK);  // stage kt + 2 (past the end: harmless)
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+    // everything but the weight load just issued (vector loads complete in order), and
+    // the widened-weight stores
+    __builtin_amdgcn_s_waitcnt(1 | 0x70);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  // ---- epilogue: acc[i][j][q] = C[m = m0+wm0+16j+lr][n = n0+wn0+16i+4lk+q]; split rows:
+  // tiles 2j' and 2j' + 1 hold the hi and lo parts of output row (m0 + wm0) / 2 + 16j' + lr
+  static_assert(!SPLIT || (TM % 2 == 0 && (WTM % 32) == 0), "split rows pair whole 32-row groups");
+  OT* c = static_cast<OT*>(p.c);
+#pragma unroll
+  for (int i = 0; i < TN; ++i) {
+    const int nb = n0 + wn0 + i * 16 + 4 * lk;
+    if (nb >= N) continue;
+#pragma unroll
+    for (int j = 0; j < (SPLIT ? TM / 2 : TM); ++j) {
+      const int m = SPLIT ? (m0 + wm0) / 2 + j * 16 + lr : m0 + wm0 + j * 16 + lr;
+      if (m >= (SPLIT ? p.m_out : M)) continue;
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = SPLIT ? acc[i][2 * j][q] + acc[i][2 * j + 1][q] : acc[i][j][q];
+      OT* dst = c + (int64_t)m * p.ldc + nb;
+      if (nb + 3 < N && (p.ldc % 4) == 0) {
+        store4<OT>(dst, v[0], v[1], v[2], v[3]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (nb + q < N) dst[q] = from_f32<OT>(v[q]);
+      }
+    }
+  }
+}
+
+// Whether mfma16_w4_kernel takes a dense INT4 GEMM: its coefficient table holds the groups
+// (group a multiple of 32, G <= kW4MaxGroups); MLS_W4 = 0 keeps the 128-row kernel (A/B runs).
+static bool w4_ok(const Mfma16Params& p) {
+  static const bool on = env_int("MLS_W4", 1) != 0;
+  return on && p.group % 32 == 0 && p.K % p.group == 0 && p.K / p.group <= kW4MaxGroups && p.M >= 256;
+}
+
+template <typename MT, typename OT, bool SPLIT = false>
+static int launch_w4(Mfma16Params p, hipStream_t st) {
+  constexpr int BN = 128;
+  p.m_tiles = (int)cdiv(p.M, 256);
+  p.n_tiles = (int)cdiv(p.N, BN);
+  static const int gm = env_int("MLS_TILE_GM", 4);
+  p.tile_gm = gm;
+  const int64_t blocks = (int64_t)p.n_tiles * p.m_tiles;
+  hipLaunchKernelGGL((mfma16_w4_kernel<MT, OT, 256, BN, 2, 4, SPLIT>), dim3((unsigned)blocks), dim3(512), 0, st, p);
+  return check_launch("INT4 GEMM");
+}
+
 template <int BKIND, typename MT, typename OT, int BM, int BN, int WM, int WN, bool GROUPED, bool SPLIT = false>
 static int launch_adma(Mfma16Params p, hipStream_t st) {
   if constexpr (BKIND == B_INT8 && !GROUPED && BM == 256 && WM == 2 && WN == 4) {
@@ -846,6 +1065,14 @@ static int dense16(Mfma16Params p, hipStream_t st) {
       return launch_bytes_fp8(p, st, AKIND == A_E5M2,
                               __is_same(OT, float) ? MLS_F32 : __is_same(OT, _Float16) ? MLS_F16 : MLS_BF16);
   }
+  if constexpr (AKIND == A_RAW16 && BKIND == B_INT4) {
+    // 256 x 128 tiles on the INT4 kernel with the INT8 kernel's schedule, when they take no
+    // more rounds of 256 blocks than the 128 x 256 tiles
+    if (adma && w8 && w4_ok(p)) {
+      const int64_t b_w4 = cdiv(p.M, 256) * cdiv(p.N, 128), b_128 = cdiv(p.M, 128) * cdiv(p.N, 256);
+      if (cdiv(b_w4, 256) <= cdiv(b_128, 256)) return launch_w4<MT, OT>(p, st);
+    }
+  }
   if constexpr (AKIND == A_RAW16) {
     if (adma && w8 && bm == 256) {
       if constexpr (MAXBM >= 256) {
@@ -926,6 +1153,8 @@ int launch_gemm_wq_mfma_split(int wbits, const WqArgs& w, int64_t m_out) {
     if (c192 < c256) return launch_adma<B_INT8, __bf16, float, 256, 192, 2, 4, false, true>(p, w.stream);
     return launch_adma<B_INT8, __bf16, float, 256, 256, 2, 4, false, true>(p, w.stream);
   }
+  if (wbits == 4 && w4_ok(p) && cdiv(cdiv(p.M, 256) * cdiv(p.N, 128), 256) <= cdiv(cdiv(p.M, 128) * cdiv(p.N, 256), 256))
+    return launch_w4<__bf16, float, true>(p, w.stream);
   p.m_tiles = (int)cdiv(p.M, 128);
   if (wbits == 8) return launch_adma<B_INT8, __bf16, float, 128, 256, 2, 4, false, true>(p, w.stream);
   return launch_adma<B_INT4, __bf16, float, 128, 256, 2, 4, false, true>(p, w.stream);

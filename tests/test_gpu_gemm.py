@@ -395,6 +395,24 @@ def test_mfma_int4(dev, M, N, K, gs, dtype):
     _check(int4_matmul(a, p, s, gs), want, f"int4 {M}x{N}x{K} g{gs}")
 
 
+@pytest.mark.parametrize("M,N,K,gs,dtype,sdt", [
+    (1000, 3000, 4096, 128, torch.bfloat16, torch.float16),  # 256 x 128 tiles, M and N ragged, 32 groups
+    (700, 520, 8192, 128, torch.bfloat16, torch.float16),    # 64 groups: the coefficient table's limit
+    (512, 1024, 2048, 32, torch.bfloat16, torch.float16),    # groups of 32: a group end every k-step
+    (600, 640, 1024, 64, torch.float16, torch.float32),      # fp16 x, fp32 scales, groups of 64
+    (300, 256, 16384, 128, torch.bfloat16, torch.float16),   # 128 groups: the 128-row kernel instead
+])
+def test_mfma_int4_256_row_tiles(dev, M, N, K, gs, dtype, sdt):
+    """Shapes that take the 256-row INT4 kernel (widening interleaved with the MFMAs, group
+    scales by summation by parts from a coefficient table in LDS), with partial tiles."""
+    a, w = _data(M, N, K, M + N + K + gs + 11, 0.02)
+    p, s = quantize_int4(w.to(dev), gs)
+    s = s.to(sdt)
+    a = a.to(dtype)
+    want = ref.int4_matmul(a.float().numpy(), p.cpu().numpy(), s.float().cpu().numpy(), gs)
+    _check(int4_matmul(a.to(dev), p, s, gs), want, f"int4 {M}x{N}x{K} g{gs}")
+
+
 def test_config_c_int8_prefill(dev):
     """INT8, x bf16 [2048, 4096], W [11008, 4096], fp16 scales, bf16 out."""
     M, N, K = 2048, 11008, 4096
