@@ -415,6 +415,26 @@ def int8_prefill(dev, steps: int, warmup: int, M=2048, N=11008, K=4096, act=None
     return dict(ms=ms, bytes=nbytes, flops=2 * M * N * K, copies=copies, parity=par)
 
 
+def int4_prefill(dev, steps: int, warmup: int, M=2048, N=11008, K=4096, gs=128):
+    """int4_matmul at config C's prefill shape (INT4 g128 weights, fp16 scales, bf16 x):
+    the reference's INT4 QuantLinear on a 2048-token prompt (dequant_matmul.py:69-100)."""
+    import torch
+    from kernels.dequant_matmul import int4_matmul
+    from serve.quantize import quantize_int4
+    g = torch.Generator(device=dev).manual_seed(4)
+    p, s = quantize_int4(torch.randn(N, K, generator=g, device=dev) * 0.02, gs)
+    s = s.to(torch.float16)
+    copies = 8
+    xs = [torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16) for _ in range(copies)]
+    ps = [p] + [p.clone() for _ in range(copies - 1)]
+    r = _rows(M)
+    par = gate(int4_matmul(xs[0], p, s, gs)[r], xs[0][r].float() @ _deq4(p, s, gs).t(), "bf16")
+    fns = [lambda i=i: int4_matmul(xs[i], ps[i], s, gs) for i in range(copies)]
+    ms = time_steps(fns, warmup, steps) if par["ok"] else None
+    nbytes = N * K // 2 + N * (K // gs) * 2 + M * K * 2 + M * N * 2
+    return dict(ms=ms, bytes=nbytes, flops=2 * M * N * K, copies=copies, parity=par)
+
+
 def fp32_rows(dev, steps: int, warmup: int):
     """fp32 activations at the reference engine's call shapes (its serving path runs fp32
     end to end, serve/engine.py:166): M = 1 / 5 (decode of one / five sequences), 64 (a
@@ -1161,7 +1181,7 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=512)
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--only", default=None,
-                    help="run one workload: int4_gemv, int4_m4, int4_m16, int8_gemv, int8_prefill, "
+                    help="run one workload: int4_gemv, int4_m4, int4_m16, int8_gemv, int8_prefill, int4_prefill, "
                          "fp8_gemm, fp8_native, fp8_bwd, fp8_bwd_native, moe_int4, moe_mlp_int4, paged_attn, "
                          "quantize_int4, ref_shapes, unquantized (the reference's fp16 / dequantize-then-matmul "
                          "comparison rows), fp32 (fp32 activations), clocks (M=1 step split), "
@@ -1195,6 +1215,8 @@ def main(argv=None) -> int:
         "int8_m2": lambda: _hbm_row("int8_gemv_m2", int8_gemv(dev, 2, args.steps, args.warmup)),
         "int8_prefill": lambda: _mfma_row("int8_prefill_2048x11008x4096",
                                           int8_prefill(dev, small, 4), BF16_PEAK_TFLOPS),
+        "int4_prefill": lambda: _mfma_row("int4_prefill_2048x11008x4096_g128", int4_prefill(dev, small, 4),
+                                          BF16_PEAK_TFLOPS),
         "int8_dgrad": lambda: _mfma_row("int8_dgrad_4096x11008x4096_bf16", int8_dgrad_row(dev, small, 4),
                                         BF16_PEAK_TFLOPS,
                                         {"launches": "dy*s to bf16, W_q^T copy, INT8 MFMA GEMM (unit scales)"}),
@@ -1267,7 +1289,8 @@ def main(argv=None) -> int:
         return 1
     extra = []
     if not args.no_extra:
-        for k in ("int4_m2", "int4_m4", "int4_m16", "int8_gemv", "int8_m2", "int8_prefill", "fp32", "int8_dgrad",
+        for k in ("int4_m2", "int4_m4", "int4_m16", "int8_gemv", "int8_m2", "int8_prefill", "int4_prefill", "fp32",
+                  "int8_dgrad",
                   "fp8_gemm", "fp8_native",
                   "fp8_bwd", "fp8_bwd_native", "moe_int4", "moe_mlp_int4", "paged_attn", "quantize_int4",
                   "ref_shapes", "unquantized", "copy", "floor", "clocks", "vendor_fp8_rowwise", "vendor_fp8_tensorwise",
