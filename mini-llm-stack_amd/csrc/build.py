@@ -25,13 +25,25 @@ BUILD = CSRC / "_build"
 SOURCES = ["abi.hip", "e4m3.hip", "quant.hip", "gemv.hip", "gemv_mfma.hip", "gemv_mfma8.hip", "gemm_mfma16.hip", "gemm_grouped.hip",
            "wq_abi.hip", "gemm_small.hip", "gemm_bytes.hip", "gemm_fp8.hip", "dgrad.hip", "moe.hip", "transpose.hip", "paged_attn.hip", "split.hip"]
 ARCH = "gfx950"
-# Per-source device-code options. gemv_mfma.hip (the skinny GEMM's INT4 kernels): MFMA
-# results in VGPRs (the kernel scales every MFMA result with VALU FMAs; in AGPRs each one is
-# first copied back with v_accvgpr_read, 56 extra VALU instructions per wavefront at
-# K = 4096). Its INT8 kernels (gemv_mfma8.hip) measured slower that way and keep the default.
-EXTRA_FLAGS = {"gemv_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-               "gemm_small.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-               "gemm_grouped.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+# Per-source device-code options.
+# - Kernel-argument preloading (gemv.hip, gemv_mfma*.hip, and bench.py's calibration kernels
+#   in floor.hip): the first 14 dwords of a kernel's arguments arrive in SGPRs at wavefront
+#   start, so the microsecond kernels issue their first loads without a scalar-load round
+#   trip for the arguments (their argument lists put what those loads need first). The code
+#   object keeps a prologue that loads them for firmware without preloading.
+# - gemv_mfma.hip (the skinny GEMM's INT4 kernels), gemm_small.hip, gemm_grouped.hip: MFMA
+#   results in VGPRs (the kernels scale MFMA results with VALU FMAs; in AGPRs each one is
+#   first copied back with v_accvgpr_read, 56 extra VALU instructions per wavefront in the
+#   skinny kernel at K = 4096). The skinny INT8 kernels (gemv_mfma8.hip) measured slower
+#   that way and keep the default.
+PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
+VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+EXTRA_FLAGS = {"gemv.hip": PRELOAD,
+               "floor.hip": PRELOAD,
+               "gemv_mfma.hip": VGPR_FORM + PRELOAD,
+               "gemv_mfma8.hip": PRELOAD,
+               "gemm_small.hip": VGPR_FORM,
+               "gemm_grouped.hip": VGPR_FORM}
 
 
 def hipcc() -> str:

@@ -104,14 +104,16 @@ __global__ __launch_bounds__(256) void floor_stream_kernel(const u32x4_t* __rest
 
 // The library's M = 1 GEMV (gemv1.h) with 16-bit activations and fp16 scales, clocked.
 template <int WBITS, typename AT, int CPL, int R, int XI, int SI, bool WAIT>
+// Arguments in the library kernel's order (both files are built with kernel-argument preloading).
 __global__ __launch_bounds__(256) void floor_gemv1_clocked_kernel(const AT* __restrict__ x,
-                                                                  const uint8_t* __restrict__ w, int ldw,
-                                                                  int w_bytes, const _Float16* __restrict__ s,
-                                                                  int s_row_bytes, int s_bytes, int group,
-                                                                  AT* __restrict__ y, int N, int K, int s_dw,
+                                                                  const uint8_t* __restrict__ w,
+                                                                  const _Float16* __restrict__ s, int K, int N,
+                                                                  int ldw, int s_bytes, int s_dw, int s_row_bytes,
+                                                                  int group, AT* __restrict__ y,
                                                                   uint64_t* __restrict__ clocks) {
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   __builtin_amdgcn_sched_barrier(0);
+  const int w_bytes = (int)((uint32_t)N * (uint32_t)ldw);
   mls::gemv1_body<WBITS, AT, _Float16, CPL, R, XI, SI, 1>(x, w, ldw, w_bytes, s, s_row_bytes, s_bytes, group, y,
                                                            N, K, s_dw, 0, 1, 0);
   store_clocks<WAIT>(clocks, t0);
@@ -199,9 +201,9 @@ extern "C" int mlsf_gemv1_clocked(int wbits, const void* x, const uint8_t* w, in
     const int blocks = (int)((N + 15) / 16);
     auto go = [&](auto wc) {
       hipLaunchKernelGGL((floor_gemv1_clocked_kernel<4, __bf16, 2, 4, 2, 1, decltype(wc)::value>),
-                         dim3((unsigned)blocks), dim3(256), 0, st, (const __bf16*)x, w, (int)ldw, (int)(N * ldw),
-                         (const _Float16*)s, (int)(ld_sn * 2), (int)(((N - 1) * ld_sn + 32) * 2), group, (__bf16*)y,
-                         (int)N, (int)K, 16, clocks);
+                         dim3((unsigned)blocks), dim3(256), 0, st, (const __bf16*)x, w, (const _Float16*)s, (int)K,
+                         (int)N, (int)ldw, (int)(((N - 1) * ld_sn + 32) * 2), 16, (int)(ld_sn * 2), group,
+                         (__bf16*)y, clocks);
     };
     if (wait) go(std::true_type{});
     else go(std::false_type{});
@@ -212,8 +214,8 @@ extern "C" int mlsf_gemv1_clocked(int wbits, const void* x, const uint8_t* w, in
     const int blocks = (int)((N + 3) / 4);
     auto go = [&](auto wc) {
       hipLaunchKernelGGL((floor_gemv1_clocked_kernel<8, __bf16, 4, 1, 2, 1, decltype(wc)::value>),
-                         dim3((unsigned)blocks), dim3(256), 0, st, (const __bf16*)x, w, (int)ldw, (int)(N * ldw),
-                         (const _Float16*)s, 2, 0, 0, (__bf16*)y, (int)N, (int)K, 0, clocks);
+                         dim3((unsigned)blocks), dim3(256), 0, st, (const __bf16*)x, w, (const _Float16*)s, (int)K,
+                         (int)N, (int)ldw, 0, 0, 2, 0, (__bf16*)y, clocks);
     };
     if (wait) go(std::true_type{});
     else go(std::false_type{});

@@ -96,14 +96,20 @@ __global__ __launch_bounds__(256) void gemv_wq_kernel(
   }
 }
 
-// M = 1 (and M = 2) with 16-bit activations: x and the group scales through LDS (gemv1.h)
+// M = 1 (and M = 2) with 16-bit activations: x and the group scales through LDS (gemv1.h).
+// This file is built with kernel-argument preloading: the first 14 dwords of the arguments
+// arrive in SGPRs at wavefront start. They hold everything the kernel needs before its
+// weight loads, so no load waits for a scalar load of the arguments (the output pointer and
+// stride come last). The weight buffer's size is N ldw (as the 32-bit product), and the
+// launcher takes MX = M.
 template <int WBITS, typename AT, typename ST, int CPL, int R, int XI, int SI, int MX>
 __global__ __launch_bounds__(256) void gemv1_kernel(const AT* __restrict__ x, const uint8_t* __restrict__ w,
-                                                    int ldw, int w_bytes, const ST* __restrict__ s, int s_row_bytes,
-                                                    int s_bytes, int group, AT* __restrict__ y, int N, int K,
-                                                    int s_dw, int lda_b, int M, int ldy) {
+                                                    const ST* __restrict__ s, int K, int N, int ldw, int s_bytes,
+                                                    int s_dw, int s_row_bytes, int group, int lda_b,
+                                                    AT* __restrict__ y, int ldy) {
+  const int w_bytes = (int)((uint32_t)N * (uint32_t)ldw);
   gemv1_body<WBITS, AT, ST, CPL, R, XI, SI, MX>(x, w, ldw, w_bytes, s, s_row_bytes, s_bytes, group, y, N, K, s_dw,
-                                                lda_b, M, ldy);
+                                                lda_b, MX, ldy);
 }
 
 template <int WBITS, typename AT, typename ST, int CPL, int SI>
@@ -128,9 +134,8 @@ static int launch_gemv1_si(const WqArgs& p, int s_dw) {
   auto go = [&](auto mxc, auto rc) {
     constexpr int MX = decltype(mxc)::value, R = decltype(rc)::value;
     hipLaunchKernelGGL((gemv1_kernel<WBITS, AT, ST, CPL, R, XI, SI, MX>), dim3((unsigned)cdiv(p.N, 4 * R)), dim3(256),
-                       0, p.stream, (const AT*)p.a, p.w, (int)p.ldw, (int)(p.N * p.ldw), (const ST*)p.s, s_row_bytes,
-                       s_bytes, p.group, (AT*)p.c, (int)p.N, (int)p.K, s_dw, (int)(mx > 1 ? lda_b : 0), (int)p.M,
-                       (int)(mx > 1 ? p.ldc : 0));
+                       0, p.stream, (const AT*)p.a, p.w, (const ST*)p.s, (int)p.K, (int)p.N, (int)p.ldw, s_bytes,
+                       s_dw, s_row_bytes, p.group, (int)(mx > 1 ? lda_b : 0), (AT*)p.c, (int)(mx > 1 ? p.ldc : 0));
     return MLS_OK;
   };
   using I1 = std::integral_constant<int, 1>;

@@ -379,6 +379,7 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
     for (int j = 0; j < CPL; ++j)
       wv[r][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, lane * 16 + 1024 * j,
                                                                                  (n0 + r) * ldw, 2));
+  __builtin_amdgcn_sched_barrier(0);  // nothing below (e.g. the group division's setup) ahead of the loads
 
   // the slice index of each (row, chunk)'s group scale (a division by the runtime group
   // size), computed while the loads are in flight instead of after the barrier

@@ -139,10 +139,15 @@ constexpr int SLG = 16;
 template <int WBITS, typename AT, typename ST, int R, int WAVES, int U, bool SL, bool XL, bool S64, bool SPL = false>
 // One wavefront per SIMD is the design point (a grid of N / 16 blocks of WAVES
 // wavefronts), so the compiler may spend registers on keeping a chunk's loads in flight.
+// The files that instantiate this kernel are built with kernel-argument preloading (the
+// first 14 dwords of the arguments arrive in SGPRs at wavefront start): everything the
+// first loads need comes first, with the strides as 32-bit values (launch_one checks that
+// they fit), and the output pointer and stride last.
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2))) void gemv_mfma_kernel(
-    const AT* __restrict__ a, int64_t lda, const uint8_t* __restrict__ w, int64_t ldw,
-    const ST* __restrict__ s, int64_t ld_sn, int64_t ld_sg, int group,
-    std::conditional_t<SPL, float, AT>* __restrict__ c, int64_t ldc, int M, int N, int K) {
+    const AT* __restrict__ a, const uint8_t* __restrict__ w, const ST* __restrict__ s, int K, int N, int M,
+    int lda32, int ldw32, int ld_sn32, int ld_sg32, int group, std::conditional_t<SPL, float, AT>* __restrict__ c,
+    int64_t ldc) {
+  const int64_t lda = lda32, ldw = ldw32, ld_sn = ld_sn32, ld_sg = ld_sg32;
   using OT = std::conditional_t<SPL, float, AT>;
   static_assert(!(SPL && XL), "split x comes from global");
   constexpr int XPARTS = SPL ? 2 : 1;
@@ -422,13 +427,16 @@ int launch_one(const WqArgs& p) {
   static const bool xl_env = env_int("MLS_GEMV_MFMA_XL", 1) != 0;
   constexpr bool XL_FITS = !SPL && WAVES * U * 16 * KB * 2 <= 128 * 1024;
   const bool xl = XL_FITS && xl_env && per_wave <= U;
+  // the strides travel as 32-bit kernel arguments
+  if (p.lda > 0x7FFFFFFF || p.ldw > 0x7FFFFFFF || p.ld_sn > 0x7FFFFFFF || p.ld_sg > 0x7FFFFFFF)
+    return MLS_ERR_UNSUPPORTED;
   using OT = std::conditional_t<SPL, float, AT>;
   auto go = [&](auto slc, auto xlc) {
     hipLaunchKernelGGL((gemv_mfma_kernel<WBITS, AT, ST, R, WAVES, U, decltype(slc)::value, decltype(xlc)::value, S64,
                                          SPL>),
-                       dim3((unsigned)blocks), dim3(64 * WAVES), 0, p.stream, static_cast<const AT*>(p.a), p.lda, p.w,
-                       p.ldw, static_cast<const ST*>(p.s), p.ld_sn, p.ld_sg, p.group, static_cast<OT*>(p.c), p.ldc,
-                       (int)p.M, (int)p.N, (int)p.K);
+                       dim3((unsigned)blocks), dim3(64 * WAVES), 0, p.stream, static_cast<const AT*>(p.a), p.w,
+                       static_cast<const ST*>(p.s), (int)p.K, (int)p.N, (int)p.M, (int)p.lda, (int)p.ldw,
+                       (int)p.ld_sn, (int)p.ld_sg, p.group, static_cast<OT*>(p.c), p.ldc);
   };
   using T_ = std::true_type;
   using F_ = std::false_type;

@@ -87,7 +87,7 @@ bool split_ok(int wbits, const WqArgs& p) {
   if (p.M <= 16 && wbits == 4 && p.group % 128 == 0 && p.K % 128 != 0) return false;  // (K % group == 0 anyway)
   const int64_t m2 = split_rows(p.M);
   return m2 <= 0x3FFFFFFF && p.N <= 0x3FFFFFFF && p.K <= 0x3FFFFFFF && p.K * 2 * 256 < (1ll << 31) &&
-         p.ldw * 256 < (1ll << 31);
+         p.ldw * 256 < (1ll << 31) && p.ld_sn <= 0x7FFFFFFF && p.ld_sg <= 0x7FFFFFFF;
 }
 
 int64_t split_ws_bytes(const WqArgs& p) { return split_rows(p.M) * p.K * 2; }
