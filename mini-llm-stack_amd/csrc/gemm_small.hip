@@ -95,7 +95,13 @@ __device__ __forceinline__ uint32_t andor(uint32_t a, uint32_t m, uint32_t c) { 
 // wavefront reads only its own slice, so its own vmcnt wait is the only synchronisation.
 template <int WBITS, typename AT, typename ST, int TM, int TN, int D, bool S64 = false, bool SPLIT = false, int WV = 4,
           bool XLS = false>
-__global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) {
+// The arguments the first loads need come first, as scalars: this file is built with
+// kernel-argument preloading (the first 14 dwords arrive in SGPRs at wavefront start), so
+// those loads issue without waiting for a scalar load of the arguments. p (not preloaded)
+// holds the rest; its copies of these fields are not read.
+__global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const void* pa, const uint8_t* pw, int lda, int a_bytes,
+                                                            int ldw, int w_bytes, int N, int K, int x_lds, int xs_log2,
+                                                            const SmallArgs p) {
   using MM = Mfma16<AT>;
   // split rows: 16-row tiles 2t and 2t + 1 hold the hi and lo parts of output rows
   // m0 / 2 + 16 t .. + 15, added in the epilogue; the output is fp32
@@ -116,26 +122,21 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
   // and the weight tile is fetched from HBM once.
   const int nt = blockIdx.x, mt = blockIdx.y;
   const int m0 = mt * 16 * TM, n0 = nt * 16 * TN;
-  if (n0 >= p.N) return;  // padding column tile
-  const int nsteps = p.K / KS;
+  if (n0 >= N) return;  // padding column tile
+  const int nsteps = K / KS;
   const int s_lo = nsteps * wave / WV, s_hi = nsteps * (wave + 1) / WV;
 
-  // every argument into SGPRs at once (one round of kernel-argument loads)
-  asm volatile("" ::"s"(p.a), "s"(p.lda), "s"(p.a_bytes), "s"(p.w), "s"(p.ldw), "s"(p.w_bytes), "s"(p.s),
-               "s"(p.ld_sn), "s"(p.group), "s"(p.s_bytes), "s"(p.c), "s"(p.ldc), "s"(p.M), "s"(p.N), "s"(p.K),
-               "s"(p.G));
-
   // ---- operand descriptors and this lane's offsets (nothing else before the first loads)
-  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc((void*)p.a, (short)0, p.a_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc((void*)p.w, (short)0, p.w_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc((void*)pa, (short)0, a_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc((void*)pw, (short)0, w_bytes, 0x00020000);
   int xo[TM];
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) xo[tm] = (m0 + 16 * tm + r16) * p.lda * 2 + XP * 16 * q;
+  for (int tm = 0; tm < TM; ++tm) xo[tm] = (m0 + 16 * tm + r16) * lda * 2 + XP * 16 * q;
   int wo[TN];
 #pragma unroll
-  for (int tn = 0; tn < TN; ++tn) wo[tn] = (n0 + 16 * tn + r16) * p.ldw + WB * q;
+  for (int tn = 0; tn < TN; ++tn) wo[tn] = (n0 + 16 * tn + r16) * ldw + WB * q;
 
-  uint8_t* xsl = smem + p.x_lds + wave * ((16 * TM) << (p.xs_log2 + 4));
+  uint8_t* xsl = smem + x_lds + wave * ((16 * TM) << (xs_log2 + 4));
 
   struct Slot {
     uint4 x[XLS ? 1 : TM][XLS ? 1 : XP];
@@ -170,13 +171,13 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
   // issued first the weights' latency runs under the slice's transfer (issued after the
   // slice, they queued behind all of it: the reference's bench shape, INT8 M = 128, ~0.2 us)
   if constexpr (XLS) {
-    const int cpr_mask = (1 << p.xs_log2) - 1;
-    const int total = (16 * TM) << p.xs_log2;  // chunks of the slice
+    const int cpr_mask = (1 << xs_log2) - 1;
+    const int total = (16 * TM) << xs_log2;  // chunks of the slice
     for (int c0 = 0; c0 < total; c0 += 64) {
-      const int sidx = c0 + lane, row = sidx >> p.xs_log2, cp = sidx & cpr_mask;
+      const int sidx = c0 + lane, row = sidx >> xs_log2, cp = sidx & cpr_mask;
       const int cl = cp ^ (row & 7);  // logical chunk stored at physical slot cp
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (__attribute__((address_space(3))) void*)(xsl + c0 * 16), 16,
-                                               (m0 + row) * p.lda * 2 + cl * 16, s_lo * KS * 2, 0, 0);
+                                               (m0 + row) * lda * 2 + cl * 16, s_lo * KS * 2, 0, 0);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -185,6 +186,10 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
     __builtin_amdgcn_s_waitcnt(0 | 0x70 | 0xF00);
     asm volatile("" ::: "memory");
   }
+
+  // the remaining arguments into SGPRs at once (one round of scalar loads, issued at entry
+  // and waited for here, after the first loads)
+  asm volatile("" ::"s"(p.s), "s"(p.ld_sn), "s"(p.group), "s"(p.s_bytes), "s"(p.c), "s"(p.ldc), "s"(p.M), "s"(p.G));
 
   // ---- INT4 group scales of the block's 16 TN rows into LDS ([row][group] in ST), issued
   // after the first two steps' operands: the first step waits for nearly all of those
@@ -225,7 +230,7 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
       const bool live = st < s_hi;  // wave-uniform
       const int row = 16 * tm + r16;
       const int cl = (live ? st - s_lo : 0) * (KS * 2 / 16) + XP * q + h;
-      const uint4 v = *reinterpret_cast<const uint4*>(xsl + ((row << p.xs_log2) + (cl ^ (row & 7))) * 16);
+      const uint4 v = *reinterpret_cast<const uint4*>(xsl + ((row << xs_log2) + (cl ^ (row & 7))) * 16);
       return live ? v : make_uint4(0u, 0u, 0u, 0u);
     } else {
       return sl.x[tm][h];
@@ -318,19 +323,19 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const SmallArgs p) 
       m = m0 + 16 * to + (l & 15);
     }
     const int nb = n0 + 16 * tn + 4 * (l >> 4);
-    if (m >= (SPLIT ? p.m_out : p.M) || nb >= p.N) continue;
+    if (m >= (SPLIT ? p.m_out : p.M) || nb >= N) continue;
     if constexpr (!I4) {
       const ST* sv = static_cast<const ST*>(p.s);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] *= to_f32(sv[min(nb + i, p.N - 1)]);
+      for (int i = 0; i < 4; ++i) v[i] *= to_f32(sv[min(nb + i, N - 1)]);
     }
     OT* dst = c + (int64_t)m * p.ldc + nb;
-    if (nb + 3 < p.N && ((uintptr_t)dst & (SPLIT ? 15 : 7)) == 0) {
+    if (nb + 3 < N && ((uintptr_t)dst & (SPLIT ? 15 : 7)) == 0) {
       store4<OT>(dst, v[0], v[1], v[2], v[3]);
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (nb + i < p.N) dst[i] = from_f32<OT>(v[i]);
+        if (nb + i < N) dst[i] = from_f32<OT>(v[i]);
     }
   }
 }
@@ -367,7 +372,8 @@ int launch_small_wv(SmallArgs a, hipStream_t st) {
       attr_set = true;
     }
   }
-  hipLaunchKernelGGL(kern, dim3((unsigned)nt, (unsigned)a.m_tiles), dim3(64 * WV), lds, st, a);
+  hipLaunchKernelGGL(kern, dim3((unsigned)nt, (unsigned)a.m_tiles), dim3(64 * WV), lds, st, a.a, a.w, a.lda,
+                     a.a_bytes, a.ldw, a.w_bytes, a.N, a.K, a.x_lds, a.xs_log2, a);
   return MLS_OK;
 }
 
