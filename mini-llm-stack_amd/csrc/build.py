@@ -26,8 +26,8 @@ SOURCES = ["abi.hip", "e4m3.hip", "quant.hip", "gemv.hip", "gemv_mfma.hip", "gem
            "wq_abi.hip", "gemm_small.hip", "gemm_bytes.hip", "gemm_fp8.hip", "dgrad.hip", "moe.hip", "transpose.hip", "paged_attn.hip", "split.hip"]
 ARCH = "gfx950"
 # Per-source device-code options.
-# - Kernel-argument preloading (gemv.hip, gemv_mfma*.hip, gemm_small.hip, and bench.py's
-#   calibration kernels in floor.hip): the first 14 dwords of a kernel's arguments arrive in SGPRs at wavefront
+# - Kernel-argument preloading (gemv.hip, gemv_mfma*.hip, gemm_small.hip, split.hip, and
+#   bench.py's calibration kernels in floor.hip): the first 14 dwords of a kernel's arguments arrive in SGPRs at wavefront
 #   start, so the microsecond kernels issue their first loads without a scalar-load round
 #   trip for the arguments (their argument lists put what those loads need first). The code
 #   object keeps a prologue that loads them for firmware without preloading.
@@ -43,7 +43,8 @@ EXTRA_FLAGS = {"gemv.hip": PRELOAD,
                "gemv_mfma.hip": VGPR_FORM + PRELOAD,
                "gemv_mfma8.hip": PRELOAD,
                "gemm_small.hip": VGPR_FORM + PRELOAD,
-               "gemm_grouped.hip": VGPR_FORM}
+               "gemm_grouped.hip": VGPR_FORM,
+               "split.hip": PRELOAD}
 
 
 def hipcc() -> str:

@@ -9,10 +9,13 @@ namespace mls {
 // Chunks past K contribute nothing (their term is selected away); rows past N or
 // M are computed on clamped data and never stored.
 template <int WBITS, typename AT, typename ST, int MT, int CPL, int R>
+// Arguments for kernel-argument preloading (the first 14 dwords arrive in SGPRs): what the
+// loads need first, strides as 32-bit values (launch_gemv_wq checks that they fit), the
+// output last.
 __global__ __launch_bounds__(256) void gemv_wq_kernel(
-    const AT* __restrict__ x, int64_t ldx, const uint8_t* __restrict__ w, int64_t ldw,
-    const ST* __restrict__ s, int64_t ld_sn, int64_t ld_sg, int group,
-    AT* __restrict__ y, int64_t ldy, int M, int N, int K) {
+    const AT* __restrict__ x, const uint8_t* __restrict__ w, const ST* __restrict__ s, int K, int N, int M,
+    int ldx32, int ldw32, int ld_sn32, int ld_sg32, int group, AT* __restrict__ y, int64_t ldy) {
+  const int64_t ldx = ldx32, ldw = ldw32, ld_sn = ld_sn32, ld_sg = ld_sg32;
   using S = XSlot<WBITS, AT>;
   constexpr int KC = S::KC, NV = S::NV;
   constexpr float OFF = code_offset<WBITS, AT>();
@@ -209,8 +212,8 @@ template <int WBITS, typename AT, typename ST, int MT, int CPL, int R>
 static void launch_r(const WqArgs& p) {
   const dim3 grid((unsigned)cdiv(p.N, 4 * R), (unsigned)cdiv(p.M, MT));
   hipLaunchKernelGGL((gemv_wq_kernel<WBITS, AT, ST, MT, CPL, R>), grid, dim3(256), 0, p.stream,
-                     (const AT*)p.a, p.lda, p.w, p.ldw, (const ST*)p.s, p.ld_sn, p.ld_sg, p.group,
-                     (AT*)p.c, p.ldc, (int)p.M, (int)p.N, (int)p.K);
+                     (const AT*)p.a, p.w, (const ST*)p.s, (int)p.K, (int)p.N, (int)p.M, (int)p.lda, (int)p.ldw,
+                     (int)p.ld_sn, (int)p.ld_sg, p.group, (AT*)p.c, p.ldc);
 }
 
 // Rows per wavefront: by default enough that each lane has 8 weight chunks in
@@ -289,6 +292,9 @@ int launch_gemv_wq(int wbits, const WqArgs& p) {
   if (p.N > 0x7FFFFFFF / 2 || p.M > 4 * 65535) return MLS_ERR_UNSUPPORTED;  // grid.y = M / MT
   const int rc = p.M == 1 ? launch_gemv1(wbits, p) : MLS_ERR_UNSUPPORTED;
   if (rc != MLS_ERR_UNSUPPORTED) return rc;
+  // gemv_wq_kernel takes the strides as 32-bit arguments
+  if (p.lda > 0x7FFFFFFF || p.ldw > 0x7FFFFFFF || p.ld_sn > 0x7FFFFFFF || p.ld_sg > 0x7FFFFFFF)
+    return MLS_ERR_UNSUPPORTED;
   if (wbits == 4) {
     if (p.a_dt == MLS_F32) return dispatch_st<4, float>(p);
     if (p.a_dt == MLS_F16) return dispatch_st<4, _Float16>(p);
