@@ -219,6 +219,11 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const void* pa, con
     for (int tm = 0; tm < TM; ++tm) acc[tn][tm] = f32x4{0.f, 0.f, 0.f, 0.f};
   uint32_t nmask = 0x000F000Fu, magic = Nib<AT>::MAGIC;
   asm volatile("" : "+v"(nmask), "+v"(magic));
+  constexpr bool F16I8 = !I4 && std::is_same_v<AT, _Float16> && !SPLIT;
+  const uint32_t hi64 = 0x64646464u;  // the fp16 high byte of 1024 + u (F16I8)
+  f32x4 xsum[TM];                     // F16I8: sum_k x of row tile tm over this wavefront's steps
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) xsum[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
   const uint4 ones = make_uint4(Nib<AT>::ONE2, Nib<AT>::ONE2, Nib<AT>::ONE2, Nib<AT>::ONE2);
   const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -273,6 +278,35 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const void* pa, con
           for (int i = 0; i < 4; ++i) acc[tn][tm][i] = fmaf(sc[i], fmaf(-Nib<AT>::OFF, xs[tm][i], pp[i]), acc[tn][tm][i]);
         }
       }
+    } else if constexpr (F16I8) {
+      // INT8 with fp16 x: u = q ^ 0x80 = q + 128 goes into the low byte of an fp16 whose
+      // high byte is 0x64 (one v_perm per two weights): exactly 1024 + u = 1152 + q. The
+      // 1152 sum_k x is removed after the loop, from x's row sums (an MFMA against ones).
+      uint4 xv[TM][2];
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) {
+        xv[tm][0] = x_piece(sl, st, tm, 0);
+        xv[tm][1] = x_piece(sl, st, tm, 1);
+        xsum[tm] = MM::mma(ones, xv[tm][0], xsum[tm]);
+        xsum[tm] = MM::mma(ones, xv[tm][1], xsum[tm]);
+      }
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const uint32_t d[4] = {sl.w[tn].x ^ 0x80808080u, sl.w[tn].y ^ 0x80808080u, sl.w[tn].z ^ 0x80808080u,
+                               sl.w[tn].w ^ 0x80808080u};
+        uint32_t o[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          o[2 * j + 0] = __builtin_amdgcn_perm(hi64, d[j], 0x04010400u);
+          o[2 * j + 1] = __builtin_amdgcn_perm(hi64, d[j], 0x04030402u);
+        }
+        const uint4 w0 = make_uint4(o[0], o[1], o[2], o[3]), w1 = make_uint4(o[4], o[5], o[6], o[7]);
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) {
+          acc[tn][tm] = MM::mma(w0, xv[tm][0], acc[tn][tm]);
+          acc[tn][tm] = MM::mma(w1, xv[tm][1], acc[tn][tm]);
+        }
+      }
     } else {
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
@@ -294,6 +328,13 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const void* pa, con
       compute(sl[d], st + d);
       load(sl[d], st + d + D);
     }
+  }
+
+  if constexpr (F16I8) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) acc[tn][tm] -= 1152.0f * xsum[tm];
   }
 
   // ---- the WV partial tiles meet in LDS; each thread finishes TN * TM / WV accumulators
