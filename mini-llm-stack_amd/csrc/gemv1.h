@@ -32,6 +32,11 @@ __device__ __forceinline__ float load_scale(const void* s, int s_dt, int64_t i) 
   return s_dt == MLS_F16 ? (float)((const _Float16*)s)[i] : ((const float*)s)[i];
 }
 
+__device__ __forceinline__ float ub0(uint32_t v) { return (float)(v & 0xFFu); }
+__device__ __forceinline__ float ub1(uint32_t v) { return (float)((v >> 8) & 0xFFu); }
+__device__ __forceinline__ float ub2(uint32_t v) { return (float)((v >> 16) & 0xFFu); }
+__device__ __forceinline__ float ub3(uint32_t v) { return (float)(v >> 24); }
+
 template <typename AT> struct Half16;
 
 template <> struct Half16<__bf16> {
@@ -49,6 +54,13 @@ template <> struct Half16<__bf16> {
     v.y = (__bf16)hi;
     return __builtin_bit_cast(uint32_t, v);
   }
+  // INT8: bytes H2, H2 + 1 of u (biased codes q + 128) as the pair (u, u'); code_offset
+  // is 128
+  template <int H2>
+  __device__ static __forceinline__ uint32_t byte_pair(uint32_t u) {
+    if constexpr (H2 == 0) return pack2(ub0(u), ub1(u));
+    else return pack2(ub2(u), ub3(u));
+  }
 };
 
 template <> struct Half16<_Float16> {
@@ -62,12 +74,14 @@ template <> struct Half16<_Float16> {
   __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
   }
+  // INT8: bytes H2, H2 + 1 of u (biased codes q + 128) as the exact pair (1024 + u,
+  // 1024 + u'): each byte becomes the low byte of an fp16 with high byte 0x64, one v_perm
+  // per pair (code_offset is 1152 = 1024 + 128)
+  template <int H2>
+  __device__ static __forceinline__ uint32_t byte_pair(uint32_t u) {
+    return __builtin_amdgcn_perm(0x64646464u, u, H2 == 0 ? 0x04010400u : 0x04030402u);
+  }
 };
-
-__device__ __forceinline__ float ub0(uint32_t v) { return (float)(v & 0xFFu); }
-__device__ __forceinline__ float ub1(uint32_t v) { return (float)((v >> 8) & 0xFFu); }
-__device__ __forceinline__ float ub2(uint32_t v) { return (float)((v >> 16) & 0xFFu); }
-__device__ __forceinline__ float ub3(uint32_t v) { return (float)(v >> 24); }
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -205,8 +219,8 @@ __device__ __forceinline__ float chunk_dot(const uint4 wq, const uint32_t* xr, u
         acc = fmaf(ub3(u), x[3], acc);
       } else {
         using H = Half16<AT>;
-        acc = H::dot2(H::pack2(ub0(u), ub1(u)), xr[2 * t + 0], acc);
-        acc = H::dot2(H::pack2(ub2(u), ub3(u)), xr[2 * t + 1], acc);
+        acc = H::dot2(H::template byte_pair<0>(u), xr[2 * t + 0], acc);
+        acc = H::dot2(H::template byte_pair<2>(u), xr[2 * t + 1], acc);
       }
     }
   }
@@ -235,8 +249,8 @@ __device__ __forceinline__ void chunk_widen(const uint4 wq, uint32_t nib_mask, u
       w.v[4 * b + 3] = and_or(q[b] >> 12, nib_mask, magic);
     } else {
       const uint32_t u = q[b] ^ 0x80808080u;
-      w.v[2 * b + 0] = H::pack2(ub0(u), ub1(u));
-      w.v[2 * b + 1] = H::pack2(ub2(u), ub3(u));
+      w.v[2 * b + 0] = H::template byte_pair<0>(u);
+      w.v[2 * b + 1] = H::template byte_pair<2>(u);
     }
   }
 }
@@ -253,7 +267,7 @@ __device__ __forceinline__ float pairs_dot(const WPairs<WBITS, AT>& w, const uin
 
 template <int WBITS, typename AT>
 constexpr float code_offset() {
-  if constexpr (WBITS == 8) return 128.0f;
+  if constexpr (WBITS == 8) return std::is_same_v<AT, _Float16> ? 1152.0f : 128.0f;
   else if constexpr (sizeof(AT) == 4) return 8.0f;
   else return Half16<AT>::OFF4;
 }

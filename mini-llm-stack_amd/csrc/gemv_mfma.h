@@ -44,6 +44,7 @@ template <> struct Mx<__bf16> {
   static constexpr uint32_t MAGIC = 0x43004300u;  // bf16 (128, 128)
   static constexpr float OFF4 = 136.0f;
   static constexpr uint32_t ONE2 = 0x3F803F80u;   // bf16 (1, 1)
+  static constexpr float I8OFF = 128.0f;           // INT8 operands hold q + 128
   __device__ static __forceinline__ f32x4 mma(const uint4& a, const uint4& b, const f32x4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -58,6 +59,7 @@ template <> struct Mx<_Float16> {
   static constexpr uint32_t MAGIC = 0x64006400u;  // fp16 (1024, 1024)
   static constexpr float OFF4 = 1032.0f;
   static constexpr uint32_t ONE2 = 0x3C003C00u;   // fp16 (1, 1)
+  static constexpr float I8OFF = 1152.0f;          // INT8 operands hold 1024 + q + 128
   __device__ static __forceinline__ f32x4 mma(const uint4& a, const uint4& b, const f32x4& c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
@@ -102,10 +104,15 @@ __device__ __forceinline__ uint4 x_perm(const uint4& v) {
                     __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
 }
 
-// INT8: 8 bytes (two dwords, k order) -> 8 exact 16-bit values q + 128
+// INT8: 8 bytes (two dwords, k order) -> 8 exact 16-bit values q + 128 (bf16), or
+// 1024 + q + 128 for fp16: each biased byte u becomes the low byte of an fp16 whose high
+// byte is 0x64, one v_perm per pair (Mx<AT>::I8OFF is what the operands add to q)
 template <typename AT>
 __device__ __forceinline__ uint4 byte_operand(uint32_t d0, uint32_t d1) {
   const uint32_t u = d0 ^ 0x80808080u, v = d1 ^ 0x80808080u;
+  if constexpr (std::is_same_v<AT, _Float16>)
+    return make_uint4(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u),
+                      __builtin_amdgcn_perm(0x64646464u, v, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, v, 0x04030402u));
   return make_uint4(Mx<AT>::pack_int((float)(u & 0xFFu), (float)((u >> 8) & 0xFFu)),
                     Mx<AT>::pack_int((float)((u >> 16) & 0xFFu), (float)(u >> 24)),
                     Mx<AT>::pack_int((float)(v & 0xFFu), (float)((v >> 8) & 0xFFu)),
@@ -374,7 +381,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
     for (int t = 0; t < R; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(-128.0f, xsum[i], acc[t][i]);
+      for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(-Mx<AT>::I8OFF, xsum[i], acc[t][i]);
   }
 
   // ---- sum the wavefronts' partial results, scale (INT8), store
