@@ -1,5 +1,7 @@
 // Decode-shaped weight-only GEMM (small M): the HBM-bound family. The lane layout, the
 // dequantising dot products and the M = 1 kernel's body are in gemv1.h.
+#include <type_traits>
+
 #include "gemv1.h"
 
 namespace mls {
@@ -118,10 +120,11 @@ __global__ __launch_bounds__(256) void gemv1_kernel(const AT* __restrict__ x, co
 template <int WBITS, typename AT, typename ST, int CPL, int SI>
 static int launch_gemv1_si(const WqArgs& p, int s_dw) {
   constexpr int R2 = CPL >= 8 ? 1 : 8 / CPL;  // rows per wavefront: 8 loads per lane
-  // x instructions per wavefront: 4 wavefronts x 1 KiB cover 2K bytes (INT4: K <= 2048 CPL;
-  // INT8: K <= 1024 CPL)
-  constexpr int XI = WBITS == 4 ? CPL : (CPL >= 2 ? CPL / 2 : 1);
-  if (p.K * 2 > XI * 4096) return MLS_ERR_UNSUPPORTED;
+  // x instructions per wavefront: 4 wavefronts x 1 KiB cover the K sizeof(AT) bytes of x
+  // (16-bit x: INT4 K <= 2048 CPL, INT8 K <= 1024 CPL; fp32 x twice the instructions)
+  constexpr int XI16 = WBITS == 4 ? CPL : (CPL >= 2 ? CPL / 2 : 1);
+  constexpr int XI = std::is_same_v<AT, float> ? 2 * XI16 : XI16;
+  if (p.K * (int64_t)sizeof(AT) > XI * 4096) return MLS_ERR_UNSUPPORTED;
   const int s_row_bytes = (int)(p.ld_sn * (int64_t)sizeof(ST));
   // the scale descriptor spans exactly the scales that exist: row N - 1 starts at
   // (N - 1) ld_sn and holds G groups (ld_sn may be below G, e.g. 0 for one row broadcast)
@@ -152,7 +155,8 @@ static int launch_gemv1_si(const WqArgs& p, int s_dw) {
       if (p.N < 4 * R2 * 256) return go(I1{}, std::integral_constant<int, 2>{});
     return go(I1{}, std::integral_constant<int, R2>{});
   }
-  if constexpr (XI <= 4) return go(std::integral_constant<int, 2>{}, std::integral_constant<int, R2>{});
+  if constexpr (XI <= 4 && !std::is_same_v<AT, float>)
+    return go(std::integral_constant<int, 2>{}, std::integral_constant<int, R2>{});
   return MLS_ERR_UNSUPPORTED;
 }
 
@@ -195,9 +199,16 @@ static int launch_gemv1_st(const WqArgs& p) {
 // (A/B sweeps).
 static int launch_gemv1(int wbits, const WqArgs& p) {
   static const int enabled = env_int("MLS_GEMV1", 1);
-  if (!enabled || p.M < 1 || p.M > 2 || p.a_dt == MLS_F32) return MLS_ERR_UNSUPPORTED;
+  // fp32 x with M = 1, INT4: x split into bf16 hi + lo parts (K = N = 4096 g128: 4.98 -> 4.27 us
+  // against the register kernel; INT8 measured slower that way, 5.64 -> 6.06, and keeps the
+  // register kernel). MLS_GEMV1_F32=0: the register kernel for INT4 too (A/B runs).
+  static const int f32_on = env_int("MLS_GEMV1_F32", 1);
+  if (!enabled || p.M < 1 || p.M > 2 || (p.a_dt == MLS_F32 && (p.M != 1 || !f32_on || wbits != 4)))
+    return MLS_ERR_UNSUPPORTED;
   // x in LDS (at most 32 KiB); 32-bit buffer offsets into the whole weight matrix
-  if (p.K * 2 > 32768 || (p.N + 4) * p.ldw >= (1ll << 31)) return MLS_ERR_UNSUPPORTED;
+  if (p.K * dt_size(p.a_dt) > 32768 || (p.N + 4) * p.ldw >= (1ll << 31)) return MLS_ERR_UNSUPPORTED;
+  if (p.a_dt == MLS_F32)
+    return p.s_dt == MLS_F16 ? launch_gemv1_st<4, float, _Float16>(p) : launch_gemv1_st<4, float, float>(p);
   if (wbits == 4) {
     if (p.a_dt == MLS_F16) return p.s_dt == MLS_F16 ? launch_gemv1_st<4, _Float16, _Float16>(p)
                                                     : launch_gemv1_st<4, _Float16, float>(p);

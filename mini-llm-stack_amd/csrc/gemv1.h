@@ -330,9 +330,14 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
                                                   int ldw, int w_bytes, const ST* __restrict__ s, int s_row_bytes,
                                                   int s_bytes, int group, AT* __restrict__ y, int N, int K,
                                                   int s_dw, int lda_b, int M, int ldy) {
-  using S = XSlot<WBITS, AT>;
+  // fp32 x (M = 1): staged in LDS as fp32, split in registers into bf16 hi (truncation) and
+  // lo (x - hi, rounded) parts, each dotted as a row of bf16 x; the output is fp32
+  constexpr bool XF32 = std::is_same_v<AT, float>;
+  static_assert(!XF32 || MX == 1, "fp32 x: one row");
+  using HT = std::conditional_t<XF32, __bf16, AT>;  // the dot products' 16-bit type
+  using S = XSlot<WBITS, HT>;
   constexpr int KC = S::KC, NV = S::NV;
-  constexpr float OFF = code_offset<WBITS, AT>();
+  constexpr float OFF = code_offset<WBITS, HT>();
   constexpr int S_SLICE = 64 * SI;  // scale dwords per wavefront slice
   constexpr int XB = XI * 4096;     // LDS bytes per row of x
   __shared__ __attribute__((aligned(16))) uint8_t smem[MX * XB + (WBITS == 4 ? 4 * S_SLICE * 4 : 16)];
@@ -432,7 +437,70 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
 #pragma unroll
       for (int j = 0; j < CPL; ++j) sc[r][j] = to_f32(st[sidx[r][j]]);
   }
-  if constexpr (MX == 1) {
+  if constexpr (XF32) {
+    // lane's chunk j: KC fp32 values of x, 16-byte pieces q (8 values) as bf16 hi and lo
+    XRaw<WBITS, HT> xh[CPL], xo[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const uint4* xl = reinterpret_cast<const uint4*>(smem + (lane + 64 * j) * KC * 4);
+#pragma unroll
+      for (int q = 0; q < XRaw<WBITS, HT>::XQ; ++q) {
+        const uint4 a = xl[2 * q], b = xl[2 * q + 1];
+        const uint32_t f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint32_t hp[4], lp[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          hp[t] = __builtin_amdgcn_perm(f[2 * t + 1], f[2 * t], 0x07060302u);  // truncated halves
+          const float l0 = __uint_as_float(f[2 * t]) - __uint_as_float(f[2 * t] & 0xFFFF0000u);
+          const float l1 = __uint_as_float(f[2 * t + 1]) - __uint_as_float(f[2 * t + 1] & 0xFFFF0000u);
+          lp[t] = Half16<HT>::pack2(l0, l1);
+        }
+        xh[j].v[q] = make_uint4(hp[0], hp[1], hp[2], hp[3]);
+        xo[j].v[q] = make_uint4(lp[0], lp[1], lp[2], lp[3]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t xrh[CPL][NV], xrl[CPL][NV];
+    float osx[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      osx[j] = OFF * (x_from_raw<WBITS, HT>(xh[j], xrh[j]) + x_from_raw<WBITS, HT>(xo[j], xrl[j]));
+    uint32_t nib_mask = 0x000F000Fu, magic = 0;
+    if constexpr (WBITS == 4) magic = Half16<HT>::MAGIC4;
+    asm volatile("" : "+v"(nib_mask), "+v"(magic));
+    float part[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        WPairs<WBITS, HT> wp;
+        chunk_widen<WBITS, HT>(wv[r][j], nib_mask, magic, wp);
+        const float d = (pairs_dot<WBITS, HT>(wp, xrh[j]) + pairs_dot<WBITS, HT>(wp, xrl[j])) - osx[j];
+        const float t = WBITS == 4 ? fmaf(sc[r][j], d, acc) : acc + d;
+        acc = (64 * (j + 1) > nchunks && lane + 64 * j >= nchunks) ? acc : t;
+      }
+      part[r] = acc;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) part[r] = wave_total_dpp(part[r]);
+    const int rows = min(R, N - n0);
+    if (lane == 63 && rows > 0) {
+      float v[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[r] = WBITS == 8 ? part[r] * srow[r] : part[r];
+      float* dst = reinterpret_cast<float*>(y) + n0;
+      if constexpr (R == 4) {
+        if (rows == 4 && ((uintptr_t)dst & 15) == 0) {
+          *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+          return;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (r < rows) dst[r] = v[r];
+    }
+  } else if constexpr (MX == 1) {
     // one row of x (the M = 1 GEMV)
     XRaw<WBITS, AT> xraw[CPL];
 #pragma unroll

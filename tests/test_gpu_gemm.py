@@ -177,6 +177,31 @@ def test_gemv_other_dtypes(dev, dtype, M):
            ref.int8_matmul(a2.float().numpy(), q.cpu().numpy(), s8.cpu().numpy()), f"int8 {dtype} M={M}")
 
 
+@pytest.mark.parametrize("N,K,gs,sdt", [
+    (4096, 4096, 128, torch.float16),  # the engine's decode shape: 4 rows per wavefront, 2 chunks per lane
+    (1000, 3072, 32, torch.float16),   # ragged N, chunks past K
+    (8200, 2048, 64, torch.float32),   # one chunk per lane, 8 rows per wavefront, fp32 scales, ragged block
+    (300, 8192, 128, torch.float16),   # 4 chunks per lane: 32 KiB of fp32 x in LDS
+    (77, 1088, 64, torch.float32),     # 34 chunks: most lanes past K
+])
+def test_gemv_m1_fp32_split(dev, N, K, gs, sdt):
+    """INT4 M = 1 with fp32 x (the reference engine's decode dtype): x staged in LDS as fp32 and
+    split into bf16 hi + lo parts, each dotted with the same widened weights; fp32 output within
+    the fp32 rule of the oracle, with weights and scales as views with padded rows."""
+    a, w = _data(1, N, K, 1300 + N, 0.02)
+    p, s = quantize_int4(w.to(dev), gs)
+    s = s.to(sdt)
+    pw = torch.zeros(N, K // 2 + 32, dtype=torch.uint8, device=dev)
+    pw[:, :K // 2] = p
+    sw = torch.zeros(N, K // gs + 2, dtype=sdt, device=dev)
+    sw[:, :K // gs] = s
+    x = (a * torch.logspace(-3, 3, K)).float()  # magnitudes over six decades: the lo part matters
+    out = int4_matmul(x.to(dev), pw[:, :K // 2], sw[:, :K // gs], gs)
+    assert out.dtype == torch.float32
+    _check(out, ref.int4_matmul(x.numpy(), p.cpu().numpy(), s.float().cpu().numpy(), gs),
+           f"int4 fp32 M=1 N={N} K={K} g{gs}")
+
+
 @pytest.mark.parametrize("N,K,gs,dtype,sdt", [
     (1000, 3072, 32, torch.bfloat16, torch.float16),   # ragged N, chunks past K, 4 scale instructions
     (777, 4096, 128, torch.float16, torch.float32),    # fp32 scales: 2 scale instructions per wavefront
