@@ -119,6 +119,24 @@ __device__ __forceinline__ uint4 byte_operand(uint32_t d0, uint32_t d1) {
                     Mx<AT>::pack_int((float)((v >> 16) & 0xFFu), (float)(v >> 24)));
 }
 
+// fp32 x piece (values 0..3 in a, 4..7 in b) -> its bf16 hi piece in a (the truncated upper
+// halves) and lo piece in b (x - hi, rounded to nearest): x to about 2^-16 of its magnitude,
+// the split pass's arithmetic for finite x
+__device__ __forceinline__ void split_piece(uint4& a, uint4& b) {
+  const uint32_t f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    h[t] = __builtin_amdgcn_perm(f[2 * t + 1], f[2 * t], 0x07060302u);
+    bf16x2 v;
+    v.x = (__bf16)(__uint_as_float(f[2 * t]) - __uint_as_float(f[2 * t] & 0xFFFF0000u));
+    v.y = (__bf16)(__uint_as_float(f[2 * t + 1]) - __uint_as_float(f[2 * t + 1] & 0xFFFF0000u));
+    l[t] = __builtin_bit_cast(uint32_t, v);
+  }
+  a = make_uint4(h[0], h[1], h[2], h[3]);
+  b = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
 // INT4 group scales of a wavefront's steps through LDS (SL): the wavefront's slice of the
 // block's scale table, SLG groups from its first step's group g0 by 16 R rows, stored
 // [group][row], one dword per scale (fp16 in the low half), so that a lane's 4
@@ -143,7 +161,12 @@ constexpr int SLG = 16;
 // M <= 16 rows of x, the hi parts in rows 0..15 and the lo parts in rows 16..31; every MFMA
 // on an x operand runs once on each part into the same accumulator, and the output is fp32.
 // x comes straight from global (the LDS slice of both parts would not fit).
-template <int WBITS, typename AT, typename ST, int R, int WAVES, int U, bool SL, bool XL, bool S64, bool SPL = false>
+// XF (with SPL): a holds the M rows of x in fp32 (row stride lda floats) instead of split
+// rows; each 8-value piece is loaded as two 16-byte halves and split in registers into its
+// bf16 hi (truncated upper halves) and lo (x - hi, rounded to bf16) pieces, the split pass's
+// arithmetic on finite x, so no separate split launch or workspace is needed.
+template <int WBITS, typename AT, typename ST, int R, int WAVES, int U, bool SL, bool XL, bool S64, bool SPL = false,
+          bool XF = false>
 // One wavefront per SIMD is the design point (a grid of N / 16 blocks of WAVES
 // wavefronts), so the compiler may spend registers on keeping a chunk's loads in flight.
 // The files that instantiate this kernel are built with kernel-argument preloading (the
@@ -157,6 +180,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
   const int64_t lda = lda32, ldw = ldw32, ld_sn = ld_sn32, ld_sg = ld_sg32;
   using OT = std::conditional_t<SPL, float, AT>;
   static_assert(!(SPL && XL), "split x comes from global");
+  static_assert(!XF || (SPL && std::is_same_v<AT, __bf16>), "fp32 x: split into bf16 parts");
+  constexpr int XES = XF ? 4 : (int)sizeof(AT);  // bytes per x element in memory
   constexpr int XPARTS = SPL ? 2 : 1;
   constexpr bool W16 = WBITS == 8 || !S64;    // 16 weight bytes per lane and step (else 8)
   constexpr int KB = WBITS == 4 && W16 ? 128 : 64;  // k per step
@@ -207,13 +232,13 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
   // rows of x past M and weight rows past N read as zeros (split x: the lo parts' M rows
   // start 16 rows down, through a descriptor of their own)
   const __amdgpu_buffer_rsrc_t rsx = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)a, (short)0, (int)(M * lda * (int64_t)sizeof(AT)), 0x00020000);
+      (void*)a, (short)0, (int)(M * lda * (int64_t)XES), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsx_lo = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a + (SPL ? 16 * lda : 0)), (short)0, (int)(M * lda * (int64_t)sizeof(AT)), 0x00020000);
   const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(w + (int64_t)n_base * ldw), (short)0, (int)(rows_w * ldw), 0x00020000);
   // this lane's byte offsets inside a step (x row m = r)
-  const int x_off = r * (int)lda * (int)sizeof(AT) + NMF * 16 * q;
+  const int x_off = r * (int)lda * XES + NMF * 16 * q * (XES / (int)sizeof(AT));
   int w_off[R];
 #pragma unroll
   for (int t = 0; t < R; ++t) w_off[t] = (16 * t + r) * (int)ldw + (W16 ? 16 : 8) * q;
@@ -258,7 +283,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
     for (int u = 0; u < U; ++u) {
       const bool live = s0 + u < s_hi;  // wave-uniform
       const int st = live ? s0 + u : s_hi - 1;
-      const int xs_off = live ? st * KB * (int)sizeof(AT) : 0x7FFFFFF0;
+      const int xs_off = live ? st * KB * XES : 0x7FFFFFF0;
 #pragma unroll
       for (int t = 0; t < R; ++t)
         if constexpr (W16) {
@@ -267,7 +292,15 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
           const uint2 v2 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rsw, w_off[t], st * 32, kNonTemporal));
           wv[u][t] = make_uint4(v2.x, v2.y, 0u, 0u);
         }
-      if constexpr (!XL) {
+      if constexpr (XF) {
+        // piece j: fp32 values 0..3 into xv, 4..7 into xvl (split before use)
+#pragma unroll
+        for (int j = 0; j < NMF; ++j) {
+          xv[u][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsx, x_off + 32 * j, xs_off, 0));
+          xvl[u][j] =
+              __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsx, x_off + 32 * j + 16, xs_off, 0));
+        }
+      } else if constexpr (!XL) {
 #pragma unroll
         for (int j = 0; j < NMF; ++j)
           xv[u][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -332,6 +365,10 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
         // 5.96; INT8 2048^2 M = 16 4.21 -> 4.05)
         if (u + 1 < U) read_x(u + 1);
         __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (XF) {
+#pragma unroll
+        for (int j = 0; j < NMF; ++j) split_piece(xv[u][j], xvl[u][j]);
       }
       if constexpr (WBITS == 4) {
         uint4 xo[XPARTS][NMF];
@@ -418,7 +455,7 @@ int env_pair(int& r, int& waves) {
   return sscanf(v, "%d,%d", &r, &waves) == 2;
 }
 
-template <int WBITS, typename AT, typename ST, int R, int WAVES, bool S64, bool SPL = false>
+template <int WBITS, typename AT, typename ST, int R, int WAVES, bool S64, bool SPL = false, bool XF = false>
 int launch_one(const WqArgs& p) {
   constexpr int U = SPL ? 4 : 8;  // split x: both parts' registers for half the steps
   constexpr int KB = WBITS == 4 && !S64 ? 128 : 64;
@@ -440,7 +477,7 @@ int launch_one(const WqArgs& p) {
   using OT = std::conditional_t<SPL, float, AT>;
   auto go = [&](auto slc, auto xlc) {
     hipLaunchKernelGGL((gemv_mfma_kernel<WBITS, AT, ST, R, WAVES, U, decltype(slc)::value, decltype(xlc)::value, S64,
-                                         SPL>),
+                                         SPL, XF>),
                        dim3((unsigned)blocks), dim3(64 * WAVES), 0, p.stream, static_cast<const AT*>(p.a), p.w,
                        static_cast<const ST*>(p.s), (int)p.K, (int)p.N, (int)p.M, (int)p.lda, (int)p.ldw,
                        (int)p.ld_sn, (int)p.ld_sg, p.group, static_cast<OT*>(p.c), p.ldc);
@@ -459,7 +496,7 @@ int launch_one(const WqArgs& p) {
   return MLS_OK;
 }
 
-template <int WBITS, typename AT, typename ST, bool S64, bool SPL = false>
+template <int WBITS, typename AT, typename ST, bool S64, bool SPL = false, bool XF = false>
 int launch_shape(const WqArgs& p) {
   constexpr int KB = WBITS == 4 && !S64 ? 128 : 64;
   const int64_t nsteps = p.K / KB;
@@ -476,15 +513,15 @@ int launch_shape(const WqArgs& p) {
       return launch_one<WBITS, AT, ST, 2, 4, S64>(p);
     }
   }
-  if (waves == 16) return launch_one<WBITS, AT, ST, 1, 16, S64, SPL>(p);
-  if (waves == 8) return launch_one<WBITS, AT, ST, 1, 8, S64, SPL>(p);
-  return launch_one<WBITS, AT, ST, 1, 4, S64, SPL>(p);
+  if (waves == 16) return launch_one<WBITS, AT, ST, 1, 16, S64, SPL, XF>(p);
+  if (waves == 8) return launch_one<WBITS, AT, ST, 1, 8, S64, SPL, XF>(p);
+  return launch_one<WBITS, AT, ST, 1, 4, S64, SPL, XF>(p);
 }
 
-template <int WBITS, typename AT, bool S64 = false, bool SPL = false>
+template <int WBITS, typename AT, bool S64 = false, bool SPL = false, bool XF = false>
 int launch_st(const WqArgs& p) {
-  return p.s_dt == MLS_F16 ? launch_shape<WBITS, AT, _Float16, S64, SPL>(p)
-                           : launch_shape<WBITS, AT, float, S64, SPL>(p);
+  return p.s_dt == MLS_F16 ? launch_shape<WBITS, AT, _Float16, S64, SPL, XF>(p)
+                           : launch_shape<WBITS, AT, float, S64, SPL, XF>(p);
 }
 
 }  // namespace
@@ -492,5 +529,6 @@ int launch_st(const WqArgs& p) {
 // The INT8 kernels (gemv_mfma8.hip): p as checked by launch_gemv_mfma / launch_gemv_mfma_split.
 int launch_gemv_mfma_int8(const WqArgs& p);
 int launch_gemv_mfma_split_int8(const WqArgs& q);
+int launch_gemv_mfma_f32_int8(const WqArgs& p);
 
 }  // namespace mls

@@ -10,4 +10,6 @@ int launch_gemv_mfma_int8(const WqArgs& p) {
 
 int launch_gemv_mfma_split_int8(const WqArgs& q) { return launch_st<8, __bf16, false, true>(q); }
 
+int launch_gemv_mfma_f32_int8(const WqArgs& p) { return launch_st<8, __bf16, false, true, true>(p); }
+
 }  // namespace mls

@@ -33,6 +33,9 @@ int launch_gemv_rows(int wbits, const WqArgs& p);
 // MFMA skinny GEMM for M <= 16 and 16-bit activations (weights read once for all M).
 // MLS_ERR_UNSUPPORTED outside its fast path.
 int launch_gemv_mfma(int wbits, const WqArgs& p);
+// The same for fp32 x, 2 <= M <= 16: x read in fp32 and split into bf16 hi + lo parts in
+// registers; fp32 output. MLS_ERR_UNSUPPORTED outside its fast path.
+int launch_gemv_mfma_f32(int wbits, const WqArgs& p);
 
 // Small / medium GEMM for 16-bit activations (MFMA operands straight into registers, K
 // split over a block's wavefronts). MLS_ERR_UNSUPPORTED outside its fast path.

@@ -63,6 +63,7 @@ int run(const char* fn, int wbits, const WqArgs& p) {
       static const bool rows_env = env_int("MLS_GEMV_M2", 1) != 0;
       if (rows_env && p.M == 2) rc = launch_gemv_rows(wbits, p);
       if (rc == MLS_ERR_UNSUPPORTED && p.M >= 2 && p.a_dt != MLS_F32) rc = launch_gemv_mfma(wbits, p);
+      if (rc == MLS_ERR_UNSUPPORTED && p.M >= 2 && p.a_dt == MLS_F32) rc = launch_gemv_mfma_f32(wbits, p);
       if (rc == MLS_ERR_UNSUPPORTED) rc = launch_gemv_wq(wbits, p);
     } else {
       rc = launch_gemm_wq_mfma(wbits, p);
@@ -112,6 +113,11 @@ int run_split(const char* fn, int wbits, const WqArgs& p, void* ws) {
 }
 
 int run_ws(const char* fn, int wbits, const WqArgs& p, void* ws, int64_t ws_bytes) {
+  if (p.M >= 2 && p.M <= 16 && p.N > 0 && p.a_dt == MLS_F32) {
+    // fp32 x, 2 <= M <= 16: the skinny kernel splits x itself (no split pass, no workspace)
+    const int rc = launch_gemv_mfma_f32(wbits, p);
+    if (rc != MLS_ERR_UNSUPPORTED) return rc == MLS_OK ? check_launch(fn) : rc;
+  }
   if (p.M == 0 || p.N == 0 || !split_ok(wbits, p)) return run(fn, wbits, p);
   const int64_t need = split_ws_bytes(p);
   if (!ws || ws_bytes < need || !aligned(ws, 256))

@@ -23,6 +23,7 @@ namespace {
 int launch_gemv_wq(int, const WqArgs&) { reached("launch_gemv_wq"); }
 int launch_gemv_rows(int, const WqArgs&) { reached("launch_gemv_rows"); }
 int launch_gemv_mfma(int, const WqArgs&) { reached("launch_gemv_mfma"); }
+int launch_gemv_mfma_f32(int, const WqArgs&) { reached("launch_gemv_mfma_f32"); }
 int launch_gemm_small(int, const WqArgs&) { reached("launch_gemm_small"); }
 int launch_gemm_wq_mfma(int, const WqArgs&) { reached("launch_gemm_wq_mfma"); }
 int launch_gemm_wq_generic(int, const WqArgs&) { reached("launch_gemm_wq_generic"); }

@@ -157,8 +157,9 @@ def test_fp32_split_nonfinite(dev):
 
 
 def test_fp32_small_m_unchanged(dev):
-    """M = 1 keeps the VALU GEMV (HBM-bound; fp32 FMAs): no workspace is asked for; from
-    M = 2 on the split rows are 32 per 16 rows of x."""
+    """M = 1 asks for no workspace (INT8: the VALU GEMV with fp32 FMAs; INT4: the LDS GEMV
+    splitting x in registers); from M = 2 on the split rows are 32 per 16 rows of x (used by
+    the split pass where the skinny kernel cannot split x itself)."""
     import kernels
     L = kernels.lib()
     assert L.mls_wq_gemm_workspace(8, 1, 4096, 4096, kernels.MLS_F32, 0) == 0
@@ -197,6 +198,46 @@ def test_fp32_split_skinny(dev, bits, M, N, K, gs):
         out = int4_matmul(a.to(dev), q.to(dev), s.to(dev), gs)
         want = ref.int4_matmul(a.numpy(), q.numpy(), s.numpy(), gs)
     _check32(out, want, f"fp32 skinny int{bits} M={M} N={N} K={K}")
+
+
+@pytest.mark.parametrize("bits", [8, 4])
+def test_fp32_skinny_without_workspace(dev, bits):
+    """2 <= M <= 16 with fp32 x splits x inside the skinny kernel, so the entry points without a
+    workspace (mls_int8_gemm / mls_int4_gemm) take the matrix cores too, with the same outputs
+    as the workspace entry points; x whose rows the kernel cannot load as 16-byte pieces (an odd
+    row stride) takes the split pass, under the same rule."""
+    import kernels
+    from kernels._hip import stream
+    M, N, K, gs = 5, 1000, 2048, 128
+    g = torch.Generator().manual_seed(55 + bits)
+    a = torch.randn(M, K, generator=g)
+    w = torch.randn(N, K, generator=g) * 0.02
+    L = kernels.lib()
+    ad = a.to(dev)
+    c = torch.empty(M, N, dtype=torch.float32, device=dev)
+    if bits == 8:
+        q, s = quantize_int8(w.to(dev))
+        s = s.to(torch.float16)
+        rc = L.mls_int8_gemm(ad.data_ptr(), kernels.MLS_F32, K, q.data_ptr(), K, s.data_ptr(), kernels.MLS_F16,
+                             c.data_ptr(), kernels.MLS_F32, N, M, N, K, stream(dev))
+        via_ws = int8_matmul(ad, q, s)
+        want = ref.int8_matmul(a.numpy(), q.cpu().numpy(), s.float().cpu().numpy())
+    else:
+        q, s = quantize_int4(w.to(dev), gs)
+        rc = L.mls_int4_gemm(ad.data_ptr(), kernels.MLS_F32, K, q.data_ptr(), K // 2, s.data_ptr(), kernels.MLS_F32,
+                             s.stride(0), 1, gs, c.data_ptr(), kernels.MLS_F32, N, M, N, K, stream(dev))
+        via_ws = int4_matmul(ad, q, s, gs)
+        want = ref.int4_matmul(a.numpy(), q.cpu().numpy(), s.cpu().numpy(), gs)
+    torch.cuda.synchronize(dev)
+    assert rc == 0
+    assert torch.equal(c, via_ws)
+    _check32(c, want, f"fp32 M={M} int{bits}, no workspace")
+    # row stride K + 1 floats: not a whole number of 16-byte pieces per row
+    big = torch.zeros(M, K + 1, dtype=torch.float32, device=dev)
+    big[:, :K] = ad
+    xs = big[:, :K]
+    out = int8_matmul(xs, q, s) if bits == 8 else int4_matmul(xs, q, s, gs)
+    _check32(out, want, f"fp32 M={M} int{bits}, odd row stride")
 
 
 def test_int8_dgrad_fp32_training_shape(dev):
