@@ -389,7 +389,11 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
   __builtin_amdgcn_sched_barrier(0);
 
   // 2. every weight chunk of this lane: rows past N read zeros (past the descriptor's range);
-  //    chunks past K read whatever follows in memory and their terms are dropped below
+  //    chunks past K read whatever follows in memory and their terms are dropped below. Cache
+  //    policy: non-temporal, but the default for INT8 with one row of x (K = N = 4096, one box:
+  //    INT4 3.36 us with the hint against 3.41 without; INT8 M = 1 4.66 against 4.58, M = 2
+  //    5.28 against 5.32)
+  constexpr int WCPOL = WBITS == 8 && MX == 1 ? 0 : 2;
   const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, w_bytes, 0x00020000);
   uint4 wv[R][CPL];
 #pragma unroll
@@ -397,7 +401,7 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
       wv[r][j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, lane * 16 + 1024 * j,
-                                                                                 (n0 + r) * ldw, 2));
+                                                                                 (n0 + r) * ldw, WCPOL));
   __builtin_amdgcn_sched_barrier(0);  // nothing below (e.g. the group division's setup) ahead of the loads
 
   // the slice index of each (row, chunk)'s group scale (a division by the runtime group

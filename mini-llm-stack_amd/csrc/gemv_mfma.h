@@ -69,7 +69,9 @@ template <> struct Mx<_Float16> {
   }
 };
 
-// buffer-load cache policy: non-temporal (the weights are read once)
+// buffer-load cache policy for the INT4 weights: non-temporal (read once; measured faster
+// than the default: M = 4 4.60 against 5.05 us); the INT8 weights take the default (M = 16
+// fp16 3.73 against 3.79 us)
 constexpr int kNonTemporal = 2;
 
 template <typename ST> __device__ __forceinline__ float ld_scale(const ST* s, int64_t i) {
@@ -287,7 +289,8 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
       for (int t = 0; t < R; ++t)
         if constexpr (W16) {
-          wv[u][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, w_off[t], st * 64, kNonTemporal));
+          wv[u][t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rsw, w_off[t], st * 64,
+                                                                                     WBITS == 8 ? 0 : kNonTemporal));
         } else {
           const uint2 v2 = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rsw, w_off[t], st * 32, kNonTemporal));
           wv[u][t] = make_uint4(v2.x, v2.y, 0u, 0u);
