@@ -157,7 +157,9 @@ __global__ __launch_bounds__(64 * WV) void gemm_small_kernel(const void* pa, con
         const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rsw, wo[tn], sw, 2));
         sl.w[tn] = make_uint4(v.x, v.y, 0u, 0u);
       } else {
-        sl.w[tn] = ld16_nt(rsw, wo[tn], sw);
+        // INT8 weights with the default cache policy (the reference's M = 128 shape: 6.19 ->
+        // 5.94 us), INT4 non-temporal
+        sl.w[tn] = I4 ? ld16_nt(rsw, wo[tn], sw) : ld16(rsw, wo[tn], sw);
       }
     }
   };
