@@ -291,8 +291,8 @@ __device__ __forceinline__ float scale_value(const ST* s, int64_t i) {
 //    address arithmetic before the loads issue);
 //  - one wait for the LDS-direct loads (they were issued first and complete first) and one
 //    barrier, which falls inside the weights' HBM latency;
-//  - the cross-lane sums are DPP moves only (row sums, then row_bcast:15 / row_bcast:31), and
-//    lane 63, which ends up holding every row's total, writes the R outputs at once.
+//  - the cross-lane sums of the R rows are reduced together (lane-half and 16-lane-row swaps,
+//    then DPP moves within rows: wave_totals), and one lane per row writes that row's output.
 // LDS: x in XI * 4 KiB (the LDS-direct loads past 2K bytes read zeros past the buffer), then
 // 4 scale slices of R * s_dw dwords, each rounded up to SI whole 64-dword LDS-direct
 // instructions.
@@ -309,6 +309,80 @@ __device__ __forceinline__ float wave_total_dpp(float v) {
   v = dpp_add_rows<0x142, 0xA>(v);  // row_bcast:15: rows 1, 3 += last lane of rows 0, 2
   v = dpp_add_rows<0x143, 0xC>(v);  // row_bcast:31: rows 2, 3 += lane 31 (rows 0 + 1)
   return v;
+}
+
+// v_permlane32_swap / v_permlane16_swap: the upper 32 lanes of a trade places with the lower
+// 32 of b (16: the odd 16-lane rows of a with the even rows of b). The elements of the
+// returned pair are copied into scalars one by one: a __builtin_bit_cast of the pair's second
+// element compiled into a read of the first.
+__device__ __forceinline__ void swap_halves32(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  a = __uint_as_float(r0);
+  b = __uint_as_float(r1);
+}
+__device__ __forceinline__ void swap_rows16(float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  a = __uint_as_float(r0);
+  b = __uint_as_float(r1);
+}
+
+// Wave totals of V per-lane partials (V = 1, 2 or a multiple of 4), reduced together: a swap
+// of lane halves and an add leave each value's two halves summed in one half of a register
+// (two values per register), a swap of 16-lane rows and an add the same per row (four values
+// per register), and 4 DPP steps finish each row: 3 + 3 + 4 instructions for 4 values where
+// a DPP reduction per value takes 4 x 10. Slot k of lane l holds value total_index<V>(l, k),
+// -1 where the lane is not the one that writes it.
+template <int V>
+struct WaveTotals {
+  static_assert(V == 1 || V == 2 || V % 4 == 0, "1, 2 or a multiple of 4 values");
+  static constexpr int NT = V >= 4 ? V / 4 : 1;
+  float t[NT];
+};
+
+template <int V>
+__device__ __forceinline__ WaveTotals<V> wave_totals(float (&p)[V]) {
+  WaveTotals<V> out;
+  if constexpr (V == 1) {
+    out.t[0] = wave_total_dpp(p[0]);
+  } else if constexpr (V == 2) {
+    swap_halves32(p[0], p[1]);
+    const float a = lane_group_sum<16>(p[0] + p[1]);  // lanes 0-31: value 0, 32-63: value 1
+    out.t[0] = dpp_add_rows<0x142, 0xA>(a);           // row_bcast:15: rows 1, 3 += rows 0, 2
+  } else {
+    float a[V / 2];
+#pragma unroll
+    for (int i = 0; i < V / 2; ++i) {
+      swap_halves32(p[2 * i], p[2 * i + 1]);
+      a[i] = p[2 * i] + p[2 * i + 1];  // lanes 0-31: value 2i, 32-63: value 2i + 1
+    }
+#pragma unroll
+    for (int j = 0; j < V / 4; ++j) {
+      swap_rows16(a[2 * j], a[2 * j + 1]);
+      out.t[j] = lane_group_sum<16>(a[2 * j] + a[2 * j + 1]);  // rows: values 4j + {0, 2, 1, 3}
+    }
+  }
+  return out;
+}
+
+template <int V>
+__device__ __forceinline__ int total_index(int lane, int k) {
+  if constexpr (V == 1) return lane == 63 ? 0 : -1;
+  else if constexpr (V == 2) return (lane & 31) == 31 ? lane >> 5 : -1;
+  else {
+    const int g = lane >> 4;
+    return (lane & 15) == 15 ? 4 * k + (((g & 1) << 1) | (g >> 1)) : -1;
+  }
+}
+
+// v[i] for a lane-dependent i < R (selects, no indexed register access)
+template <int R>
+__device__ __forceinline__ float pick(const float (&v)[R], int i) {
+  float s = v[0];
+#pragma unroll
+  for (int r = 1; r < R; ++r) s = i == r ? v[r] : s;
+  return s;
 }
 
 __device__ __forceinline__ void lds_direct16(__amdgpu_buffer_rsrc_t rs, void* lds, int voff, int soff) {
@@ -486,23 +560,13 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
       }
       part[r] = acc;
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r) part[r] = wave_total_dpp(part[r]);
+    const WaveTotals<R> tot = wave_totals<R>(part);
     const int rows = min(R, N - n0);
-    if (lane == 63 && rows > 0) {
-      float v[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) v[r] = WBITS == 8 ? part[r] * srow[r] : part[r];
-      float* dst = reinterpret_cast<float*>(y) + n0;
-      if constexpr (R == 4) {
-        if (rows == 4 && ((uintptr_t)dst & 15) == 0) {
-          *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-          return;
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (r < rows) dst[r] = v[r];
+    for (int k = 0; k < WaveTotals<R>::NT; ++k) {
+      const int r = total_index<R>(lane, k);
+      if (r >= 0 && r < rows)
+        reinterpret_cast<float*>(y)[n0 + r] = WBITS == 8 ? tot.t[k] * pick<R>(srow, r) : tot.t[k];
     }
   } else if constexpr (MX == 1) {
     // one row of x (the M = 1 GEMV)
@@ -537,30 +601,13 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
       part[r] = acc;
     }
 
-    // 5. wave totals by DPP; lane 63 holds every row's and writes them
-#pragma unroll
-    for (int r = 0; r < R; ++r) part[r] = wave_total_dpp(part[r]);
+    // 5. wave totals of the R rows together; one lane per row writes it
+    const WaveTotals<R> tot = wave_totals<R>(part);
     const int rows = min(R, N - n0);
-    if (lane == 63 && rows > 0) {
-      float v[R];
 #pragma unroll
-      for (int r = 0; r < R; ++r) v[r] = WBITS == 8 ? part[r] * srow[r] : part[r];
-      AT* dst = y + n0;
-      if constexpr (R == 4) {
-        if (rows == 4 && ((uintptr_t)dst & 7) == 0) {
-          *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_bits(from_f32<AT>(v[0]), from_f32<AT>(v[1])),
-                                                      pack2_bits(from_f32<AT>(v[2]), from_f32<AT>(v[3])));
-          return;
-        }
-      } else if constexpr (R == 2) {
-        if (rows == 2 && ((uintptr_t)dst & 3) == 0) {
-          *reinterpret_cast<uint32_t*>(dst) = pack2_bits(from_f32<AT>(v[0]), from_f32<AT>(v[1]));
-          return;
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (r < rows) dst[r] = from_f32<AT>(v[r]);
+    for (int k = 0; k < WaveTotals<R>::NT; ++k) {
+      const int r = total_index<R>(lane, k);
+      if (r >= 0 && r < rows) y[n0 + r] = from_f32<AT>(WBITS == 8 ? tot.t[k] * pick<R>(srow, r) : tot.t[k]);
     }
   } else {
     // MX rows of x: each weight chunk is widened once and dotted with every row
@@ -608,35 +655,20 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
       for (int mi = 0; mi < MX; ++mi) part[mi][r] = acc[mi];
     }
 
-    // 5. wave totals by DPP; lane 63 holds every row's and writes them
+    // 5. wave totals of the MX x R outputs together; one lane per output writes it
+    float flat[MX * R];
 #pragma unroll
     for (int mi = 0; mi < MX; ++mi)
 #pragma unroll
-      for (int r = 0; r < R; ++r) part[mi][r] = wave_total_dpp(part[mi][r]);
+      for (int r = 0; r < R; ++r) flat[mi * R + r] = part[mi][r];
+    const WaveTotals<MX * R> tot = wave_totals<MX * R>(flat);
     const int rows = min(R, N - n0);
-    if (lane != 63 || rows <= 0) return;
 #pragma unroll
-    for (int mi = 0; mi < MX; ++mi) {
-      if (mi >= M) break;  // (a row of x past M: never stored)
-      float v[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) v[r] = WBITS == 8 ? part[mi][r] * srow[r] : part[mi][r];
-      AT* dst = y + (int64_t)mi * ldy + n0;
-      if constexpr (R == 4) {
-        if (rows == 4 && ((uintptr_t)dst & 7) == 0) {
-          *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_bits(from_f32<AT>(v[0]), from_f32<AT>(v[1])),
-                                                      pack2_bits(from_f32<AT>(v[2]), from_f32<AT>(v[3])));
-          continue;
-        }
-      } else if constexpr (R == 2) {
-        if (rows == 2 && ((uintptr_t)dst & 3) == 0) {
-          *reinterpret_cast<uint32_t*>(dst) = pack2_bits(from_f32<AT>(v[0]), from_f32<AT>(v[1]));
-          continue;
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (r < rows) dst[r] = from_f32<AT>(v[r]);
+    for (int k = 0; k < WaveTotals<MX * R>::NT; ++k) {
+      const int i = total_index<MX * R>(lane, k);
+      const int mi = i / R, r = i % R;  // (a row of x past M: computed, never stored)
+      if (i >= 0 && r < rows && mi < M)
+        y[(int64_t)mi * ldy + n0 + r] = from_f32<AT>(WBITS == 8 ? tot.t[k] * pick<R>(srow, r) : tot.t[k]);
     }
   }
 }
