@@ -20,7 +20,6 @@ __global__ __launch_bounds__(256) void gemv_wq_kernel(
   const int64_t ldx = ldx32, ldw = ldw32, ld_sn = ld_sn32, ld_sg = ld_sg32;
   using S = XSlot<WBITS, AT>;
   constexpr int KC = S::KC, NV = S::NV;
-  constexpr float OFF = code_offset<WBITS, AT>();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nchunks = K / KC;
   const int m0 = blockIdx.y * MT;
@@ -61,7 +60,7 @@ __global__ __launch_bounds__(256) void gemv_wq_kernel(
 #pragma unroll
   for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) osx[mi][j] = OFF * x_from_raw<WBITS, AT>(xraw[mi][j], xr[mi][j]);
+    for (int j = 0; j < CPL; ++j) osx[mi][j] = offset_term<WBITS, AT>(x_from_raw<WBITS, AT>(xraw[mi][j], xr[mi][j]));
 
   // 3. dot products. The INT4 16-bit path's widening constants live in VGPRs (an empty
   // asm hides their values, so they are not re-materialised as literals; see and_or).

@@ -36,6 +36,11 @@ __device__ __forceinline__ float ub0(uint32_t v) { return (float)(v & 0xFFu); }
 __device__ __forceinline__ float ub1(uint32_t v) { return (float)((v >> 8) & 0xFFu); }
 __device__ __forceinline__ float ub2(uint32_t v) { return (float)((v >> 16) & 0xFFu); }
 __device__ __forceinline__ float ub3(uint32_t v) { return (float)(v >> 24); }
+// signed bytes of v (one v_cvt_f32_i32 with an SDWA sign-extended byte select each)
+__device__ __forceinline__ float sb0(uint32_t v) { return (float)(signed char)v; }
+__device__ __forceinline__ float sb1(uint32_t v) { return (float)(signed char)(v >> 8); }
+__device__ __forceinline__ float sb2(uint32_t v) { return (float)(signed char)(v >> 16); }
+__device__ __forceinline__ float sb3(uint32_t v) { return (float)((int32_t)v >> 24); }
 
 template <typename AT> struct Half16;
 
@@ -54,12 +59,11 @@ template <> struct Half16<__bf16> {
     v.y = (__bf16)hi;
     return __builtin_bit_cast(uint32_t, v);
   }
-  // INT8: bytes H2, H2 + 1 of u (biased codes q + 128) as the pair (u, u'); code_offset
-  // is 128
+  // INT8: the signed bytes H2, H2 + 1 of q as the exact pair (q, q'); code_offset is 0
   template <int H2>
-  __device__ static __forceinline__ uint32_t byte_pair(uint32_t u) {
-    if constexpr (H2 == 0) return pack2(ub0(u), ub1(u));
-    else return pack2(ub2(u), ub3(u));
+  __device__ static __forceinline__ uint32_t byte_pair(uint32_t q) {
+    if constexpr (H2 == 0) return pack2(sb0(q), sb1(q));
+    else return pack2(sb2(q), sb3(q));
   }
 };
 
@@ -74,12 +78,12 @@ template <> struct Half16<_Float16> {
   __device__ static __forceinline__ uint32_t pack2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
   }
-  // INT8: bytes H2, H2 + 1 of u (biased codes q + 128) as the exact pair (1024 + u,
-  // 1024 + u'): each byte becomes the low byte of an fp16 with high byte 0x64, one v_perm
-  // per pair (code_offset is 1152 = 1024 + 128)
+  // INT8: bytes H2, H2 + 1 of q as the exact pair (1024 + u, 1024 + u') of the biased codes
+  // u = q + 128: each u becomes the low byte of an fp16 with high byte 0x64, one v_perm per
+  // pair (code_offset is 1152 = 1024 + 128)
   template <int H2>
-  __device__ static __forceinline__ uint32_t byte_pair(uint32_t u) {
-    return __builtin_amdgcn_perm(0x64646464u, u, H2 == 0 ? 0x04010400u : 0x04030402u);
+  __device__ static __forceinline__ uint32_t byte_pair(uint32_t q) {
+    return __builtin_amdgcn_perm(0x64646464u, q ^ 0x80808080u, H2 == 0 ? 0x04010400u : 0x04030402u);
   }
 };
 
@@ -170,8 +174,9 @@ __device__ __forceinline__ float load_x_chunk(const AT* __restrict__ xrow, int c
 // VALU write to insert the wait states an MFMA reading the result needs.)
 __device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) { return (a & m) | c; }
 
-// sum_k x_k * u_k over one 16-byte weight chunk, where u_k is the biased code
-// (INT4: nibble + bias of the 16-bit path, or the raw nibble for fp32; INT8: q + 128).
+// sum_k x_k * u_k over one 16-byte weight chunk, where u_k is the code as widened
+// (INT4: nibble + bias of the 16-bit path, or the raw nibble for fp32; INT8: q, or 1024 + q +
+// 128 for fp16 x); code_offset<WBITS, AT>() times sum_k x_k is what u_k adds to the signed code.
 // nib_mask / magic: 0x000F000F and the 16-bit path's bias pattern, held in registers.
 template <int WBITS, typename AT>
 __device__ __forceinline__ float chunk_dot(const uint4 wq, const uint32_t* xr, uint32_t nib_mask, uint32_t magic) {
@@ -210,17 +215,16 @@ __device__ __forceinline__ float chunk_dot(const uint4 wq, const uint32_t* xr, u
   } else {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const uint32_t u = q[t] ^ 0x80808080u;  // signed int8 -> q + 128
       if constexpr (S::F32) {
         const float* x = reinterpret_cast<const float*>(xr) + 4 * t;
-        acc = fmaf(ub0(u), x[0], acc);
-        acc = fmaf(ub1(u), x[1], acc);
-        acc = fmaf(ub2(u), x[2], acc);
-        acc = fmaf(ub3(u), x[3], acc);
+        acc = fmaf(sb0(q[t]), x[0], acc);
+        acc = fmaf(sb1(q[t]), x[1], acc);
+        acc = fmaf(sb2(q[t]), x[2], acc);
+        acc = fmaf(sb3(q[t]), x[3], acc);
       } else {
         using H = Half16<AT>;
-        acc = H::dot2(H::template byte_pair<0>(u), xr[2 * t + 0], acc);
-        acc = H::dot2(H::template byte_pair<2>(u), xr[2 * t + 1], acc);
+        acc = H::dot2(H::template byte_pair<0>(q[t]), xr[2 * t + 0], acc);
+        acc = H::dot2(H::template byte_pair<2>(q[t]), xr[2 * t + 1], acc);
       }
     }
   }
@@ -228,7 +232,7 @@ __device__ __forceinline__ float chunk_dot(const uint4 wq, const uint32_t* xr, u
 }
 
 // The 16-bit operand pairs of one weight chunk, as chunk_dot forms them (INT4: 16 dwords
-// of biased nibble pairs in k order (0,4)(1,5)(2,6)(3,7) per 8 k; INT8: 8 dwords of q + 128),
+// of biased nibble pairs in k order (0,4)(1,5)(2,6)(3,7) per 8 k; INT8: 8 dwords of byte pairs),
 // for reuse across several rows of x (16-bit activations only).
 template <int WBITS, typename AT>
 struct WPairs {
@@ -248,9 +252,8 @@ __device__ __forceinline__ void chunk_widen(const uint4 wq, uint32_t nib_mask, u
       w.v[4 * b + 2] = and_or(q[b] >> 8, nib_mask, magic);
       w.v[4 * b + 3] = and_or(q[b] >> 12, nib_mask, magic);
     } else {
-      const uint32_t u = q[b] ^ 0x80808080u;
-      w.v[2 * b + 0] = H::template byte_pair<0>(u);
-      w.v[2 * b + 1] = H::template byte_pair<2>(u);
+      w.v[2 * b + 0] = H::template byte_pair<0>(q[b]);
+      w.v[2 * b + 1] = H::template byte_pair<2>(q[b]);
     }
   }
 }
@@ -267,9 +270,18 @@ __device__ __forceinline__ float pairs_dot(const WPairs<WBITS, AT>& w, const uin
 
 template <int WBITS, typename AT>
 constexpr float code_offset() {
-  if constexpr (WBITS == 8) return std::is_same_v<AT, _Float16> ? 1152.0f : 128.0f;
+  if constexpr (WBITS == 8) return std::is_same_v<AT, _Float16> ? 1152.0f : 0.0f;
   else if constexpr (sizeof(AT) == 4) return 8.0f;
   else return Half16<AT>::OFF4;
+}
+
+// code_offset times a chunk's x sum, what the widened codes add to the dot product; exactly
+// 0 when they add nothing (the sum is then never used, and its dot products are not emitted)
+template <int WBITS, typename AT>
+__device__ __forceinline__ float offset_term(float xsum) {
+  constexpr float OFF = code_offset<WBITS, AT>();
+  if constexpr (OFF == 0.0f) return 0.0f;
+  else return OFF * xsum;
 }
 
 template <typename ST>
@@ -411,7 +423,6 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
   using HT = std::conditional_t<XF32, __bf16, AT>;  // the dot products' 16-bit type
   using S = XSlot<WBITS, HT>;
   constexpr int KC = S::KC, NV = S::NV;
-  constexpr float OFF = code_offset<WBITS, HT>();
   constexpr int S_SLICE = 64 * SI;  // scale dwords per wavefront slice
   constexpr int XB = XI * 4096;     // LDS bytes per row of x
   __shared__ __attribute__((aligned(16))) uint8_t smem[MX * XB + (WBITS == 4 ? 4 * S_SLICE * 4 : 16)];
@@ -542,7 +553,7 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
     float osx[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j)
-      osx[j] = OFF * (x_from_raw<WBITS, HT>(xh[j], xrh[j]) + x_from_raw<WBITS, HT>(xo[j], xrl[j]));
+      osx[j] = offset_term<WBITS, HT>(x_from_raw<WBITS, HT>(xh[j], xrh[j]) + x_from_raw<WBITS, HT>(xo[j], xrl[j]));
     uint32_t nib_mask = 0x000F000Fu, magic = 0;
     if constexpr (WBITS == 4) magic = Half16<HT>::MAGIC4;
     asm volatile("" : "+v"(nib_mask), "+v"(magic));
@@ -584,7 +595,7 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
     uint32_t xr[CPL][NV];
     float osx[CPL];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) osx[j] = OFF * x_from_raw<WBITS, AT>(xraw[j], xr[j]);
+    for (int j = 0; j < CPL; ++j) osx[j] = offset_term<WBITS, AT>(x_from_raw<WBITS, AT>(xraw[j], xr[j]));
     uint32_t nib_mask = 0x000F000Fu, magic = 0;
     if constexpr (WBITS == 4) magic = Half16<AT>::MAGIC4;
     asm volatile("" : "+v"(nib_mask), "+v"(magic));
@@ -629,7 +640,7 @@ __device__ __forceinline__ void gemv1_body(const AT* __restrict__ x, const uint8
 #pragma unroll
     for (int mi = 0; mi < MX; ++mi)
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) osx[mi][j] = OFF * x_from_raw<WBITS, AT>(xraw[mi][j], xr[mi][j]);
+      for (int j = 0; j < CPL; ++j) osx[mi][j] = offset_term<WBITS, AT>(x_from_raw<WBITS, AT>(xraw[mi][j], xr[mi][j]));
     uint32_t nib_mask = 0x000F000Fu, magic = 0;
     if constexpr (WBITS == 4) magic = Half16<AT>::MAGIC4;
     asm volatile("" : "+v"(nib_mask), "+v"(magic));
