@@ -359,6 +359,16 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
             &xls[wave][(u * 16 + r) * XRB + (((NMF * q + j) ^ (r & (CH - 1))) * 16)]);
     };
     if constexpr (XL) read_x(0);
+    // INT4: step u's products (pp_st: weights against x; xs_st: ones against x, the row sums
+    // behind the widening's offset), scaled into acc by scale_step one step later
+    f32x4 xs_st[U], pp_st[U][R];
+    auto scale_step = [&](int u) __attribute__((always_inline)) {
+#pragma unroll
+      for (int t = 0; t < R; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          acc[t][i] = fmaf(sc[u][t][i], fmaf(-Mx<AT>::OFF4, xs_st[u][i], pp_st[u][t][i]), acc[t][i]);
+    };
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if constexpr (XL) {
@@ -385,6 +395,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
         for (int h = 0; h < XPARTS; ++h)
 #pragma unroll
           for (int j = 0; j < NMF; ++j) xs = Mx<AT>::mma(ones, xo[h][j], xs);
+        xs_st[u] = xs;
 #pragma unroll
         for (int t = 0; t < R; ++t) {
           const uint32_t d[4] = {wv[u][t].x, wv[u][t].y, wv[u][t].z, wv[u][t].w};
@@ -395,9 +406,12 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
 #pragma unroll
             for (int h = 0; h < XPARTS; ++h) pp = Mx<AT>::mma(wop, xo[h][j], pp);
           }
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[t][i] = fmaf(sc[u][t][i], fmaf(-Mx<AT>::OFF4, xs[i], pp[i]), acc[t][i]);
+          pp_st[u][t] = pp;
         }
+        // the previous step's group scaling, behind this step's MFMAs: its products have
+        // long landed, where this step's own would hold the wavefront (one per SIMD) until
+        // the MFMA chain drains
+        if (u > 0) scale_step(u - 1);
       } else {
 #pragma unroll
         for (int j = 0; j < NMF; ++j) {
@@ -416,6 +430,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(1, 2
         }
       }
     }
+    if constexpr (WBITS == 4) scale_step(U - 1);
   }
   if constexpr (WBITS == 8) {
 #pragma unroll
