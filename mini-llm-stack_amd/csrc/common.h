@@ -74,6 +74,28 @@ __device__ __forceinline__ float dpp_mov(float v) {
 }
 
 namespace detail {
+// v_permlane32_swap (BIT = 32) / v_permlane16_swap (BIT = 16): the lanes with lane & BIT
+// of a trade places with the lanes without it of b, so that a + b afterwards holds, in the
+// lanes without the bit, a's value plus its xor-BIT partner's, and in the lanes with it,
+// b's: the xor-shuffle step of a and b at once, without the LDS crossbar. The pair's
+// elements are copied out one by one (a __builtin_bit_cast of the second element compiled
+// into a read of the first).
+template <int BIT>
+__device__ __forceinline__ float swap_add(float a, float b) {
+  static_assert(BIT == 16 || BIT == 32, "lane-half or 16-lane-row swap");
+  uint32_t r0, r1;
+  if constexpr (BIT == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    r0 = r[0];
+    r1 = r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    r0 = r[0];
+    r1 = r[1];
+  }
+  return __uint_as_float(r0) + __uint_as_float(r1);
+}
+
 // Halves the live values per step: lanes with lane & BIT keep the upper half,
 // the others the lower half, each adding its xor-partner's copy. With one value
 // left, the lane bits BIT..0 are summed (lowest first, so the mirror patterns
@@ -82,12 +104,16 @@ template <int N, int BIT>
 __device__ __forceinline__ void reduce_split(float* v, int lane) {
   if constexpr (N > 1) {
     constexpr int H = N / 2;
-    const bool upper = (lane & BIT) != 0;
 #pragma unroll
     for (int i = 0; i < H; ++i) {
-      const float send = upper ? v[i] : v[i + H];
-      const float keep = upper ? v[i + H] : v[i];
-      v[i] = keep + __shfl_xor(send, BIT, 64);
+      if constexpr (BIT >= 16) {
+        v[i] = swap_add<BIT>(v[i], v[i + H]);
+      } else {
+        const bool upper = (lane & BIT) != 0;
+        const float send = upper ? v[i] : v[i + H];
+        const float keep = upper ? v[i + H] : v[i];
+        v[i] = keep + __shfl_xor(send, BIT, 64);
+      }
     }
     reduce_split<H, BIT / 2>(v, lane);
   } else {
@@ -95,8 +121,8 @@ __device__ __forceinline__ void reduce_split(float* v, int lane) {
     if constexpr (BIT >= 2) v[0] += dpp_mov<0x4E>(v[0]);   // quad_perm [2,3,0,1]: lane ^ 2
     if constexpr (BIT >= 4) v[0] += dpp_mov<0x141>(v[0]);  // row_half_mirror: the other quad
     if constexpr (BIT >= 8) v[0] += dpp_mov<0x140>(v[0]);  // row_mirror: the other octet
-    if constexpr (BIT >= 16) v[0] += __shfl_xor(v[0], 16, 64);
-    if constexpr (BIT >= 32) v[0] += __shfl_xor(v[0], 32, 64);
+    if constexpr (BIT >= 16) v[0] = swap_add<16>(v[0], v[0]);
+    if constexpr (BIT >= 32) v[0] = swap_add<32>(v[0], v[0]);
   }
 }
 }  // namespace detail
