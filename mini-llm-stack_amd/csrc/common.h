@@ -73,13 +73,13 @@ __device__ __forceinline__ float dpp_mov(float v) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
-namespace detail {
 // v_permlane32_swap (BIT = 32) / v_permlane16_swap (BIT = 16): the lanes with lane & BIT
-// of a trade places with the lanes without it of b, so that a + b afterwards holds, in the
-// lanes without the bit, a's value plus its xor-BIT partner's, and in the lanes with it,
-// b's: the xor-shuffle step of a and b at once, without the LDS crossbar. The pair's
-// elements are copied out one by one (a __builtin_bit_cast of the second element compiled
-// into a read of the first).
+// of a trade places with the lanes without it of b (the upper 32 lanes of a with the lower
+// 32 of b; the odd 16-lane rows of a with the even rows of b), so that a + b afterwards
+// holds, in the lanes without the bit, a's value plus its xor-BIT partner's, and in the
+// lanes with it, b's: the xor-shuffle step of a and b at once, without the LDS crossbar.
+// The pair's elements are copied out one by one (a __builtin_bit_cast of the second
+// element compiled into a read of the first).
 template <int BIT>
 __device__ __forceinline__ float swap_add(float a, float b) {
   static_assert(BIT == 16 || BIT == 32, "lane-half or 16-lane-row swap");
@@ -96,6 +96,7 @@ __device__ __forceinline__ float swap_add(float a, float b) {
   return __uint_as_float(r0) + __uint_as_float(r1);
 }
 
+namespace detail {
 // Halves the live values per step: lanes with lane & BIT keep the upper half,
 // the others the lower half, each adding its xor-partner's copy. With one value
 // left, the lane bits BIT..0 are summed (lowest first, so the mirror patterns

@@ -323,29 +323,12 @@ __device__ __forceinline__ float wave_total_dpp(float v) {
   return v;
 }
 
-// v_permlane32_swap / v_permlane16_swap: the upper 32 lanes of a trade places with the lower
-// 32 of b (16: the odd 16-lane rows of a with the even rows of b). The elements of the
-// returned pair are copied into scalars one by one: a __builtin_bit_cast of the pair's second
-// element compiled into a read of the first.
-__device__ __forceinline__ void swap_halves32(float& a, float& b) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-  const uint32_t r0 = r[0], r1 = r[1];
-  a = __uint_as_float(r0);
-  b = __uint_as_float(r1);
-}
-__device__ __forceinline__ void swap_rows16(float& a, float& b) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
-  const uint32_t r0 = r[0], r1 = r[1];
-  a = __uint_as_float(r0);
-  b = __uint_as_float(r1);
-}
-
 // Wave totals of V per-lane partials (V = 1, 2 or a multiple of 4), reduced together: a swap
-// of lane halves and an add leave each value's two halves summed in one half of a register
-// (two values per register), a swap of 16-lane rows and an add the same per row (four values
-// per register), and 4 DPP steps finish each row: 3 + 3 + 4 instructions for 4 values where
-// a DPP reduction per value takes 4 x 10. Slot k of lane l holds value total_index<V>(l, k),
-// -1 where the lane is not the one that writes it.
+// of lane halves and an add (swap_add<32>) leave each value's two halves summed in one half
+// of a register (two values per register), a swap of 16-lane rows and an add the same per
+// row (four values per register), and 4 DPP steps finish each row: 3 + 3 + 4 instructions
+// for 4 values where a DPP reduction per value takes 4 x 10. Slot k of lane l holds value
+// total_index<V>(l, k), -1 where the lane is not the one that writes it.
 template <int V>
 struct WaveTotals {
   static_assert(V == 1 || V == 2 || V % 4 == 0, "1, 2 or a multiple of 4 values");
@@ -354,26 +337,20 @@ struct WaveTotals {
 };
 
 template <int V>
-__device__ __forceinline__ WaveTotals<V> wave_totals(float (&p)[V]) {
+__device__ __forceinline__ WaveTotals<V> wave_totals(const float (&p)[V]) {
   WaveTotals<V> out;
   if constexpr (V == 1) {
     out.t[0] = wave_total_dpp(p[0]);
   } else if constexpr (V == 2) {
-    swap_halves32(p[0], p[1]);
-    const float a = lane_group_sum<16>(p[0] + p[1]);  // lanes 0-31: value 0, 32-63: value 1
-    out.t[0] = dpp_add_rows<0x142, 0xA>(a);           // row_bcast:15: rows 1, 3 += rows 0, 2
+    const float a = lane_group_sum<16>(swap_add<32>(p[0], p[1]));  // lanes 0-31: value 0, 32-63: 1
+    out.t[0] = dpp_add_rows<0x142, 0xA>(a);                          // row_bcast:15: rows 1, 3 += rows 0, 2
   } else {
     float a[V / 2];
 #pragma unroll
-    for (int i = 0; i < V / 2; ++i) {
-      swap_halves32(p[2 * i], p[2 * i + 1]);
-      a[i] = p[2 * i] + p[2 * i + 1];  // lanes 0-31: value 2i, 32-63: value 2i + 1
-    }
+    for (int i = 0; i < V / 2; ++i) a[i] = swap_add<32>(p[2 * i], p[2 * i + 1]);  // value 2i | 2i + 1
 #pragma unroll
-    for (int j = 0; j < V / 4; ++j) {
-      swap_rows16(a[2 * j], a[2 * j + 1]);
-      out.t[j] = lane_group_sum<16>(a[2 * j] + a[2 * j + 1]);  // rows: values 4j + {0, 2, 1, 3}
-    }
+    for (int j = 0; j < V / 4; ++j)
+      out.t[j] = lane_group_sum<16>(swap_add<16>(a[2 * j], a[2 * j + 1]));  // rows: values 4j + {0, 2, 1, 3}
   }
   return out;
 }
