@@ -18,7 +18,8 @@
 // - off * sum_k x_k)  where v'_k = v_k + bias is produced by OR-ing the nibble into
 // the mantissa of a 16-bit float constant (bf16 128.0 / fp16 1024.0): one
 // v_and_or per two weights and one v_dot2 per two products. fp32 activations use
-// exact byte->float converts and FMAs. INT8 uses u = q ^ 0x80 = q + 128 bytes.
+// exact byte->float converts and FMAs. INT8 converts the signed bytes exactly (bf16 and fp32
+// x, no offset), or, for fp16 x, places u = q ^ 0x80 = q + 128 in an fp16's low byte.
 // Each lane's partial sums are reduced across the wavefront at the end.
 #pragma once
 
