@@ -240,6 +240,30 @@ def test_fp32_skinny_without_workspace(dev, bits):
     _check32(out, want, f"fp32 M={M} int{bits}, odd row stride")
 
 
+@pytest.mark.parametrize("M,K,pad", [
+    (1, 8192, 0),   # 1 weight row per wavefront, 8 chunks per lane: one partial per lane
+    (1, 4096, 0),   # 2 rows: 2 partials
+    (1, 2048, 0),   # 4 rows: 4 partials
+    (1, 1024, 0),   # 8 rows: 8 partials
+    (2, 1008, 1),   # K % 64 != 0 (no matrix-core path), x rows K + 1 apart: 2 x 8 = 16 partials
+    (3, 1008, 0),   # 4 rows of x per block (the last repeats row 2) x 8 = 32 partials
+])
+def test_fp32_register_gemv_reduction_depths(dev, M, K, pad):
+    """INT8 with fp32 x on the register GEMV (M = 1, or K that the matrix-core paths do not
+    take): every number of per-lane partials its butterfly reduces, the lane-half and
+    16-lane-row steps as swaps, against the oracle under the fp32 rule (ragged N)."""
+    N = 1000
+    g = torch.Generator(device="cpu").manual_seed(4000 + K + M)
+    a = torch.randn(M, K + pad, generator=g)
+    w = torch.randn(N, K, generator=g) * 0.02
+    q, s = quantize_int8(w.to(dev))
+    ax = a.to(dev)[:, :K]
+    out = int8_matmul(ax, q, s)
+    assert out.shape == (M, N)
+    _check32(out, ref.int8_matmul(a[:, :K].numpy(), q.cpu().numpy(), s.float().cpu().numpy()),
+             f"register GEMV fp32 INT8 M={M} K={K}")
+
+
 def test_int8_dgrad_fp32_training_shape(dev):
     """The INT8 STE input gradient with fp32 dy at a training shape (4096 x 11008 -> 4096):
     ys = dy * s in fp32 split into hi + lo rows on the matrix cores. Every output within
